@@ -1,0 +1,311 @@
+"""Benchmark of the MI355X sigmoid-tension hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+
+Workload (the 117M-model shape the metric is quoted
+on): windowed tension fwd+bwd, B=8 H=12 T=1024 d=64 W=64, bf16 storage with
+fp32 accumulation, Q/K/V ~ 0.5 N(0,1) with RoPE (base 10000) on Q/K, upstream
+grad ~ N(0,1), tau-mass normalised output (the north star's
+out = sum tau v / sum tau), tau not materialised.  One step = forward +
+backward (dQ, dK, dV) of one batch.
+
+Method: NSETS independent input sets (more than the 256 MB Infinity Cache
+in total) are generated on the GPU and rotated, so every step reads its
+inputs from HBM.  Each step (1 forward + 2 backward kernels, launched through
+the public autograd op) is captured once per input set in a HIP graph; the
+timed region replays K graphs between two events after a synchronize.  The
+dominant kernel is then timed alone the same way (graph of its launches on
+the same stream) for the roofline entry; ``rocprofv3 --kernel-trace --stats``
+of this command gives the per-kernel durations in profiles/.
+
+The CPU baseline times the reference's CPU path (unfold gather + tau-mass +
+autograd, restated in oracle/torch_ref.py) in float32 on the host cores, on
+a bounded sample (one of the 8 sequences, repeated for ~10 s).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+NSETS = 8                      # 8 x 50 MB of inputs > 256 MB Infinity Cache
+METRIC = "tension fwd+bwd tokens/s at 117M shape (T=1024,W=64); % MFMA/HBM roofline"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def pairs_window(B, H, T, W):
+    """Valid (query, key) pairs of the local band."""
+    full = max(0, T - W) * W
+    ramp = sum(min(t, W) for t in range(min(T, W)))
+    return B * H * (full + ramp)
+
+
+def rope_tables(T, D, dev):
+    half = D // 2
+    theta = 1.0 / (10000 ** (torch.arange(0, half).float() / half))
+    freqs = torch.outer(torch.arange(T).float(), theta)
+    return freqs.cos().to(dev), freqs.sin().to(dev)
+
+
+def make_window_sets(n, B, T, H, D, dev, seed):
+    from bozo_amd import rope
+    cos, sin = rope_tables(T, D, dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    sets = []
+    for _ in range(n):
+        q = torch.randn(B, T, H, D, device=dev, generator=g) * 0.5
+        k = torch.randn(B, T, H, D, device=dev, generator=g) * 0.5
+        v = torch.randn(B, T, H, D, device=dev, generator=g) * 0.5
+        do = torch.randn(B, T, H, D, device=dev, generator=g)
+        s = dict(Q=rope(q, cos, sin, out_dtype=torch.bfloat16).detach().requires_grad_(True),
+                 K=rope(k, cos, sin, out_dtype=torch.bfloat16).detach().requires_grad_(True),
+                 V=v.to(torch.bfloat16).requires_grad_(True), dO=do.to(torch.bfloat16))
+        sets.append(s)
+    torch.cuda.synchronize()
+    return sets
+
+
+def capture(fn, warm=2):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warm):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graphs(graphs, steps, warmup):
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per replay
+
+
+def window_step_fn(s, W, scale, normalize, return_tau=False):
+    from bozo_amd import causal_tension
+
+    def fn():
+        if return_tau:
+            out, tau = causal_tension(s["Q"], s["K"], s["V"], W, scale, return_tau=True,
+                                      normalize=normalize)
+            return torch.autograd.grad((out, tau), (s["Q"], s["K"], s["V"]), (s["dO"], s["dTau"]))
+        out = causal_tension(s["Q"], s["K"], s["V"], W, scale, normalize=normalize)
+        return torch.autograd.grad(out, (s["Q"], s["K"], s["V"]), s["dO"])
+    return fn
+
+
+def kernel_fns(s, W, scale, flags):
+    """One launch of each of the three kernels on set s, through the C ABI
+    entry points that launch exactly one kernel each."""
+    from bozo_amd import _lib as L
+    B, T, H, D = s["Q"].shape
+    Q, K, V, dO = (s[n].detach() for n in ("Q", "K", "V", "dO"))
+    out = torch.empty_like(Q)
+    mass = torch.empty(B, T, H, device=Q.device)
+    dq, dk, dv = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+    ws = torch.empty(max(1, L.lib().tension_window_bwd_workspace(B, T, H, L.F32, flags)),
+                     dtype=torch.uint8, device=Q.device)
+    lib = L.lib()
+    bq, bk, bv, bo, bm, bdo = (L.buf(t) for t in (Q, K, V, out, mass, dO))
+    bdq, bdk, bdv = L.buf(dq), L.buf(dk), L.buf(dv)
+    keep = (out, mass, dq, dk, dv, ws)
+
+    def fwd():
+        L.check(lib.tension_window_fwd(bq, bk, bv, bo, None, None, bm, B, T, H, D, W, scale, flags,
+                                       L.stream_handle()), "fwd")
+
+    def dqf():
+        L.check(lib.tension_window_bwd_dq(bq, bk, bv, bdo, None, None, bo, bm, bdq, ws.data_ptr(),
+                                          B, T, H, D, W, scale, flags, L.stream_handle()), "dq")
+
+    def dkvf():
+        L.check(lib.tension_window_bwd_dkv(bq, bk, bv, bdo, None, None, bdk, bdv, ws.data_ptr(),
+                                           B, T, H, D, W, scale, flags, L.stream_handle()), "dkv")
+    return {"fwd": fwd, "dq": dqf, "dkv": dkvf}, keep
+
+
+def kernel_bytes(B, T, H, D, W, el=2):
+    """Algorithmic (compulsory) HBM bytes per launch of each kernel of the
+    tau-mass-normalised step: every tensor the kernel must touch, once."""
+    act = B * T * H * D * el           # one [B,T,H,D] bf16 tensor
+    vec = B * T * H * 4                # one [B,T,H] fp32 tensor
+    return {
+        "fwd": 3 * act + act + vec,              # Q,K,V -> out, mass
+        "dq": 5 * act + vec + act + 2 * vec,     # Q,K,V,dO,out,mass -> dQ, ws(a,c)
+        "dkv": 4 * act + 2 * vec + 2 * act,      # Q,K,V,dO,ws -> dK,dV
+    }
+
+
+def cpu_baseline(B, T, H, D, W, seconds=10.0):
+    """Reference CPU path (unfold + tau-mass + autograd, fp32) on the host."""
+    from oracle import torch_ref as R
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(1)
+    b = 1  # bounded sample: one sequence of the batch
+    q, k, v = (torch.randn(b, T, H, D, generator=g) * 0.5 for _ in range(3))
+    do = torch.randn(b, T, H, D, generator=g)
+
+    def once():
+        qq, kk, vv = (x.clone().requires_grad_(True) for x in (q, k, v))
+        msg, tau = R.unfold_tension(qq, kk, vv, W, math.sqrt(D), return_tau=True)
+        out = R.normalize_mass(msg, tau)
+        torch.autograd.grad(out, (qq, kk, vv), do)
+
+    once()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        once()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(b * T * n / el, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n} fwd+bwd passes of 1 sequence (T={T}, H={H}, d={D}, W={W}) fp32, "
+                      f"unfold+tau-mass+autograd (oracle/torch_ref.py), {el:.1f} s on {cpu}"}
+
+
+def bench_window(args, dev):
+    B, H, T, D, W = 8, 12, 1024, 64, 64
+    scale = math.sqrt(D)
+    tokens = B * T
+    P = pairs_window(B, H, T, W)
+    flops = (4 + 8) * D * P
+    sets = make_window_sets(NSETS, B, T, H, D, dev, seed=1)
+
+    log(f"[bench] capturing {NSETS} step graphs (B{B} H{H} T{T} d{D} W{W} bf16, tau-mass)")
+    graphs = [capture(window_step_fn(s, W, scale, "mass")) for s in sets]
+    ms = time_graphs(graphs, args.steps, args.warmup)
+    log(f"[bench] fwd+bwd {ms * 1e3:.1f} us/step")
+
+    # per-kernel durations (same stream, graph of one launch per set)
+    from bozo_amd import _lib as L
+    kfns, keep = [], []
+    for s in sets:
+        f, kp = kernel_fns(s, W, scale, L.NORM_MASS)
+        kfns.append(f)
+        keep.append(kp)
+    kbytes = kernel_bytes(B, T, H, D, W)
+    per_kernel = {}
+    for name in ("fwd", "dq", "dkv"):
+        if name == "dkv":  # its workspace must hold what dq wrote
+            for f in kfns:
+                f["dq"]()
+        gs = [capture(f[name], warm=1) for f in kfns]
+        kms = time_graphs(gs, max(NSETS * 10, args.steps), NSETS)
+        per_kernel[name] = {"us": round(kms * 1e3, 2),
+                            "alg_bytes": kbytes[name],
+                            "GBps": round(kbytes[name] / (kms * 1e-3) / 1e9, 1)}
+        log(f"[bench] kernel {name}: {kms * 1e3:.2f} us, {per_kernel[name]['GBps']} GB/s algorithmic")
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
+    d = per_kernel[dom]
+
+    step_bytes = sum(kbytes.values()) - 2 * B * T * H * 4  # ws a/c are produced and consumed internally
+    result = {
+        "metric": METRIC,
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "windowed sigmoid-tension fwd+bwd, tau-mass normalised (config 2)",
+                   "B": B, "H": H, "T": T, "head_dim": D, "window": W, "global_batch": B,
+                   "seq_len": T, "parallelism": "none (1 GPU)", "input_sets_rotated": NSETS},
+        "roofline": {"bound": "hbm", "kernel": f"mfma_bwd_{dom}" if dom != "fwd" else "mfma_fwd",
+                     "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(d["GBps"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "step": {"alg_bytes": step_bytes,
+                 "hbm_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                 "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "alg_flops": flops,
+                 "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+                 "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                 "kernels": per_kernel},
+    }
+    tfile = os.path.join(ROOT, "profiles", "traffic_window_c2.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            tr = json.load(f)
+        if tr.get("kernel") == result["roofline"]["kernel"]:
+            result["roofline"]["traffic"] = tr.get("bytes_per_launch")
+
+    # secondary variants: raw contract, and tau materialised + dTau (export path)
+    del graphs
+    raw_graphs = [capture(window_step_fn(s, W, scale, None)) for s in sets]
+    result["variants"] = {"raw_out_ms": round(time_graphs(raw_graphs, args.steps, args.warmup), 5)}
+    del raw_graphs
+    g = torch.Generator(device=dev).manual_seed(7)
+    for s in sets:
+        s["dTau"] = (torch.randn(B, T, H, W, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    tau_graphs = [capture(window_step_fn(s, W, scale, "mass", return_tau=True)) for s in sets]
+    result["variants"]["tau_materialised_ms"] = round(time_graphs(tau_graphs, args.steps, args.warmup), 5)
+    del tau_graphs
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every box has one GPU); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    result = bench_window(args, dev)
+    if not args.no_cpu:
+        log("[bench] CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(1, 1024, 12, 64, 64, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,267 @@
+// Exact (non-MFMA) band kernels (templates; instantiated by exact_*.hip): any input dtype (f32 / bf16 / f16 / f64),
+// accumulation in A = float or double.  One thread owns one query row
+// (forward, dQ) or one key row (dK/dV) and walks its band sequentially, so
+// the result follows the reference's per-pair arithmetic in full precision:
+// the dot is divided by scale (kernel.py:100), sigmoid is libm-accurate and
+// every product is accumulated in A.  These kernels serve fp32 / fp64 /
+// mixed-dtype calls (gradcheck runs through them in float64) and every shape
+// the MFMA kernels do not take.
+#pragma once
+
+#include "kernels.h"
+
+namespace tension {
+
+template <typename A, int D>
+__global__ __launch_bounds__(128) void exact_fwd(BandParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.H * p.T;
+  if (idx >= total) return;
+  const int t = (int)(idx % p.T);
+  const int64_t bh = idx / p.T;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+
+  const int64_t qo = b * p.q.s0 + (int64_t)t * p.q.s1 + h * p.q.s2;
+  A q[D], acc[D];
+#pragma unroll
+  for (int d = 0; d < D; d += 8) ld8<A>(p.q, qo + d, q + d);
+#pragma unroll
+  for (int d = 0; d < D; ++d) acc[d] = A(0);
+  A mass = A(0);
+  const A scale = (A)p.scale;
+
+  const int s_lo = t - p.win > 0 ? t - p.win : 0;
+  const int s_hi = t - 1 + p.diag;
+  for (int s = s_lo; s <= s_hi; ++s) {
+    const int64_t ko = b * p.k.s0 + (int64_t)s * p.k.s1 + h * p.k.s2;
+    const int64_t vo = b * p.v.s0 + (int64_t)s * p.v.s1 + h * p.v.s2;
+    A dot = A(0);
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A r[8];
+      ld8<A>(p.k, ko + d, r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dot += q[d + i] * r[i];
+    }
+    A x = dot / scale;
+    if (p.bias.p) x += ld<A>(p.bias, bias_off(p, b, t, s));
+    const A tau = sigmoid_exact(x);
+    mass += tau;
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A r[8];
+      ld8<A>(p.v, vo + d, r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[d + i] += tau * r[i];
+    }
+    if (p.tau.p) {
+      const int c = tau_col(p, t, s);
+      if (c >= 0) st<A>(p.tau, tau_off(p.tau, b, t, h, c), tau);
+    }
+  }
+  if (p.tau.p) {
+    const int e = tau_empty_bound(p, t);
+    for (int c = 0; c < e; ++c) st<A>(p.tau, tau_off(p.tau, b, t, h, c), A(0));
+  }
+  A inv = A(1);
+  if (p.flags & TENSION_NORM_MASS) inv = A(1) / (mass > A(kMassEps) ? mass : A(kMassEps));
+  if (p.flags & TENSION_NORM_COUNT) {
+    const int cnt = t < p.W ? t : p.W;
+    inv = A(1) / A(cnt > 1 ? cnt : 1);
+  }
+  const int64_t oo = b * p.out.s0 + (int64_t)t * p.out.s1 + h * p.out.s2;
+#pragma unroll
+  for (int d = 0; d < D; ++d) acc[d] *= inv;
+#pragma unroll
+  for (int d = 0; d < D; d += 8) st8<A>(p.out, oo + d, acc + d);
+  if (p.mass.p) st<A>(p.mass, b * p.mass.s0 + (int64_t)t * p.mass.s1 + h * p.mass.s2, mass);
+}
+
+// Per-query coefficients of the backward:  dtau = a_t * (dO_t . v_s) - c_t
+// (+ dTau).  raw: a = 1, c = 0; count: a = 1/max(min(t,W),1), c = 0;
+// tau-mass (out = msg/m): a = 1/m, c = (dO_t . out_t)/m while mass >= eps
+// (the clamp passes no gradient below eps).
+template <typename A>
+__device__ __forceinline__ void query_coeffs(const BandParams& p, int b, int t, int h,
+                                             A dot_dout_out, A* a, A* c) {
+  *a = A(1);
+  *c = A(0);
+  if (p.flags & TENSION_NORM_MASS) {
+    const A mass = ld<A>(p.mass, b * p.mass.s0 + (int64_t)t * p.mass.s1 + h * p.mass.s2);
+    const A m = mass > A(kMassEps) ? mass : A(kMassEps);
+    *a = A(1) / m;
+    *c = mass >= A(kMassEps) ? dot_dout_out / m : A(0);
+  } else if (p.flags & TENSION_NORM_COUNT) {
+    const int cnt = t < p.W ? t : p.W;
+    *a = A(1) / A(cnt > 1 ? cnt : 1);
+  }
+}
+
+template <typename A, int D>
+__global__ __launch_bounds__(128) void exact_bwd_dq(BandParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.H * p.T;
+  if (idx >= total) return;
+  const int t = (int)(idx % p.T);
+  const int64_t bh = idx / p.T;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+
+  const int64_t qo = b * p.q.s0 + (int64_t)t * p.q.s1 + h * p.q.s2;
+  const int64_t go = b * p.dout.s0 + (int64_t)t * p.dout.s1 + h * p.dout.s2;
+  A q[D], g[D], dq[D];
+  A dgo = A(0);
+  const int64_t oo = b * p.out.s0 + (int64_t)t * p.out.s1 + h * p.out.s2;
+#pragma unroll
+  for (int d = 0; d < D; d += 8) {
+    ld8<A>(p.q, qo + d, q + d);
+    ld8<A>(p.dout, go + d, g + d);
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) dq[d] = A(0);
+  if (p.flags & TENSION_NORM_MASS) {
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A r[8];
+      ld8<A>(p.out, oo + d, r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dgo += g[d + i] * r[i];
+    }
+  }
+  A ca, cc;
+  query_coeffs<A>(p, b, t, h, dgo, &ca, &cc);
+  if (p.ws && (p.flags & TENSION_NORM_MASS)) {
+    const int64_t n = (int64_t)p.B * p.T * p.H;
+    const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
+    ((A*)p.ws)[wi] = ca;
+    ((A*)p.ws)[n + wi] = cc;
+  }
+  const A scale = (A)p.scale;
+  const int s_lo = t - p.win > 0 ? t - p.win : 0;
+  const int s_hi = t - 1 + p.diag;
+  for (int s = s_lo; s <= s_hi; ++s) {
+    const int64_t ko = b * p.k.s0 + (int64_t)s * p.k.s1 + h * p.k.s2;
+    const int64_t vo = b * p.v.s0 + (int64_t)s * p.v.s1 + h * p.v.s2;
+    A dot = A(0), gv = A(0);
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A rk[8], rv[8];
+      ld8<A>(p.k, ko + d, rk);
+      ld8<A>(p.v, vo + d, rv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dot += q[d + i] * rk[i];
+        gv += g[d + i] * rv[i];
+      }
+    }
+    A x = dot / scale;
+    if (p.bias.p) x += ld<A>(p.bias, bias_off(p, b, t, s));
+    const A tau = sigmoid_exact(x);
+    A dtau = gv * ca - cc;
+    if (p.dtau.p) {
+      const int c = tau_col(p, t, s);
+      if (c >= 0) dtau += ld<A>(p.dtau, tau_off(p.dtau, b, t, h, c));
+    }
+    const A dd = dtau * tau * (A(1) - tau);
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A rk[8];
+      ld8<A>(p.k, ko + d, rk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dq[d + i] += dd * rk[i];
+    }
+  }
+  const int64_t dqo = b * p.dq.s0 + (int64_t)t * p.dq.s1 + h * p.dq.s2;
+#pragma unroll
+  for (int d = 0; d < D; ++d) dq[d] /= scale;
+#pragma unroll
+  for (int d = 0; d < D; d += 8) st8<A>(p.dq, dqo + d, dq + d);
+}
+
+template <typename A, int D>
+__global__ __launch_bounds__(128) void exact_bwd_dkv(BandParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.H * p.T;
+  if (idx >= total) return;
+  const int s = (int)(idx % p.T);
+  const int64_t bh = idx / p.T;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+
+  const int64_t ko = b * p.k.s0 + (int64_t)s * p.k.s1 + h * p.k.s2;
+  const int64_t vo = b * p.v.s0 + (int64_t)s * p.v.s1 + h * p.v.s2;
+  A k[D], v[D], dk[D], dv[D];
+#pragma unroll
+  for (int d = 0; d < D; d += 8) {
+    ld8<A>(p.k, ko + d, k + d);
+    ld8<A>(p.v, vo + d, v + d);
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    dk[d] = A(0);
+    dv[d] = A(0);
+  }
+  const A scale = (A)p.scale;
+  const int64_t n = (int64_t)p.B * p.T * p.H;
+  // queries that see key s: s + 1 - diag <= t <= s + win
+  const int t_lo = s + 1 - p.diag;
+  const int t_hi = (int64_t)s + p.win < p.T - 1 ? s + p.win : p.T - 1;
+  for (int t = t_lo; t <= t_hi; ++t) {
+    const int64_t qo = b * p.q.s0 + (int64_t)t * p.q.s1 + h * p.q.s2;
+    const int64_t go = b * p.dout.s0 + (int64_t)t * p.dout.s1 + h * p.dout.s2;
+    A dot = A(0), gv = A(0);
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A rq[8], rg[8];
+      ld8<A>(p.q, qo + d, rq);
+      ld8<A>(p.dout, go + d, rg);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dot += rq[i] * k[d + i];
+        gv += rg[i] * v[d + i];
+      }
+    }
+    A ca = A(1), cc = A(0);
+    if (p.flags & TENSION_NORM_MASS) {
+      const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
+      ca = ((const A*)p.ws)[wi];
+      cc = ((const A*)p.ws)[n + wi];
+    } else if (p.flags & TENSION_NORM_COUNT) {
+      const int cnt = t < p.W ? t : p.W;
+      ca = A(1) / A(cnt > 1 ? cnt : 1);
+    }
+    A x = dot / scale;
+    if (p.bias.p) x += ld<A>(p.bias, bias_off(p, b, t, s));
+    const A tau = sigmoid_exact(x);
+    A dtau = gv * ca - cc;
+    if (p.dtau.p) {
+      const int c = tau_col(p, t, s);
+      if (c >= 0) dtau += ld<A>(p.dtau, tau_off(p.dtau, b, t, h, c));
+    }
+    const A dd = dtau * tau * (A(1) - tau);
+    const A tv = tau * ca;
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      A rq[8], rg[8];
+      ld8<A>(p.q, qo + d, rq);
+      ld8<A>(p.dout, go + d, rg);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dk[d + i] += dd * rq[i];
+        dv[d + i] += tv * rg[i];
+      }
+    }
+  }
+  const int64_t dko = b * p.dk.s0 + (int64_t)s * p.dk.s1 + h * p.dk.s2;
+  const int64_t dvo = b * p.dv.s0 + (int64_t)s * p.dv.s1 + h * p.dv.s2;
+#pragma unroll
+  for (int d = 0; d < D; ++d) dk[d] /= scale;
+#pragma unroll
+  for (int d = 0; d < D; d += 8) {
+    st8<A>(p.dk, dko + d, dk + d);
+    st8<A>(p.dv, dvo + d, dv + d);
+  }
+}
+
+}  // namespace tension

@@ -1,0 +1,34 @@
+// Launcher declarations and parameter blocks shared by the C API and the
+// kernel translation units.
+#pragma once
+
+#include "band.h"
+
+namespace tension {
+
+struct DecodeParams {
+  Buf q, kn, vn, kc, vc, out, tau;
+  const int32_t* pos_in;
+  int32_t* pos_out;
+  int N, H, D, W;
+  double scale;
+  int flags;
+};
+
+struct RopeParams {
+  Buf x, y;
+  const float* cos;
+  const float* sin;
+  int B, T, H, D;
+  int64_t pos_offset;
+  int inverse;
+};
+
+// phase: 0 forward, 1 dQ, 2 dK/dV.  Return 0 when launched (HIP status in
+// *err), -1 when no kernel exists for the request.
+int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
+int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
+int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err);
+int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
+
+}  // namespace tension

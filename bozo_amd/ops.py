@@ -1,0 +1,317 @@
+"""Host side of the MI355X sigmoid-tension op: autograd Functions over the
+C ABI of libtension_hip.so.
+
+Drop-in for ``triton_tension.ops`` of the reference:
+
+    from bozo_amd import causal_tension
+    out          = causal_tension(Q, K, V, window=64, scale=8.0)
+    out, tau     = causal_tension(Q, K, V, window=64, scale=8.0, return_tau=True)
+
+Same name, arguments, defaults, return types and dtypes as
+``triton_tension/ops.py:192-224``; ``_CausalTensionFn`` keeps the reference
+Function's arity and gradient semantics (``ops.py:73-187``).  Differences,
+all additive or stricter:
+
+* ``normalize=`` (keyword only, default ``None`` = the reference's raw
+  ``sum tau*v``): ``"mass"`` fuses the tau-mass normalisation of
+  ``model.py:257-258,281-282`` into the kernel (forward and backward),
+  ``"count"`` the valid-count one of ``model.py:264``.
+* There is no CPU fallback.  The reference routes CPU and float64 inputs to a
+  PyTorch unfold path (``ops.py:217-219``); here CPU tensors raise, and
+  float64 runs on the GPU through the exact kernels, so ``gradcheck`` in
+  float64 exercises the HIP backward itself.
+* Inputs may be strided (unit innermost stride) and of mixed float dtypes;
+  each is read in its own dtype (no upcast copies).  Outputs are returned in
+  ``Q.dtype`` (``ops.py:122-124``); gradients in each input's dtype
+  (``ops.py:186-187``).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib as L
+
+_NORMS = {None: 0, "raw": 0, "mass": L.NORM_MASS, "count": L.NORM_COUNT}
+
+
+def _on_gpu(*ts: Optional[Tensor]) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "bozo_amd tension ops run on the ROCm GPU only (got a CPU tensor); "
+                "the CPU reference lives in oracle/ and is test infrastructure")
+
+
+def _rows(t: Optional[Tensor]) -> Optional[Tensor]:
+    """Unit innermost stride is all the kernels need."""
+    if t is None:
+        return None
+    if t.dim() == 0 or t.stride(-1) != 1 or t.numel() == 0:
+        return t.contiguous()
+    return t
+
+
+def _acc_code(*ts: Tensor) -> int:
+    return L.F64 if any(t.dtype == torch.float64 for t in ts) else L.F32
+
+
+def _mass_dtype(*ts: Tensor) -> torch.dtype:
+    return torch.float64 if any(t.dtype == torch.float64 for t in ts) else torch.float32
+
+
+def _side(t: Optional[Tensor], like: Tensor) -> Optional[Tensor]:
+    """Side inputs (bias) are kept in float32, as the reference does
+    (ops.py:93), or float64 for float64 calls."""
+    if t is None:
+        return None
+    return _rows(t.to(torch.float64 if like.dtype == torch.float64 else torch.float32))
+
+
+def _stream(t: Tensor):
+    return L.stream_handle(t.device)
+
+
+def _ws(nbytes: int, dev) -> Optional[Tensor]:
+    return torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
+
+
+def _ptr(t: Optional[Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+# ----------------------------------------------------------------- local window
+
+def _window_fwd(Q, K, V, W, scale, tau, bias, flags, mass):
+    B, T, H, D = Q.shape
+    out = torch.empty(B, T, H, D, dtype=Q.dtype, device=Q.device)
+    with torch.cuda.device(Q.device):
+        L.check(L.lib().tension_window_fwd(
+            L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tau), L.buf(bias), L.buf(mass),
+            B, T, H, D, W, float(scale), flags, _stream(Q)), "tension_window_fwd")
+    return out
+
+
+class _CausalTensionFn(torch.autograd.Function):
+    """Counterpart of the reference's ``_CausalTensionFn`` (ops.py:73-187)."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, W: int, scale: float, return_tau: bool, bias, normalize=None):
+        B, T, H, D = Q.shape
+        flags = _NORMS[normalize]
+        Bias = _side(bias, Q)
+        if Bias is not None and tuple(Bias.shape) != (B, T, W):
+            raise ValueError(f"bias must be [B, T, W]=[{B}, {T}, {W}], got {tuple(Bias.shape)}")
+        tau = torch.empty(B, T, H, W, dtype=Q.dtype, device=Q.device) if return_tau else None
+        mass = (torch.empty(B, T, H, dtype=_mass_dtype(Q, K, V), device=Q.device)
+                if flags & L.NORM_MASS else None)
+        out = _window_fwd(Q, K, V, W, scale, tau, Bias, flags, mass)
+        ctx.save_for_backward(Q, K, V, Bias, out if mass is not None else None, mass)
+        ctx.W, ctx.scale, ctx.flags = W, scale, flags
+        ctx.return_tau = return_tau
+        if return_tau:
+            return out, tau
+        return out
+
+    @staticmethod
+    def backward(ctx, *grads):
+        Q, K, V, Bias, out, mass = ctx.saved_tensors
+        B, T, H, D = Q.shape
+        dOut = _rows(grads[0])
+        dTau = _rows(grads[1]) if ctx.return_tau else None
+        if dOut is None:
+            dOut = torch.zeros_like(Q)
+        dQ = torch.empty_like(Q)
+        dK = torch.empty_like(K)
+        dV = torch.empty_like(V)
+        lib = L.lib()
+        ws = _ws(lib.tension_window_bwd_workspace(B, T, H, _acc_code(Q, K, V), ctx.flags), Q.device)
+        with torch.cuda.device(Q.device):
+            L.check(lib.tension_window_bwd(
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias), L.buf(out),
+                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.W,
+                float(ctx.scale), ctx.flags, _stream(Q)), "tension_window_bwd")
+        return dQ, dK, dV, None, None, None, None, None
+
+
+@torch._dynamo.disable
+def causal_tension(Q: Tensor, K: Tensor, V: Tensor, window: int, scale: float,
+                   return_tau: bool = False, bias: Optional[Tensor] = None, *,
+                   normalize: Optional[str] = None):
+    """Fused causal sigmoid tension on the MI355X.
+
+    Args:
+        Q, K, V    : [B, T, H, HD] on the GPU (float32 / bfloat16 / float16 /
+                     float64; bf16 with HD=64 takes the MFMA kernels).
+        window     : causal look-back W (keys t-W .. t-1).
+        scale      : dot-product divisor (typically sqrt(HD)).
+        return_tau : also emit tau [B, T, H, W] (w=0 oldest).
+        bias       : optional [B, T, W] pre-sigmoid bias, broadcast over H.
+        normalize  : None (raw sum tau*v, the reference contract), "mass"
+                     or "count" (fused normalisations).
+    Returns:
+        out [B, T, H, HD] in Q.dtype, and tau [B, T, H, W] when return_tau.
+    """
+    _on_gpu(Q, K, V, bias)
+    if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
+        raise ValueError(f"Q, K, V must share one [B, T, H, HD] shape, got "
+                         f"{tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
+    if normalize not in _NORMS:
+        raise ValueError(f"normalize must be one of {list(_NORMS)}")
+    if int(window) < 1:
+        raise ValueError("window must be >= 1")
+    return _CausalTensionFn.apply(_rows(Q), _rows(K), _rows(V), int(window), float(scale),
+                                  bool(return_tau), bias, normalize)
+
+
+# ----------------------------------------------------------------- global block
+
+class _GlobalTensionFn(torch.autograd.Function):
+    """Full-causal (diagonal included), tau-mass-normalised block; replaces
+    the einsum path of model.py:217-238."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, scale: float, bias, W_local):
+        B, T, H, D = Q.shape
+        Bias = _side(bias, Q)
+        if Bias is not None and tuple(Bias.shape) != (B, T, T):
+            raise ValueError(f"global bias must be [B, T, T]=[{B}, {T}, {T}], got {tuple(Bias.shape)}")
+        Wl = 0 if W_local is None else min(int(W_local), T)
+        tl = torch.empty(B, T, H, Wl, dtype=Q.dtype, device=Q.device) if Wl > 0 else None
+        mass = torch.empty(B, T, H, dtype=_mass_dtype(Q, K, V), device=Q.device)
+        out = torch.empty_like(Q)
+        with torch.cuda.device(Q.device):
+            L.check(L.lib().tension_global_fwd(
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), L.buf(mass),
+                B, T, H, D, Wl, float(scale), 0, _stream(Q)), "tension_global_fwd")
+        ctx.save_for_backward(Q, K, V, Bias, out, mass)
+        ctx.scale, ctx.Wl = scale, Wl
+        if tl is not None:
+            return out, tl
+        return out
+
+    @staticmethod
+    def backward(ctx, *grads):
+        Q, K, V, Bias, out, mass = ctx.saved_tensors
+        B, T, H, D = Q.shape
+        dOut = _rows(grads[0])
+        if dOut is None:
+            dOut = torch.zeros_like(Q)
+        dTl = _rows(grads[1]) if ctx.Wl > 0 else None
+        dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+        lib = L.lib()
+        ws = _ws(lib.tension_global_bwd_workspace(B, T, H, _acc_code(Q, K, V), 0), Q.device)
+        with torch.cuda.device(Q.device):
+            L.check(lib.tension_global_bwd(
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias), L.buf(out),
+                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.Wl,
+                float(ctx.scale), 0, _stream(Q)), "tension_global_bwd")
+        return dQ, dK, dV, None, None, None
+
+
+@torch._dynamo.disable
+def global_tension(Q: Tensor, K: Tensor, V: Tensor, scale: float,
+                   bias: Optional[Tensor] = None, W_local: Optional[int] = None):
+    """Global layer of the reference (model.py:217-238) as one fused op.
+
+    out = sum_{s<=t} tau*v / max(sum_{s<=t} tau, 1e-6),
+    tau = sigmoid(q.k/scale + bias[b,t,s]).  With ``W_local`` also returns
+    the reference's down-sampled ``tau_local`` [B,T,H,min(W_local,T)] whose
+    slot j is key T-1-j (model.py:231-237)."""
+    _on_gpu(Q, K, V, bias)
+    if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
+        raise ValueError("Q, K, V must share one [B, T, H, HD] shape")
+    return _GlobalTensionFn.apply(_rows(Q), _rows(K), _rows(V), float(scale), bias, W_local)
+
+
+# ----------------------------------------------------------------- decode
+
+def decode_step(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cache: Tensor,
+                pos_in: Tensor, pos_out: Optional[Tensor], scale: float,
+                normalize: bool = True, tau: Optional[Tensor] = None) -> Tensor:
+    """One streaming step (no autograd): attends q [N,H,D] to the cached
+    window, then appends k_new/v_new at slot pos % W of the ring caches
+    [N,H,W,D] (in place).  pos_in: int32 [N] on the GPU; pos_out receives
+    pos_in + 1 when given.  Returns out [N,H,D] in q.dtype."""
+    _on_gpu(q, k_new, v_new, k_cache, v_cache, pos_in)
+    N, H, D = q.shape
+    W = k_cache.shape[2]
+    if pos_in.dtype != torch.int32 or (pos_out is not None and pos_out.dtype != torch.int32):
+        raise TypeError("pos tensors must be int32")
+    out = torch.empty_like(q)
+    with torch.cuda.device(q.device):
+        L.check(L.lib().tension_decode_step(
+            L.buf(_rows(q)), L.buf(_rows(k_new)), L.buf(_rows(v_new)), L.buf(k_cache), L.buf(v_cache),
+            L.buf(out), L.buf(tau), pos_in.data_ptr(), _ptr(pos_out), N, H, D, W, float(scale),
+            L.NORM_MASS if normalize else 0, _stream(q)), "tension_decode_step")
+    return out
+
+
+class TensionDecodeCache:
+    """Ring K/V cache of the last W tokens per (sequence, head) for streaming
+    generation, with the position counters kept on the device (two buffers
+    swapped each step, so a captured HIP graph can replay steps)."""
+
+    def __init__(self, N: int, H: int, D: int, W: int, dtype=torch.bfloat16,
+                 device="cuda", scale: Optional[float] = None):
+        self.k = torch.zeros(N, H, W, D, dtype=dtype, device=device)
+        self.v = torch.zeros(N, H, W, D, dtype=dtype, device=device)
+        self.pos = [torch.zeros(N, dtype=torch.int32, device=device),
+                    torch.zeros(N, dtype=torch.int32, device=device)]
+        self.cur = 0
+        self.W = W
+        self.scale = float(scale) if scale is not None else math.sqrt(D)
+
+    def step(self, q: Tensor, k_new: Tensor, v_new: Tensor, normalize: bool = True,
+             return_tau: bool = False):
+        tau = (torch.empty(q.shape[0], q.shape[1], self.W, dtype=q.dtype, device=q.device)
+               if return_tau else None)
+        pin, pout = self.pos[self.cur], self.pos[1 - self.cur]
+        out = decode_step(q, k_new, v_new, self.k, self.v, pin, pout, self.scale, normalize, tau)
+        self.cur = 1 - self.cur
+        return (out, tau) if return_tau else out
+
+
+# ----------------------------------------------------------------- RoPE
+
+def _rope_call(x: Tensor, y: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, inverse: int):
+    B, T, H, D = x.shape
+    with torch.cuda.device(x.device):
+        L.check(L.lib().tension_rope(L.buf(x), L.buf(y), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                                     B, T, H, D, pos_offset, inverse, _stream(x)), "tension_rope")
+
+
+class _RopeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, cos, sin, pos_offset, out_dtype):
+        y = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+        _rope_call(x, y, cos, sin, pos_offset, 0)
+        ctx.save_for_backward(cos, sin)
+        ctx.pos_offset, ctx.in_dtype = pos_offset, x.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        cos, sin = ctx.saved_tensors
+        dy = _rows(dy)
+        dx = torch.empty(dy.shape, dtype=ctx.in_dtype, device=dy.device)
+        _rope_call(dy, dx, cos, sin, ctx.pos_offset, 1)
+        return dx, None, None, None, None
+
+
+def rope(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int = 0,
+         out_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """Half-split rotary embedding of x [B,T,H,D] with the model's float32
+    cos/sin tables [S, D/2] (model.py:54-81).  ``out_dtype`` defaults to
+    x.dtype (the reference promotes to float32 under autocast; pass
+    torch.float32 to reproduce that)."""
+    _on_gpu(x, cos, sin)
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise TypeError("cos/sin tables must be float32")
+    T, half = x.shape[1], x.shape[-1] // 2
+    if cos.shape[-1] != half or cos.shape[0] < pos_offset + T or sin.shape != cos.shape:
+        raise ValueError("cos/sin tables do not cover the requested positions")
+    return _RopeFn.apply(_rows(x), cos.contiguous(), sin.contiguous(), int(pos_offset), out_dtype)

@@ -1,0 +1,205 @@
+/*
+ * tension_hip.h -- C ABI of the MI355X (gfx950) sigmoid-tension library
+ * (libtension_hip.so).
+ *
+ * The reference has no native FFI for this path: its boundary is the Python
+ * autograd op `causal_tension(Q, K, V, window, scale, return_tau=False,
+ * bias=None)` (triton_tension/ops.py:192-224), which launches three Triton
+ * kernels with raw pointers, sizes and strides (ops.py:104-112,165-182;
+ * kernel.py:42-55,131-144,233-246).  The entry points below replace those
+ * launches one for one; the Python host layer (bozo_amd/ops.py) binds them
+ * with ctypes.
+ *
+ * Conventions
+ *  - Every tensor is described by a tension_buf: device pointer, dtype code,
+ *    and element strides.  4-D activations are [B,T,H,D] with strides
+ *    s[0..3] for (B,T,H,D); s[3] must be 1.  tau is [B,T,H,W] (s[3] == 1),
+ *    bias [B,T,W] (local) or [B,T,T] (global) uses s[0..2] and needs
+ *    s[2] == 1; mass is [B,T,H] (s[0..2]).
+ *  - A NULL tension_buf pointer means "absent" (no tau, no bias, ...).
+ *  - The library never allocates device memory.  Work is enqueued on the
+ *    given stream; no call synchronises the device.  All functions are
+ *    reentrant; the only global state is the per-thread error string.
+ *  - Return value: TENSION_OK or a TENSION_ERR_* code; tension_last_error()
+ *    describes the last failure on the calling thread.  Nothing throws
+ *    across the ABI.
+ */
+#ifndef TENSION_HIP_H
+#define TENSION_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tension_stream_t; /* == hipStream_t */
+
+/* dtype codes */
+enum {
+  TENSION_F32 = 0,
+  TENSION_BF16 = 1,
+  TENSION_F16 = 2,
+  TENSION_F64 = 3
+};
+
+/* status codes */
+enum {
+  TENSION_OK = 0,
+  TENSION_ERR_ARG = 1,         /* bad pointer / shape / stride / dtype combination */
+  TENSION_ERR_UNSUPPORTED = 2, /* valid request this build has no kernel for (e.g. D) */
+  TENSION_ERR_LAUNCH = 3       /* hipGetLastError() after the launch was not hipSuccess */
+};
+
+/* flags */
+enum {
+  /* out = msg / max(sum_w tau, 1e-6)        (model.py:257-258,281-282) */
+  TENSION_NORM_MASS = 1 << 0,
+  /* out = msg / max(min(t, W), 1)            (model.py:159-163,264) */
+  TENSION_NORM_COUNT = 1 << 1,
+  /* bias is [B,T,T] indexed by key position (global block, model.py:224-225) */
+  TENSION_GLOBAL = 1 << 2,
+  /* force the exact (non-MFMA) kernels even when the MFMA path applies */
+  TENSION_FORCE_EXACT = 1 << 3
+};
+
+typedef struct tension_buf {
+  void* ptr;
+  int32_t dtype;
+  int32_t reserved;
+  int64_t s[4];
+} tension_buf;
+
+/* ---------------------------------------------------------------------------
+ * Local window forward.  Replaces `_fwd_kernel` (kernel.py:41-125) launched by
+ * `_CausalTensionFn.forward` (ops.py:75-124).
+ *   tau[b,t,h,w] = sigmoid(q_t . k_s / scale + bias[b,t,w]),  s = t-(W-w),
+ *                  0 where s < 0;  msg = sum_w tau * v_s.
+ *   out = msg (raw, the reference contract), or normalised per flags.
+ *   q,k,v,out: [B,T,H,D]; tau (nullable, out): [B,T,H,W], written fully
+ *   (zeros on empty slots); bias (nullable): [B,T,W];
+ *   mass (nullable, out): [B,T,H] = sum_w tau (unclamped), f32 or f64.
+ *   Required when TENSION_NORM_MASS is set (the backward reads it).
+ * ------------------------------------------------------------------------- */
+int tension_window_fwd(const tension_buf* q, const tension_buf* k,
+                       const tension_buf* v, const tension_buf* out,
+                       const tension_buf* tau, const tension_buf* bias,
+                       const tension_buf* mass, int64_t B, int64_t T,
+                       int64_t H, int64_t D, int64_t W, double scale,
+                       int32_t flags, tension_stream_t stream);
+
+/* Bytes of device workspace tension_window_bwd needs (0 if none). */
+int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H,
+                                     int32_t dtype_acc, int32_t flags);
+
+/* ---------------------------------------------------------------------------
+ * Local window backward.  Replaces `_bwd_dq_kernel` + `_bwd_dkv_kernel`
+ * (kernel.py:130-341) launched by `_CausalTensionFn.backward`
+ * (ops.py:126-187).  Launches tension_window_bwd_dq then
+ * tension_window_bwd_dkv on `stream`.
+ *   dout: grad of out (or of raw msg when no NORM flag); dtau (nullable):
+ *   grad of tau; bias: same as forward.  out/mass: the forward's outputs,
+ *   required with TENSION_NORM_MASS.  dq/dk/dv written (not accumulated).
+ *   workspace: tension_window_bwd_workspace() bytes, or NULL if that is 0.
+ * ------------------------------------------------------------------------- */
+int tension_window_bwd(const tension_buf* q, const tension_buf* k,
+                       const tension_buf* v, const tension_buf* dout,
+                       const tension_buf* dtau, const tension_buf* bias,
+                       const tension_buf* out, const tension_buf* mass,
+                       const tension_buf* dq, const tension_buf* dk,
+                       const tension_buf* dv, void* workspace, int64_t B,
+                       int64_t T, int64_t H, int64_t D, int64_t W,
+                       double scale, int32_t flags, tension_stream_t stream);
+
+/* The two halves of tension_window_bwd, one kernel each (same arguments).
+ * _dq also fills the per-query workspace that _dkv reads, so on one stream
+ * _dq must precede _dkv.  Counterparts: kernel.py:130-227 / 232-341. */
+int tension_window_bwd_dq(const tension_buf* q, const tension_buf* k,
+                          const tension_buf* v, const tension_buf* dout,
+                          const tension_buf* dtau, const tension_buf* bias,
+                          const tension_buf* out, const tension_buf* mass,
+                          const tension_buf* dq, void* workspace, int64_t B,
+                          int64_t T, int64_t H, int64_t D, int64_t W,
+                          double scale, int32_t flags, tension_stream_t stream);
+int tension_window_bwd_dkv(const tension_buf* q, const tension_buf* k,
+                           const tension_buf* v, const tension_buf* dout,
+                           const tension_buf* dtau, const tension_buf* bias,
+                           const tension_buf* dk, const tension_buf* dv,
+                           void* workspace, int64_t B, int64_t T, int64_t H,
+                           int64_t D, int64_t W, double scale, int32_t flags,
+                           tension_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Global (full causal, diagonal included) block, tau-mass normalised.
+ * Replaces the PyTorch einsum path of the global layer (model.py:217-238);
+ * the reference has no kernel for it.
+ *   bias (nullable): [B,T,T] indexed [b,t,s].
+ *   tau_local (nullable, out): [B,T,H,Wl] with slot j = key s = T-1-j
+ *   (model.py:231-237), zero where s > t.  mass (out, required): [B,T,H].
+ * ------------------------------------------------------------------------- */
+int tension_global_fwd(const tension_buf* q, const tension_buf* k,
+                       const tension_buf* v, const tension_buf* out,
+                       const tension_buf* tau_local, const tension_buf* bias,
+                       const tension_buf* mass, int64_t B, int64_t T,
+                       int64_t H, int64_t D, int64_t Wl, double scale,
+                       int32_t flags, tension_stream_t stream);
+
+int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H,
+                                     int32_t dtype_acc, int32_t flags);
+
+/* Backward of tension_global_fwd: dout (grad of out), dtau_local (nullable,
+ * grad of tau_local [B,T,H,Wl]), out/mass from the forward. */
+int tension_global_bwd(const tension_buf* q, const tension_buf* k,
+                       const tension_buf* v, const tension_buf* dout,
+                       const tension_buf* dtau_local, const tension_buf* bias,
+                       const tension_buf* out, const tension_buf* mass,
+                       const tension_buf* dq, const tension_buf* dk,
+                       const tension_buf* dv, void* workspace, int64_t B,
+                       int64_t T, int64_t H, int64_t D, int64_t Wl,
+                       double scale, int32_t flags, tension_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Streaming decode step over a ring K/V cache (no reference kernel: the
+ * reference re-runs the whole forward per token, model.py:617-652,719-768;
+ * the streaming exporter reads tau[:, -1], ts_bridge/streaming.py:125-127).
+ *   q, k_new, v_new, out: [N,H,D] (s[0..2] used, s[2] == 1).
+ *   k_cache, v_cache: [N,H,W,D] (s[0..3], s[3] == 1), updated in place:
+ *   after attending, k_new/v_new are written to slot pos[n] % W.
+ *   pos_in: device int32 [N], tokens already cached per sequence.
+ *   pos_out (nullable): device int32 [N], receives pos_in + 1 (must not
+ *   alias pos_in).  tau (nullable, out): [N,H,W], w=0 oldest.
+ *   Attends to the min(pos, W) most recent cached tokens (strictly past).
+ *   flags: TENSION_NORM_MASS (tau-mass normalised) or 0 (raw).
+ * ------------------------------------------------------------------------- */
+int tension_decode_step(const tension_buf* q, const tension_buf* k_new,
+                        const tension_buf* v_new, const tension_buf* k_cache,
+                        const tension_buf* v_cache, const tension_buf* out,
+                        const tension_buf* tau, const int32_t* pos_in,
+                        int32_t* pos_out, int64_t N, int64_t H, int64_t D,
+                        int64_t W, double scale, int32_t flags,
+                        tension_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * RoPE (half-split rotation, model.py:54-81).  y = R(pos) x, or R(pos)^T x
+ * when inverse != 0 (the backward).  cos/sin: contiguous float32
+ * [table_rows, D/2] tables (the model's buffers); rows
+ * pos_offset .. pos_offset+T-1 are used and must exist.
+ * x, y: [B,T,H,D]; y may alias x.  A negative pos_in entry of
+ * tension_decode_step is read as 0.
+ * ------------------------------------------------------------------------- */
+int tension_rope(const tension_buf* x, const tension_buf* y, const float* cos,
+                 const float* sin, int64_t table_rows, int64_t B, int64_t T,
+                 int64_t H, int64_t D, int64_t pos_offset, int32_t inverse,
+                 tension_stream_t stream);
+
+/* Message for the last non-OK return on the calling thread ("" if none). */
+const char* tension_last_error(void);
+
+/* Library version string. */
+const char* tension_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENSION_HIP_H */

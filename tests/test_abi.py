@@ -1,0 +1,129 @@
+"""C ABI of libtension_hip.so, checked on the CPU (no kernel launches).
+
+* the library loads and exports every function include/tension_hip.h declares;
+* the ctypes signatures in bozo_amd/_lib.py have the header's arity;
+* argument validation rejects bad calls with TENSION_ERR_ARG and a message,
+  before any HIP call is made;
+* the product path has no CPU fallback.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tension_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = re.findall(r"^(?:const char\*|int64_t|int)\s+(tension_\w+)\s*\(([^;]*?)\)\s*;", text,
+                       flags=re.M | re.S)
+    out = {}
+    for name, params in decls:
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from bozo_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        from bozo_amd.build import build
+        build(verbose=False)
+    return L
+
+
+def test_header_parses():
+    fns = header_functions()
+    assert "tension_window_fwd" in fns and "tension_decode_step" in fns
+    assert len(fns) >= 12
+
+
+def test_library_exports_every_declared_symbol(lib):
+    h = ctypes.CDLL(lib.LIB_PATH)
+    for name in header_functions():
+        assert hasattr(h, name), f"{name} declared in tension_hip.h but not exported"
+
+
+def test_ctypes_signatures_match_header(lib):
+    fns = header_functions()
+    assert set(fns) == set(lib.SIGNATURES), set(fns) ^ set(lib.SIGNATURES)
+    for name, n in fns.items():
+        assert len(lib.SIGNATURES[name][1]) == n, name
+
+
+def test_version_and_empty_error(lib):
+    assert b"gfx950" in lib.lib().tension_version()
+    assert isinstance(lib.lib().tension_last_error(), bytes)
+
+
+def _buf(ptr=0x1000, dtype=0, strides=(4096, 64, 16, 1)):
+    from bozo_amd._lib import TensionBuf
+    return ctypes.pointer(TensionBuf(ctypes.c_void_p(ptr), dtype, 0, (ctypes.c_int64 * 4)(*strides)))
+
+
+def _fwd(lib, q=None, k=None, v=None, out=None, tau=None, bias=None, mass=None, B=1, T=16, H=1, D=16,
+         W=4, scale=4.0, flags=0):
+    q = q if q is not None else _buf()
+    return lib.lib().tension_window_fwd(q, k if k is not None else _buf(), v if v is not None else _buf(),
+                                        out if out is not None else _buf(), tau, bias, mass,
+                                        B, T, H, D, W, scale, flags, None)
+
+
+def test_validation_rejects_bad_arguments(lib):
+    L = lib
+    cases = [
+        dict(W=0),                                       # window < 1
+        dict(scale=0.0),                                 # zero scale
+        dict(scale=float("nan")),
+        dict(D=0),
+        dict(q=_buf(ptr=0)),                             # null data pointer
+        dict(k=_buf(dtype=7)),                           # bad dtype code
+        dict(v=_buf(strides=(4096, 64, 16, 2))),         # innermost stride != 1
+        dict(flags=L.NORM_MASS | L.NORM_COUNT),          # exclusive flags
+        dict(flags=L.NORM_MASS),                         # NORM_MASS without mass
+        dict(flags=L.GLOBAL),                            # global through the local entry
+    ]
+    for kw in cases:
+        assert _fwd(lib, **kw) == L.ERR_ARG, kw
+        assert lib.lib().tension_last_error(), kw
+
+
+def test_workspace_query(lib):
+    f = lib.lib().tension_window_bwd_workspace
+    assert f(2, 8, 3, lib.F32, 0) == 0
+    assert f(2, 8, 3, lib.F32, lib.NORM_MASS) == 2 * 2 * 8 * 3 * 4
+    assert f(2, 8, 3, lib.F64, lib.NORM_MASS) == 2 * 2 * 8 * 3 * 8
+    assert lib.lib().tension_global_bwd_workspace(1, 4, 2, lib.F32, 0) == 2 * 4 * 2 * 4
+
+
+def test_backward_needs_workspace_with_mass(lib):
+    b = _buf()
+    r = lib.lib().tension_window_bwd(b, b, b, b, None, None, b, _buf(strides=(16, 1, 1, 0)), b, b, b,
+                                     None, 1, 16, 1, 16, 4, 4.0, lib.NORM_MASS, None)
+    assert r == lib.ERR_ARG
+    assert b"workspace" in lib.lib().tension_last_error()
+
+
+def test_decode_validation(lib):
+    q = _buf(strides=(64, 16, 1, 0))
+    c = _buf()
+    pos = ctypes.c_void_p(0x2000)
+    f = lib.lib().tension_decode_step
+    assert f(q, q, q, c, c, q, None, None, None, 1, 1, 16, 8, 4.0, 0, None) == lib.ERR_ARG  # no pos
+    assert f(q, q, q, c, c, q, None, pos, pos, 1, 1, 16, 8, 4.0, 0, None) == lib.ERR_ARG    # aliasing
+    assert f(q, q, q, c, c, q, None, pos, None, 1, 1, 16, 0, 4.0, 0, None) == lib.ERR_ARG   # W = 0
+
+
+def test_no_cpu_fallback():
+    from bozo_amd import causal_tension, global_tension
+    x = torch.zeros(1, 8, 1, 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        causal_tension(x, x, x, 4, 4.0)
+    with pytest.raises(RuntimeError, match="GPU"):
+        global_tension(x, x, x, 4.0)

@@ -1,0 +1,100 @@
+"""Streaming decode and RoPE kernels against the oracle.
+
+Decode has no reference kernel; the contract (survey row A11) is that each
+step equals the last row of the tau-mass-normalised local window over the
+same sequence (causality, ts_bridge/streaming_parity.py:20-24), which the
+oracle's own tests pin.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tension_oracle as O
+from tests._util import f64, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def seq_inputs(N, L, H, D, seed, std=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(N, L, H, D, generator=g) * std for _ in range(3)]
+
+
+@pytest.mark.parametrize("dtype,D,W,prefill", [
+    (torch.bfloat16, 64, 64, 64),     # fast path, warm cache
+    (torch.bfloat16, 64, 32, 5),      # fast path, filling cache
+    (torch.float32, 64, 64, 70),      # exact path
+    (torch.bfloat16, 32, 16, 3),      # exact path (D != 64)
+])
+def test_decode_matches_window_rows(dev, dtype, D, W, prefill):
+    from bozo_amd import TensionDecodeCache
+    N, H, S = 3, 4, 12
+    L = prefill + S
+    q, k, v = (t.to(dtype) for t in seq_inputs(N, L, H, D, seed=W + prefill))
+    cache = TensionDecodeCache(N, H, D, W, dtype=dtype, device=dev)
+    for t in range(prefill):
+        cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev))
+    msg, tau = O.window_forward(f64(q), f64(k), f64(v), W, math.sqrt(D))
+    ref, _ = O.normalize_mass(msg, tau)
+    for t in range(prefill, L):
+        out, tt = cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev), return_tau=True)
+        torch.cuda.synchronize()
+        if dtype == torch.float32:
+            assert max_abs(f64(out), ref[:, t]) <= 1e-5
+            assert max_abs(f64(tt), tau[:, t]) <= 1e-5
+        else:
+            assert rel_l2(f64(out), ref[:, t]) <= 2e-2
+            assert max_abs(f64(tt), tau[:, t]) <= 4e-3
+    assert int(cache.pos[cache.cur][0]) == L
+
+
+def test_decode_config4_shape_steps(dev):
+    """BASELINE config 4 shape (64 seqs, H16, d64, W256 bf16): cache
+    pre-filled with W tokens, then steps checked against the oracle's
+    decode_step on the same ring contents."""
+    from bozo_amd import decode_step
+    N, H, D, W, S = 64, 16, 64, 256, 4
+    g = torch.Generator().manual_seed(3)
+    kc = (torch.randn(N, H, W, D, generator=g) * 0.5).to(torch.bfloat16)
+    vc = (torch.randn(N, H, W, D, generator=g) * 0.5).to(torch.bfloat16)
+    kd, vd = kc.to(dev), vc.to(dev)
+    pos = torch.full((N,), W, dtype=torch.int32)
+    pin, pout = pos.to(dev), torch.empty(N, dtype=torch.int32, device=dev)
+    for s in range(S):
+        q, kn, vn = ((torch.randn(N, H, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3))
+        tau = torch.empty(N, H, W, dtype=torch.bfloat16, device=dev)
+        out = decode_step(q.to(dev), kn.to(dev), vn.to(dev), kd, vd, pin, pout, 8.0, True, tau)
+        ro, rt = O.decode_step(f64(q), f64(kc), f64(vc), pos.numpy(), W, 8.0)
+        assert rel_l2(f64(out), ro) <= 2e-2
+        assert max_abs(f64(tau), rt) <= 4e-3
+        kc_np, vc_np, pos_np = O.decode_append(kc.float().numpy(), vc.float().numpy(), pos.numpy(),
+                                               kn.float().numpy(), vn.float().numpy(), W)
+        kc, vc = torch.from_numpy(kc_np).to(torch.bfloat16), torch.from_numpy(vc_np).to(torch.bfloat16)
+        pos = torch.from_numpy(pos_np.astype(np.int32))
+        assert torch.equal(kd.cpu(), kc) and torch.equal(vd.cpu(), vc)
+        assert torch.equal(pout.cpu(), pos)
+        pin, pout = pout, pin
+
+
+@pytest.mark.parametrize("dtype,out_dtype", [(torch.float32, None), (torch.bfloat16, torch.float32),
+                                             (torch.float64, None)])
+def test_rope(dev, dtype, out_dtype):
+    from bozo_amd import rope
+    B, T, H, D = 2, 50, 3, 64
+    cos, sin = O.rope_tables(128, D)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, T, H, D, generator=g).to(dtype)
+    xd = x.to(dev).requires_grad_(True)
+    y = rope(xd, torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev), pos_offset=7,
+             out_dtype=out_dtype)
+    dy = torch.randn(B, T, H, D, generator=g)
+    (y.double() * dy.to(dev).double()).sum().backward()
+    want = O.rope_apply(f64(x), cos, sin, pos_offset=7)
+    dwant = O.rope_apply_adjoint(dy.double().numpy(), cos, sin, pos_offset=7)
+    assert y.dtype == (out_dtype or dtype)
+    assert max_abs(f64(y), want) <= 1e-5
+    tol = 1e-5 if dtype != torch.bfloat16 else 2e-2
+    metric = max_abs if dtype != torch.bfloat16 else rel_l2
+    assert metric(f64(xd.grad), dwant) <= tol

@@ -1,0 +1,92 @@
+"""Parity of the global (full causal, diagonal included) block kernels
+against the float64 oracle (restating model.py:217-238)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tension_oracle as O
+from tests._util import f64, make_inputs, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def hip_run(inp, scale, dev, *, W_local=None, use_bias=False, use_dtl=False):
+    from bozo_amd import global_tension
+    Q, K, V = (inp[n].to(dev).requires_grad_(True) for n in "QKV")
+    bias = inp["bias"].to(dev) if use_bias else None
+    res = global_tension(Q, K, V, scale, bias=bias, W_local=W_local)
+    out, tl = res if W_local else (res, None)
+    loss = (out.float() * inp["dO"].to(dev).float()).sum()
+    if use_dtl:
+        loss = loss + (tl.float() * inp["dTau"].to(dev).float()).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    return out, tl, (Q.grad, K.grad, V.grad)
+
+
+def oracle_run(inp, scale, *, W_local=None, use_bias=False, use_dtl=False):
+    Q, K, V, dO = f64(inp["Q"]), f64(inp["K"]), f64(inp["V"]), f64(inp["dO"])
+    bias = f64(inp["bias"]) if use_bias else None
+    dtl = f64(inp["dTau"]) if use_dtl else None
+    out, mass, tl = O.global_forward(Q, K, V, scale, bias, W_local)
+    grads = O.global_backward(Q, K, V, scale, dO, bias, dtl)
+    return out, tl, grads
+
+
+def check(hip, ref, dtype, tl_checked=False):
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    metric = max_abs if dtype == torch.float32 else rel_l2
+    for name, g, r in zip(("out", "dQ", "dK", "dV"), (hip[0],) + tuple(hip[2]), (ref[0],) + tuple(ref[2])):
+        err = metric(f64(g), r)
+        assert err <= tol, f"{name}: err {err:.3e} > {tol:.1e}"
+    if tl_checked:
+        lim = 1e-5 if dtype == torch.float32 else 4e-3
+        assert max_abs(f64(hip[1]), ref[1]) <= lim
+
+
+def test_config3_bf16_full_size(dev):
+    """B4 H12 T2048 d64 bf16, full causal, tau-mass."""
+    B, H, T, D = 4, 12, 2048, 64
+    inp = make_inputs(B, T, H, D, seed=2, std=0.5, dtype=torch.bfloat16, rope=False)
+    check(hip_run(inp, 8.0, dev), oracle_run(inp, 8.0), torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [1, 33, 64, 130])
+def test_global_small(dev, dtype, T):
+    D = 64
+    inp = make_inputs(2, T, 3, D, seed=T, std=0.5, dtype=dtype, W=min(16, T), dtau_std=0.1,
+                      bias_std=0.5, bias_shape=(2, T, T))
+    hip = hip_run(inp, 8.0, dev, W_local=16, use_bias=True, use_dtl=True)
+    ref = oracle_run(inp, 8.0, W_local=16, use_bias=True, use_dtl=True)
+    check(hip, ref, dtype, True)
+
+
+def test_global_without_diagonal_equals_window(dev):
+    """Global with the diagonal biased to -inf equals the local window of W=T
+    (tau-mass normalised): the two kernels agree through the public ops."""
+    from bozo_amd import causal_tension, global_tension
+    B, T, H, D = 2, 96, 2, 32
+    inp = make_inputs(B, T, H, D, seed=21, dtype=torch.float32)
+    Q, K, V = (inp[n].to(dev) for n in "QKV")
+    nodiag = torch.zeros(B, T, T, device=dev)
+    nodiag[:, torch.arange(T), torch.arange(T)] = -1e30
+    a = global_tension(Q, K, V, math.sqrt(D), bias=nodiag)
+    b = causal_tension(Q, K, V, T, math.sqrt(D), normalize="mass")
+    assert max_abs(f64(a), f64(b)) <= 1e-5
+
+
+def test_gradcheck_float64(dev):
+    from bozo_amd import global_tension
+    torch.manual_seed(3)
+    B, T, H, D = 1, 12, 2, 8
+    Q, K, V = (torch.randn(B, T, H, D, device=dev, dtype=torch.float64, requires_grad=True)
+               for _ in range(3))
+    bias = torch.randn(B, T, T, device=dev, dtype=torch.float64) * 0.3
+
+    def fn(q, k, v):
+        return global_tension(q, k, v, math.sqrt(D), bias=bias, W_local=5)
+
+    assert torch.autograd.gradcheck(fn, (Q, K, V), eps=1e-6, atol=1e-6, rtol=1e-5)

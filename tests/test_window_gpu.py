@@ -1,0 +1,320 @@
+"""Parity of the local-window HIP kernels against the float64 oracle.
+
+Mirrors the reference's kernel tests (triton_tension/test.py,
+triton_tension/test_tau.py) with the oracle in place of the unfold
+reference, plus the benchmark configs and the edge cases of the band.
+Tolerances: float32 max-abs 1e-5 (normalised outputs and all gradients);
+raw float32 sums are O(10) in magnitude, so they are held to 1e-5 relative
+to max(1, |ref|max); bfloat16 relative L2 <= 2e-2 for out/dQ/dK/dV and an
+elementwise absolute bound of 4e-3 on tau (tau in [0,1], bf16 ulp at 1 is
+2^-8, rounding error <= 2^-9).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tension_oracle as O
+from tests._util import f64, make_inputs, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def hip_run(inp, W, scale, dev, *, normalize=None, return_tau=False, use_bias=False,
+            use_dtau=False, backward=True):
+    from bozo_amd import causal_tension
+    Q, K, V = (inp[n].to(dev).requires_grad_(backward) for n in "QKV")
+    bias = inp["bias"].to(dev) if use_bias else None
+    res = causal_tension(Q, K, V, W, scale, return_tau=return_tau, bias=bias, normalize=normalize)
+    out, tau = res if return_tau else (res, None)
+    grads = (None, None, None)
+    if backward:
+        loss = (out.float() * inp["dO"].to(dev).float()).sum()
+        if use_dtau:
+            loss = loss + (tau.float() * inp["dTau"].to(dev).float()).sum()
+        loss.backward()
+        grads = (Q.grad, K.grad, V.grad)
+    torch.cuda.synchronize()
+    return out, tau, grads
+
+
+def oracle_run(inp, W, scale, *, normalize=None, use_bias=False, use_dtau=False):
+    Q, K, V, dO = f64(inp["Q"]), f64(inp["K"]), f64(inp["V"]), f64(inp["dO"])
+    bias = f64(inp["bias"]) if use_bias else None
+    dTau = f64(inp["dTau"]) if use_dtau else None
+    msg, tau = O.window_forward(Q, K, V, W, scale, bias)
+    if normalize == "mass":
+        out, _ = O.normalize_mass(msg, tau)
+        grads = O.window_backward_normalized(Q, K, V, W, scale, dO, dTau, bias)
+    elif normalize == "count":
+        out = O.normalize_count(msg, W)
+        cnt = O.valid_count(Q.shape[1], W)[None, :, None, None]
+        grads = O.window_backward(Q, K, V, W, scale, dO / cnt, dTau, bias)
+    else:
+        out = msg
+        grads = O.window_backward(Q, K, V, W, scale, dO, dTau, bias)
+    return out, tau, grads
+
+
+def check_fp32(got, want, what, tol=1e-5):
+    err = max_abs(f64(got), want)
+    lim = tol * max(1.0, float(np.max(np.abs(want))) if want.size else 1.0)
+    assert err <= lim, f"{what}: max abs err {err:.3e} > {lim:.3e}"
+
+
+def check_bf16(got, want, what, tol=2e-2):
+    err = rel_l2(f64(got), want)
+    assert err <= tol, f"{what}: rel L2 err {err:.3e} > {tol:.1e}"
+
+
+def compare(hip, ref, dtype, tau_checked):
+    out, tau, grads = hip
+    rout, rtau, rgrads = ref
+    chk = check_fp32 if dtype in (torch.float32, torch.float64) else check_bf16
+    chk(out, rout, "out")
+    for n, g, r in zip(("dQ", "dK", "dV"), grads, rgrads):
+        if g is not None:
+            chk(g, r, n)
+    if tau_checked:
+        if dtype in (torch.float32, torch.float64):
+            assert max_abs(f64(tau), rtau) <= 1e-5
+        else:
+            assert max_abs(f64(tau), rtau) <= 4e-3
+
+
+# ------------------------------------------------------------ benchmark configs
+
+@pytest.mark.parametrize("with_tau", [False, True])
+def test_config1_fp32_normalised(dev, with_tau):
+    """B4 H4 T256 d32 W32 fp32, RoPE, out = sum tau v / sum tau."""
+    B, H, T, D, W = 4, 4, 256, 32, 32
+    inp = make_inputs(B, T, H, D, seed=0, W=W, dtau_std=0.1 if with_tau else None)
+    hip = hip_run(inp, W, math.sqrt(D), dev, normalize="mass", return_tau=with_tau, use_dtau=with_tau)
+    ref = oracle_run(inp, W, math.sqrt(D), normalize="mass", use_dtau=with_tau)
+    compare(hip, ref, torch.float32, with_tau)
+
+
+@pytest.mark.parametrize("normalize", [None, "mass"])
+def test_config2_bf16_full_size(dev, normalize):
+    """BASELINE config 2 at full size: B8 H12 T1024 d64 W64 bf16 (MFMA path)."""
+    B, H, T, D, W = 8, 12, 1024, 64, 64
+    inp = make_inputs(B, T, H, D, seed=1, std=0.5, dtype=torch.bfloat16)
+    hip = hip_run(inp, W, 8.0, dev, normalize=normalize)
+    ref = oracle_run(inp, W, 8.0, normalize=normalize)
+    compare(hip, ref, torch.bfloat16, False)
+
+
+def test_config2_bf16_with_tau_and_dtau(dev):
+    """Config 2 with tau materialised [B,T,H,W] and a gradient through it."""
+    B, H, T, D, W = 2, 12, 1024, 64, 64
+    inp = make_inputs(B, T, H, D, seed=1, std=0.5, dtype=torch.bfloat16, W=W, dtau_std=0.1)
+    hip = hip_run(inp, W, 8.0, dev, normalize="mass", return_tau=True, use_dtau=True)
+    ref = oracle_run(inp, W, 8.0, normalize="mass", use_dtau=True)
+    compare(hip, ref, torch.bfloat16, True)
+
+
+# ------------------------------------------------------------ reference kernel tests
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_forward_reference_shape(dev, dtype):
+    """triton_tension/test.py:59-73 (seed 0; B2 T32 H4 HD16 W8)."""
+    inp = make_inputs(2, 32, 4, 16, seed=0, rope=False, dtype=dtype)
+    hip = hip_run(inp, 8, 4.0, dev, backward=False)
+    ref = oracle_run(inp, 8, 4.0)
+    compare(hip, ref, dtype, False)
+
+
+def test_manual_grad_reference_shape(dev):
+    """triton_tension/test.py:95-128 (seed 2; B2 T24 H4 HD16 W8, fp32)."""
+    inp = make_inputs(2, 24, 4, 16, seed=2, rope=False)
+    compare(hip_run(inp, 8, 4.0, dev), oracle_run(inp, 8, 4.0), torch.float32, False)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_bias_forward_backward(dev, dtype):
+    """triton_tension/test.py:131-149,175-209 (bias [B,T,W] * 0.5)."""
+    inp = make_inputs(2, 32, 4, 16, seed=10, rope=False, dtype=dtype, bias_std=0.5,
+                      bias_shape=(2, 32, 8))
+    compare(hip_run(inp, 8, 4.0, dev, use_bias=True), oracle_run(inp, 8, 4.0, use_bias=True),
+            dtype, False)
+
+
+def test_bias_mfma_path(dev):
+    inp = make_inputs(2, 200, 3, 64, seed=12, std=0.5, dtype=torch.bfloat16, bias_std=0.5,
+                      bias_shape=(2, 200, 64), W=64, dtau_std=0.1)
+    hip = hip_run(inp, 64, 8.0, dev, normalize="mass", return_tau=True, use_bias=True, use_dtau=True)
+    ref = oracle_run(inp, 64, 8.0, normalize="mass", use_bias=True, use_dtau=True)
+    compare(hip, ref, torch.bfloat16, True)
+
+
+def test_large_bf16_spot_check(dev):
+    """triton_tension/test.py:212-227 (seed 3; B4 T512 H12 HD64 W64 bf16)."""
+    inp = make_inputs(4, 512, 12, 64, seed=3, rope=False, dtype=torch.bfloat16)
+    compare(hip_run(inp, 64, 8.0, dev), oracle_run(inp, 64, 8.0), torch.bfloat16, False)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_forward_tau(dev, dtype):
+    """triton_tension/test_tau.py:28-44."""
+    D = 16 if dtype == torch.float32 else 64
+    inp = make_inputs(2, 32, 4, D, seed=0, rope=False, dtype=dtype)
+    hip = hip_run(inp, 8, math.sqrt(D), dev, return_tau=True, backward=False)
+    compare(hip, oracle_run(inp, 8, math.sqrt(D)), dtype, True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_output_identical_with_without_tau(dev, dtype):
+    """triton_tension/test_tau.py:47-60: requesting tau does not change Out (exact)."""
+    from bozo_amd import causal_tension
+    D = 16 if dtype == torch.float32 else 64
+    inp = make_inputs(2, 70, 2, D, seed=1, rope=False, dtype=dtype)
+    Q, K, V = (inp[n].to(dev) for n in "QKV")
+    a = causal_tension(Q, K, V, 6, math.sqrt(D))
+    b, _ = causal_tension(Q, K, V, 6, math.sqrt(D), return_tau=True)
+    assert torch.equal(a, b)
+
+
+def test_backward_through_tau(dev):
+    """triton_tension/test_tau.py:63-99 (dTau * 0.1, raw output)."""
+    inp = make_inputs(2, 24, 4, 16, seed=2, rope=False, W=8, dtau_std=0.1)
+    hip = hip_run(inp, 8, 4.0, dev, return_tau=True, use_dtau=True)
+    compare(hip, oracle_run(inp, 8, 4.0, use_dtau=True), torch.float32, True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_tau_unused(dev, dtype):
+    """triton_tension/test_tau.py:102-127: unused tau leaves the grads unchanged."""
+    from bozo_amd import causal_tension
+    D = 16 if dtype == torch.float32 else 64
+    inp = make_inputs(2, 90, 4, D, seed=3, rope=False, dtype=dtype)
+    grads = []
+    for rt in (False, True):
+        Q, K, V = (inp[n].to(dev).requires_grad_(True) for n in "QKV")
+        r = causal_tension(Q, K, V, 8, math.sqrt(D), return_tau=rt)
+        out = r[0] if rt else r
+        (out.float() * inp["dO"].to(dev).float()).sum().backward()
+        grads.append((Q.grad, K.grad, V.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+def test_memory_vs_unfold(dev):
+    """triton_tension/test_tau.py:130-159: peak < unfold footprint / 4."""
+    from bozo_amd import causal_tension
+    B, T, H, D, W = 4, 1024, 16, 64, 256
+    g = torch.Generator(device=dev).manual_seed(4)
+    Q, K, V = (torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=g) for _ in range(3))
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    before = torch.cuda.memory_allocated()
+    out, tau = causal_tension(Q, K, V, W, 8.0, return_tau=True)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - before
+    unfold_bytes = B * T * H * W * D * 2
+    assert peak < unfold_bytes / 4
+    assert tau.shape == (B, T, H, W) and tau.dtype == torch.bfloat16
+
+
+# ------------------------------------------------------------ float64 gradcheck
+
+@pytest.mark.parametrize("normalize", [None, "mass", "count"])
+@pytest.mark.parametrize("use_bias", [False, True])
+def test_gradcheck_float64_on_gpu(dev, normalize, use_bias):
+    """Unlike the reference (whose float64 gradcheck falls back to PyTorch,
+    ops.py:217), this exercises the HIP backward kernels."""
+    from bozo_amd import causal_tension
+    torch.manual_seed(1)
+    B, T, H, D, W = 1, 16, 2, 16, 6
+    Q, K, V = (torch.randn(B, T, H, D, device=dev, dtype=torch.float64, requires_grad=True)
+               for _ in range(3))
+    bias = torch.randn(B, T, W, device=dev, dtype=torch.float64) * 0.3 if use_bias else None
+
+    def fn(q, k, v):
+        return causal_tension(q, k, v, W, math.sqrt(D), return_tau=True, bias=bias, normalize=normalize)
+
+    assert torch.autograd.gradcheck(fn, (Q, K, V), eps=1e-6, atol=1e-7, rtol=1e-6)
+
+
+# ------------------------------------------------------------ band edge cases
+
+@pytest.mark.parametrize("T,W", [(1, 4), (5, 8), (64, 64), (65, 64), (100, 64), (130, 1),
+                                 (300, 256), (200, 32), (77, 100)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_band_edges(dev, T, W, dtype):
+    D = 64
+    inp = make_inputs(2, T, 3, D, seed=T * 7 + W, std=0.5, dtype=dtype, W=W, dtau_std=0.1)
+    hip = hip_run(inp, W, 8.0, dev, normalize="mass", return_tau=True, use_dtau=True)
+    ref = oracle_run(inp, W, 8.0, normalize="mass", use_dtau=True)
+    compare(hip, ref, dtype, True)
+
+
+@pytest.mark.parametrize("D", [8, 16, 32, 128])
+def test_other_head_dims_exact_path(dev, D):
+    inp = make_inputs(2, 50, 2, D, seed=D, dtype=torch.bfloat16, W=12, dtau_std=0.1)
+    hip = hip_run(inp, 12, math.sqrt(D), dev, normalize="mass", return_tau=True, use_dtau=True)
+    ref = oracle_run(inp, 12, math.sqrt(D), normalize="mass", use_dtau=True)
+    compare(hip, ref, torch.bfloat16, True)
+
+
+def test_float16(dev):
+    inp = make_inputs(2, 70, 2, 64, seed=5, std=0.5, dtype=torch.float16)
+    compare(hip_run(inp, 16, 8.0, dev, normalize="mass"), oracle_run(inp, 16, 8.0, normalize="mass"),
+            torch.bfloat16, False)
+
+
+def test_strided_views_like_wkv_split(dev):
+    """model.py:206-207 splits a fused wkv projection: K and V are strided
+    views (innermost stride 1); the kernels read them in place."""
+    from bozo_amd import causal_tension
+    B, T, H, D, W = 2, 130, 4, 64, 64
+    g = torch.Generator().manual_seed(9)
+    kv = (torch.randn(B, T, H, 2 * D, generator=g) * 0.5).to(torch.bfloat16)
+    q = (torch.randn(B, T, H, D, generator=g) * 0.5).to(torch.bfloat16)
+    k, v = kv.split(D, dim=-1)
+    out = causal_tension(q.to(dev), kv.to(dev)[..., :D], kv.to(dev)[..., D:], W, 8.0, normalize="mass")
+    msg, tau = O.window_forward(f64(q), f64(k), f64(v), W, 8.0)
+    ref, _ = O.normalize_mass(msg, tau)
+    check_bf16(out, ref, "out")
+
+
+def test_mixed_dtypes_autocast_like(dev):
+    """Under autocast the reference feeds fp32 (RoPE'd) Q/K with bf16 V."""
+    inp = make_inputs(2, 96, 2, 64, seed=6, std=0.5)
+    inp["V"] = inp["V"].to(torch.bfloat16)
+    hip = hip_run(inp, 32, 8.0, dev, normalize="mass")
+    ref = oracle_run(inp, 32, 8.0, normalize="mass")
+    out, _, grads = hip
+    assert out.dtype == torch.float32 and grads[2].dtype == torch.bfloat16
+    check_fp32(out, ref[0], "out")
+    check_fp32(grads[0], ref[2][0], "dQ")
+    check_fp32(grads[1], ref[2][1], "dK")
+    check_bf16(grads[2], ref[2][2], "dV")
+
+
+def test_empty_batch(dev):
+    from bozo_amd import causal_tension
+    Q = torch.zeros(0, 16, 2, 64, device=dev, dtype=torch.bfloat16)
+    out = causal_tension(Q, Q, Q, 8, 8.0)
+    assert out.shape == Q.shape
+
+
+def test_deterministic(dev):
+    """No atomics: two runs are bitwise identical."""
+    inp = make_inputs(2, 300, 4, 64, seed=8, std=0.5, dtype=torch.bfloat16)
+    a = hip_run(inp, 64, 8.0, dev, normalize="mass")
+    b = hip_run(inp, 64, 8.0, dev, normalize="mass")
+    assert torch.equal(a[0], b[0])
+    for x, y in zip(a[2], b[2]):
+        assert torch.equal(x, y)
+
+
+def test_errors(dev):
+    from bozo_amd import causal_tension
+    Q = torch.zeros(1, 8, 1, 16, device=dev)
+    with pytest.raises(RuntimeError):
+        causal_tension(Q.cpu(), Q.cpu(), Q.cpu(), 4, 4.0)
+    with pytest.raises(ValueError):
+        causal_tension(Q, Q, Q, 4, 4.0, bias=torch.zeros(1, 8, 5, device=dev))
+    with pytest.raises(ValueError):
+        causal_tension(Q, Q, Q, 0, 4.0)
