@@ -126,21 +126,20 @@ def kernel_fns(s, W, scale, flags):
     B, T, H, D = s["Q"].shape
     Q, K, V, dO = (s[n].detach() for n in ("Q", "K", "V", "dO"))
     out = torch.empty_like(Q)
-    mass = torch.empty(B, T, H, device=Q.device)
     dq, dk, dv = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
     ws = torch.empty(max(1, L.lib().tension_window_bwd_workspace(B, T, H, L.F32, flags)),
                      dtype=torch.uint8, device=Q.device)
     lib = L.lib()
-    bq, bk, bv, bo, bm, bdo = (L.buf(t) for t in (Q, K, V, out, mass, dO))
+    bq, bk, bv, bo, bdo = (L.buf(t) for t in (Q, K, V, out, dO))
     bdq, bdk, bdv = L.buf(dq), L.buf(dk), L.buf(dv)
-    keep = (out, mass, dq, dk, dv, ws)
+    keep = (out, dq, dk, dv, ws)
 
     def fwd():
-        L.check(lib.tension_window_fwd(bq, bk, bv, bo, None, None, bm, B, T, H, D, W, scale, flags,
+        L.check(lib.tension_window_fwd(bq, bk, bv, bo, None, None, None, B, T, H, D, W, scale, flags,
                                        L.stream_handle()), "fwd")
 
     def dqf():
-        L.check(lib.tension_window_bwd_dq(bq, bk, bv, bdo, None, None, bo, bm, bdq, ws.data_ptr(),
+        L.check(lib.tension_window_bwd_dq(bq, bk, bv, bdo, None, None, bdq, ws.data_ptr(),
                                           B, T, H, D, W, scale, flags, L.stream_handle()), "dq")
 
     def dkvf():
@@ -155,8 +154,8 @@ def kernel_bytes(B, T, H, D, W, el=2):
     act = B * T * H * D * el           # one [B,T,H,D] bf16 tensor
     vec = B * T * H * 4                # one [B,T,H] fp32 tensor
     return {
-        "fwd": 3 * act + act + vec,              # Q,K,V -> out, mass
-        "dq": 5 * act + vec + act + 2 * vec,     # Q,K,V,dO,out,mass -> dQ, ws(a,c)
+        "fwd": 3 * act + act,                    # Q,K,V -> out
+        "dq": 4 * act + act + 2 * vec,           # Q,K,V,dO -> dQ, ws(a,c)
         "dkv": 4 * act + 2 * vec + 2 * act,      # Q,K,V,dO,ws -> dK,dV
     }
 
@@ -234,7 +233,9 @@ def bench_window(args, dev):
     dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
     d = per_kernel[dom]
 
-    step_bytes = sum(kbytes.values()) - 2 * B * T * H * 4  # ws a/c are produced and consumed internally
+    # compulsory HBM bytes of one fwd+bwd: read Q,K,V, write out; read Q,K,V,dO,
+    # write dQ,dK,dV (the a/c workspace is produced and consumed inside bwd)
+    step_bytes = 11 * B * T * H * D * 2
     result = {
         "metric": METRIC,
         "value": round(tokens / (ms * 1e-3), 1),

@@ -35,26 +35,30 @@ int launched(hipError_t e, const char* what) {
   return ok();
 }
 
+#define TRY(x)         \
+  do {                 \
+    int _r = (x);      \
+    if (_r) return _r; \
+  } while (0)
+
 bool dtype_ok(int dt) { return dt >= TENSION_F32 && dt <= TENSION_F64; }
 
-// A required or optional [.., .., .., D] tensor with unit innermost stride.
-int check4(const tension_buf* b, const char* what, bool required) {
+// A required or optional tensor; `unit` is the index of the stride that must
+// be 1 (the innermost one), or -1.
+int check_buf(const tension_buf* b, const char* what, bool required, int unit) {
   if (!b) return required ? fail(TENSION_ERR_ARG, "%s is required", what) : 0;
   if (!b->ptr) return fail(TENSION_ERR_ARG, "%s: null data pointer", what);
   if (!dtype_ok(b->dtype)) return fail(TENSION_ERR_ARG, "%s: bad dtype code %d", what, b->dtype);
-  if (b->s[3] != 1) return fail(TENSION_ERR_ARG, "%s: innermost stride must be 1 (got %lld)", what, (long long)b->s[3]);
-  return 0;
-}
-
-int check3(const tension_buf* b, const char* what, bool required, bool unit_last) {
-  if (!b) return required ? fail(TENSION_ERR_ARG, "%s is required", what) : 0;
-  if (!b->ptr) return fail(TENSION_ERR_ARG, "%s: null data pointer", what);
-  if (!dtype_ok(b->dtype)) return fail(TENSION_ERR_ARG, "%s: bad dtype code %d", what, b->dtype);
-  if (unit_last && b->s[2] != 1) return fail(TENSION_ERR_ARG, "%s: innermost stride must be 1", what);
+  if (unit >= 0 && b->s[unit] != 1)
+    return fail(TENSION_ERR_ARG, "%s: innermost stride must be 1 (got %lld)", what, (long long)b->s[unit]);
   return 0;
 }
 
 bool is_f64(const tension_buf* b) { return b && b->dtype == TENSION_F64; }
+
+bool any_f64(const tension_buf* a, const tension_buf* b, const tension_buf* c) {
+  return is_f64(a) || is_f64(b) || is_f64(c);
+}
 
 bool aligned_bf16_rows(const tension_buf* b) {
   if (!b || b->dtype != TENSION_BF16) return false;
@@ -68,13 +72,17 @@ struct Shape {
   int64_t B, T, H, D;
 };
 
-int check_shape(Shape sh, double scale) {
+// Shape and scale checks; sets *empty when there is nothing to compute (then
+// the data pointers are not inspected: an empty tensor may have none).
+int check_shape(Shape sh, double scale, bool* empty) {
   if (sh.B < 0 || sh.T < 0 || sh.H < 0 || sh.D <= 0)
-    return fail(TENSION_ERR_ARG, "bad shape B=%lld T=%lld H=%lld D=%lld", (long long)sh.B,
-                (long long)sh.T, (long long)sh.H, (long long)sh.D);
-  if (sh.T > 0x3fffffff || sh.H > 0x3fffffff || sh.B > 0x3fffffff || sh.B * sh.H * sh.T > (int64_t)1 << 40)
+    return fail(TENSION_ERR_ARG, "bad shape B=%lld T=%lld H=%lld D=%lld", (long long)sh.B, (long long)sh.T,
+                (long long)sh.H, (long long)sh.D);
+  if (sh.T > 0x3fffffff || sh.H > 0x3fffffff || sh.B > 0x3fffffff ||
+      sh.B * sh.H * sh.T > ((int64_t)1 << 40))
     return fail(TENSION_ERR_ARG, "shape too large");
   if (!(std::isfinite(scale) && scale != 0.0)) return fail(TENSION_ERR_ARG, "scale must be finite and non-zero");
+  *empty = sh.B * sh.H * sh.T == 0;
   return 0;
 }
 
@@ -106,81 +114,89 @@ void set_global(BandParams& p, int64_t Wl) {
   p.Wtau = (int)Wl;
 }
 
-// MFMA path: bf16 activations, D = 64, 16-byte aligned rows, fp32 side tensors.
-bool mfma_ok_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v,
-                 const tension_buf* out, const tension_buf* bias, const tension_buf* mass, int64_t D,
-                 int flags) {
-  if (flags & TENSION_FORCE_EXACT) return false;
-  if (D != 64) return false;
-  if (!aligned_bf16_rows(q) || !aligned_bf16_rows(k) || !aligned_bf16_rows(v) || !aligned_bf16_rows(out))
-    return false;
-  if (bias && bias->dtype != TENSION_F32) return false;
-  if (mass && mass->dtype != TENSION_F32) return false;
-  return true;
-}
-
 int run_band(int phase, bool mfma, bool f64, const BandParams& p, tension_stream_t stream, const char* what) {
-  if ((int64_t)p.B * p.H * p.T == 0) return ok();
   hipError_t e = hipSuccess;
   int r = mfma ? launch_mfma(phase, p, hs(stream), &e) : launch_exact(phase, f64, p, hs(stream), &e);
-  if (r != 0) return fail(TENSION_ERR_UNSUPPORTED, "%s: head dim %d not supported (exact path: 8,16,32,64,128)", what, p.D);
+  if (r != 0)
+    return fail(TENSION_ERR_UNSUPPORTED, "%s: head dim %d not supported (exact path: 8,16,32,64,128)", what, p.D);
   return launched(e, what);
 }
 
-#define TRY(x)            \
-  do {                    \
-    int _r = (x);         \
-    if (_r) return _r;    \
-  } while (0)
+// ---------------------------------------------------------------- forward
 
-int validate_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* out,
-                 const tension_buf* tau, const tension_buf* bias, const tension_buf* mass, Shape sh,
-                 double scale, int32_t flags, bool global) {
-  TRY(check_shape(sh, scale));
-  TRY(check4(q, "q", true));
-  TRY(check4(k, "k", true));
-  TRY(check4(v, "v", true));
-  TRY(check4(out, "out", true));
-  TRY(check4(tau, global ? "tau_local" : "tau", false));
-  TRY(check3(bias, "bias", false, true));
-  TRY(check3(mass, "mass", false, false));
+int band_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* out,
+             const tension_buf* tau, const tension_buf* bias, const tension_buf* mass, Shape sh, int64_t Wparam,
+             double scale, int32_t flags, tension_stream_t stream, bool global) {
+  const char* what = global ? "tension_global_fwd" : "tension_window_fwd";
+  bool empty = false;
+  TRY(check_shape(sh, scale, &empty));
+  if (!global && (Wparam < 1 || Wparam > 0x3fffffff))
+    return fail(TENSION_ERR_ARG, "window must be >= 1 (got %lld)", (long long)Wparam);
+  if (global && tau && (Wparam < 1 || Wparam > sh.T))
+    return fail(TENSION_ERR_ARG, "tau_local width must be in [1, T]");
   if ((flags & TENSION_NORM_MASS) && (flags & TENSION_NORM_COUNT))
     return fail(TENSION_ERR_ARG, "NORM_MASS and NORM_COUNT are exclusive");
+  if ((flags & TENSION_GLOBAL) && !global)
+    return fail(TENSION_ERR_ARG, "use tension_global_fwd for the global block");
+  if (global && (flags & TENSION_NORM_COUNT))
+    return fail(TENSION_ERR_ARG, "global block is tau-mass normalised only");
+  if (empty) return ok();
+  TRY(check_buf(q, "q", true, 3));
+  TRY(check_buf(k, "k", true, 3));
+  TRY(check_buf(v, "v", true, 3));
+  TRY(check_buf(out, "out", true, 3));
+  TRY(check_buf(tau, global ? "tau_local" : "tau", false, 3));
+  TRY(check_buf(bias, "bias", false, 2));
+  TRY(check_buf(mass, "mass", false, -1));
   if (mass && mass->dtype != TENSION_F32 && mass->dtype != TENSION_F64)
     return fail(TENSION_ERR_ARG, "mass must be f32 or f64");
-  return 0;
+  if (global) flags |= TENSION_NORM_MASS | TENSION_GLOBAL;
+  BandParams p = band_common(sh, scale, flags);
+  if (global) set_global(p, tau ? Wparam : 0); else set_local(p, Wparam);
+  p.q = make_buf(q); p.k = make_buf(k); p.v = make_buf(v);
+  p.out = make_buf(out); p.tau = make_buf(tau); p.bias = make_buf(bias); p.mass = make_buf(mass);
+  const bool mf = !(flags & TENSION_FORCE_EXACT) && sh.D == 64 && aligned_bf16_rows(q) && aligned_bf16_rows(k) &&
+                  aligned_bf16_rows(v) && aligned_bf16_rows(out) && (!bias || bias->dtype == TENSION_F32);
+  return run_band(0, mf, any_f64(q, k, v), p, stream, what);
 }
 
-int validate_bwd_common(const tension_buf* q, const tension_buf* k, const tension_buf* v,
-                        const tension_buf* dout, const tension_buf* dtau, const tension_buf* bias,
-                        const tension_buf* out, const tension_buf* mass, Shape sh, double scale,
-                        int32_t flags, void* ws, bool need_out) {
-  TRY(check_shape(sh, scale));
-  TRY(check4(q, "q", true));
-  TRY(check4(k, "k", true));
-  TRY(check4(v, "v", true));
-  TRY(check4(dout, "dout", true));
-  TRY(check4(dtau, "dtau", false));
-  TRY(check3(bias, "bias", false, true));
+// ---------------------------------------------------------------- backward
+
+// The workspace holds the per-query coefficients a_t, c_t of the tau-mass
+// backward (dtau = a_t * dP - c_t + dTau): fp32, or f64 when any activation
+// is f64.
+int64_t ws_bytes(int64_t B, int64_t T, int64_t H, int32_t dtype_acc, int32_t flags) {
+  if (!(flags & TENSION_NORM_MASS)) return 0;
+  const int64_t el = dtype_acc == TENSION_F64 ? 8 : 4;
+  return 2 * B * T * H * el;
+}
+
+int check_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
+              const tension_buf* dtau, const tension_buf* bias, Shape sh, int64_t Wparam, double scale,
+              int32_t flags, void* ws, bool global, bool* empty) {
+  TRY(check_shape(sh, scale, empty));
+  if (!global && (Wparam < 1 || Wparam > 0x3fffffff))
+    return fail(TENSION_ERR_ARG, "window must be >= 1 (got %lld)", (long long)Wparam);
+  if (global && dtau && (Wparam < 1 || Wparam > sh.T))
+    return fail(TENSION_ERR_ARG, "tau_local width must be in [1, T]");
   if ((flags & TENSION_NORM_MASS) && (flags & TENSION_NORM_COUNT))
     return fail(TENSION_ERR_ARG, "NORM_MASS and NORM_COUNT are exclusive");
-  if (flags & TENSION_NORM_MASS) {
-    if (need_out) {
-      TRY(check4(out, "out (saved forward output)", true));
-      TRY(check3(mass, "mass (saved forward mass)", true, false));
-    }
-    if (!ws) return fail(TENSION_ERR_ARG, "workspace is required with TENSION_NORM_MASS");
-  }
+  if (global && (flags & TENSION_NORM_COUNT))
+    return fail(TENSION_ERR_ARG, "global block is tau-mass normalised only");
+  if (*empty) return 0;
+  TRY(check_buf(q, "q", true, 3));
+  TRY(check_buf(k, "k", true, 3));
+  TRY(check_buf(v, "v", true, 3));
+  TRY(check_buf(dout, "dout", true, 3));
+  TRY(check_buf(dtau, global ? "dtau_local" : "dtau", false, 3));
+  TRY(check_buf(bias, "bias", false, 2));
+  if (((flags & TENSION_NORM_MASS) || global) && !ws)
+    return fail(TENSION_ERR_ARG, "workspace is required with tau-mass normalisation");
   return 0;
-}
-
-bool any_f64(const tension_buf* a, const tension_buf* b, const tension_buf* c) {
-  return is_f64(a) || is_f64(b) || is_f64(c);
 }
 
 bool mfma_ok_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                 const tension_buf* bias, const tension_buf* out, const tension_buf* mass,
-                 const tension_buf* o1, const tension_buf* o2, int64_t D, int flags) {
+                 const tension_buf* bias, const tension_buf* o1, const tension_buf* o2, int64_t D, int flags) {
   if (flags & TENSION_FORCE_EXACT) return false;
   if (D != 64) return false;
   if (!aligned_bf16_rows(q) || !aligned_bf16_rows(k) || !aligned_bf16_rows(v) || !aligned_bf16_rows(dout))
@@ -188,53 +204,46 @@ bool mfma_ok_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* 
   if (o1 && !aligned_bf16_rows(o1)) return false;
   if (o2 && !aligned_bf16_rows(o2)) return false;
   if (bias && bias->dtype != TENSION_F32) return false;
-  if (flags & TENSION_NORM_MASS) {
-    if (!aligned_bf16_rows(out)) return false;
-    if (!mass || mass->dtype != TENSION_F32) return false;
-  }
   return true;
 }
 
-// The workspace element type follows the path: fp32 for the MFMA path and
-// for non-f64 exact calls, f64 when any activation is f64.
-int64_t ws_bytes(int64_t B, int64_t T, int64_t H, int32_t dtype_acc, int32_t flags) {
-  if (!(flags & TENSION_NORM_MASS)) return 0;
-  const int64_t el = dtype_acc == TENSION_F64 ? 8 : 4;
-  return 2 * B * T * H * el;
+BandParams bwd_params(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
+                      const tension_buf* dtau, const tension_buf* bias, void* ws, Shape sh, int64_t Wparam,
+                      double scale, int32_t flags, bool global) {
+  if (global) flags |= TENSION_NORM_MASS | TENSION_GLOBAL;
+  BandParams p = band_common(sh, scale, flags);
+  if (global) set_global(p, dtau ? Wparam : 0); else set_local(p, Wparam);
+  p.q = make_buf(q); p.k = make_buf(k); p.v = make_buf(v);
+  p.dout = make_buf(dout); p.dtau = make_buf(dtau); p.bias = make_buf(bias); p.ws = ws;
+  return p;
 }
 
 int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                const tension_buf* dtau, const tension_buf* bias, const tension_buf* out,
-                const tension_buf* mass, const tension_buf* dq, void* ws, Shape sh, int64_t Wparam,
-                double scale, int32_t flags, tension_stream_t stream, bool global) {
-  TRY(validate_bwd_common(q, k, v, dout, dtau, bias, out, mass, sh, scale, flags, ws, true));
-  TRY(check4(dq, "dq", true));
-  if (global) flags |= TENSION_NORM_MASS;
-  BandParams p = band_common(sh, scale, flags);
-  if (global) set_global(p, Wparam); else set_local(p, Wparam);
-  p.q = make_buf(q); p.k = make_buf(k); p.v = make_buf(v);
-  p.dout = make_buf(dout); p.dtau = make_buf(dtau); p.bias = make_buf(bias);
-  p.out = make_buf(out); p.mass = make_buf(mass); p.dq = make_buf(dq); p.ws = ws;
-  const bool mf = mfma_ok_bwd(q, k, v, dout, bias, out, mass, dq, nullptr, sh.D, flags);
+                const tension_buf* dtau, const tension_buf* bias, const tension_buf* dq, void* ws, Shape sh,
+                int64_t Wparam, double scale, int32_t flags, tension_stream_t stream, bool global) {
+  bool empty = false;
+  TRY(check_bwd(q, k, v, dout, dtau, bias, sh, Wparam, scale, flags, ws, global, &empty));
+  if (empty) return ok();
+  TRY(check_buf(dq, "dq", true, 3));
+  BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, Wparam, scale, flags, global);
+  p.dq = make_buf(dq);
+  const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dq, nullptr, sh.D, flags);
   return run_band(1, mf, any_f64(q, k, v), p, stream, global ? "tension_global_bwd(dq)" : "tension_window_bwd_dq");
 }
 
 int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                 const tension_buf* dtau, const tension_buf* bias, const tension_buf* out,
-                 const tension_buf* mass, const tension_buf* dk, const tension_buf* dv, void* ws, Shape sh,
-                 int64_t Wparam, double scale, int32_t flags, tension_stream_t stream, bool global) {
-  TRY(validate_bwd_common(q, k, v, dout, dtau, bias, out, mass, sh, scale, flags, ws, false));
-  TRY(check4(dk, "dk", true));
-  TRY(check4(dv, "dv", true));
-  if (global) flags |= TENSION_NORM_MASS;
-  BandParams p = band_common(sh, scale, flags);
-  if (global) set_global(p, Wparam); else set_local(p, Wparam);
-  p.q = make_buf(q); p.k = make_buf(k); p.v = make_buf(v);
-  p.dout = make_buf(dout); p.dtau = make_buf(dtau); p.bias = make_buf(bias);
-  p.dk = make_buf(dk); p.dv = make_buf(dv); p.ws = ws;
-  // The dkv kernel reads the saved out/mass only through the workspace
-  // (fp32 unless an activation is f64, on either path).
-  const bool mf = mfma_ok_bwd(q, k, v, dout, bias, nullptr, nullptr, dk, dv, sh.D, flags & ~TENSION_NORM_MASS);
+                 const tension_buf* dtau, const tension_buf* bias, const tension_buf* dk, const tension_buf* dv,
+                 void* ws, Shape sh, int64_t Wparam, double scale, int32_t flags, tension_stream_t stream,
+                 bool global) {
+  bool empty = false;
+  TRY(check_bwd(q, k, v, dout, dtau, bias, sh, Wparam, scale, flags, ws, global, &empty));
+  if (empty) return ok();
+  TRY(check_buf(dk, "dk", true, 3));
+  TRY(check_buf(dv, "dv", true, 3));
+  BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, Wparam, scale, flags, global);
+  p.dk = make_buf(dk);
+  p.dv = make_buf(dv);
+  const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dk, dv, sh.D, flags);
   return run_band(2, mf, any_f64(q, k, v), p, stream, global ? "tension_global_bwd(dkv)" : "tension_window_bwd_dkv");
 }
 
@@ -250,17 +259,7 @@ int tension_window_fwd(const tension_buf* q, const tension_buf* k, const tension
                        const tension_buf* tau, const tension_buf* bias, const tension_buf* mass, int64_t B,
                        int64_t T, int64_t H, int64_t D, int64_t W, double scale, int32_t flags,
                        tension_stream_t stream) {
-  const Shape sh{B, T, H, D};
-  TRY(validate_fwd(q, k, v, out, tau, bias, mass, sh, scale, flags, false));
-  if (W < 1 || W > 0x3fffffff) return fail(TENSION_ERR_ARG, "window must be >= 1 (got %lld)", (long long)W);
-  if ((flags & TENSION_NORM_MASS) && !mass) return fail(TENSION_ERR_ARG, "NORM_MASS needs a mass output");
-  if (flags & TENSION_GLOBAL) return fail(TENSION_ERR_ARG, "use tension_global_fwd for the global block");
-  BandParams p = band_common(sh, scale, flags);
-  set_local(p, W);
-  p.q = make_buf(q); p.k = make_buf(k); p.v = make_buf(v);
-  p.out = make_buf(out); p.tau = make_buf(tau); p.bias = make_buf(bias); p.mass = make_buf(mass);
-  const bool mf = mfma_ok_fwd(q, k, v, out, bias, mass, D, flags);
-  return run_band(0, mf, any_f64(q, k, v), p, stream, "tension_window_fwd");
+  return band_fwd(q, k, v, out, tau, bias, mass, Shape{B, T, H, D}, W, scale, flags, stream, false);
 }
 
 int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H, int32_t dtype_acc, int32_t flags) {
@@ -269,12 +268,9 @@ int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H, int32_t dt
 
 int tension_window_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v,
                           const tension_buf* dout, const tension_buf* dtau, const tension_buf* bias,
-                          const tension_buf* out, const tension_buf* mass, const tension_buf* dq, void* ws,
-                          int64_t B, int64_t T, int64_t H, int64_t D, int64_t W, double scale, int32_t flags,
-                          tension_stream_t stream) {
-  if (W < 1 || W > 0x3fffffff) return fail(TENSION_ERR_ARG, "window must be >= 1 (got %lld)", (long long)W);
-  return band_bwd_dq(q, k, v, dout, dtau, bias, out, mass, dq, ws, Shape{B, T, H, D}, W, scale, flags, stream,
-                     false);
+                          const tension_buf* dq, void* ws, int64_t B, int64_t T, int64_t H, int64_t D, int64_t W,
+                          double scale, int32_t flags, tension_stream_t stream) {
+  return band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, Shape{B, T, H, D}, W, scale, flags, stream, false);
 }
 
 int tension_window_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* v,
@@ -282,39 +278,23 @@ int tension_window_bwd_dkv(const tension_buf* q, const tension_buf* k, const ten
                            const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T,
                            int64_t H, int64_t D, int64_t W, double scale, int32_t flags,
                            tension_stream_t stream) {
-  if (W < 1 || W > 0x3fffffff) return fail(TENSION_ERR_ARG, "window must be >= 1 (got %lld)", (long long)W);
-  return band_bwd_dkv(q, k, v, dout, dtau, bias, nullptr, nullptr, dk, dv, ws, Shape{B, T, H, D}, W, scale,
-                      flags, stream, false);
+  return band_bwd_dkv(q, k, v, dout, dtau, bias, dk, dv, ws, Shape{B, T, H, D}, W, scale, flags, stream, false);
 }
 
 int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                       const tension_buf* dtau, const tension_buf* bias, const tension_buf* out,
-                       const tension_buf* mass, const tension_buf* dq, const tension_buf* dk,
-                       const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H, int64_t D, int64_t W,
-                       double scale, int32_t flags, tension_stream_t stream) {
-  if (W < 1 || W > 0x3fffffff) return fail(TENSION_ERR_ARG, "window must be >= 1 (got %lld)", (long long)W);
+                       const tension_buf* dtau, const tension_buf* bias, const tension_buf* dq,
+                       const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H,
+                       int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
   const Shape sh{B, T, H, D};
-  TRY(check4(dk, "dk", true));
-  TRY(check4(dv, "dv", true));
-  TRY(band_bwd_dq(q, k, v, dout, dtau, bias, out, mass, dq, ws, sh, W, scale, flags, stream, false));
-  return band_bwd_dkv(q, k, v, dout, dtau, bias, out, mass, dk, dv, ws, sh, W, scale, flags, stream, false);
+  TRY(band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, sh, W, scale, flags, stream, false));
+  return band_bwd_dkv(q, k, v, dout, dtau, bias, dk, dv, ws, sh, W, scale, flags, stream, false);
 }
 
 int tension_global_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* out,
                        const tension_buf* tau_local, const tension_buf* bias, const tension_buf* mass, int64_t B,
                        int64_t T, int64_t H, int64_t D, int64_t Wl, double scale, int32_t flags,
                        tension_stream_t stream) {
-  const Shape sh{B, T, H, D};
-  TRY(validate_fwd(q, k, v, out, tau_local, bias, mass, sh, scale, flags, true));
-  if (!mass) return fail(TENSION_ERR_ARG, "tension_global_fwd: mass output is required");
-  if (flags & TENSION_NORM_COUNT) return fail(TENSION_ERR_ARG, "global block is tau-mass normalised only");
-  if (tau_local && (Wl < 1 || Wl > T)) return fail(TENSION_ERR_ARG, "tau_local width must be in [1, T]");
-  BandParams p = band_common(sh, scale, flags | TENSION_NORM_MASS | TENSION_GLOBAL);
-  set_global(p, tau_local ? Wl : 0);
-  p.q = make_buf(q); p.k = make_buf(k); p.v = make_buf(v);
-  p.out = make_buf(out); p.tau = make_buf(tau_local); p.bias = make_buf(bias); p.mass = make_buf(mass);
-  const bool mf = mfma_ok_fwd(q, k, v, out, bias, mass, D, flags);
-  return run_band(0, mf, any_f64(q, k, v), p, stream, "tension_global_fwd");
+  return band_fwd(q, k, v, out, tau_local, bias, mass, Shape{B, T, H, D}, Wl, scale, flags, stream, true);
 }
 
 int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H, int32_t dtype_acc, int32_t flags) {
@@ -322,42 +302,34 @@ int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H, int32_t dt
 }
 
 int tension_global_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                       const tension_buf* dtau_local, const tension_buf* bias, const tension_buf* out,
-                       const tension_buf* mass, const tension_buf* dq, const tension_buf* dk,
-                       const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H, int64_t D, int64_t Wl,
-                       double scale, int32_t flags, tension_stream_t stream) {
+                       const tension_buf* dtau_local, const tension_buf* bias, const tension_buf* dq,
+                       const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H,
+                       int64_t D, int64_t Wl, double scale, int32_t flags, tension_stream_t stream) {
   const Shape sh{B, T, H, D};
-  if (flags & TENSION_NORM_COUNT) return fail(TENSION_ERR_ARG, "global block is tau-mass normalised only");
-  if (dtau_local && (Wl < 1 || Wl > T)) return fail(TENSION_ERR_ARG, "tau_local width must be in [1, T]");
-  const int64_t wl = dtau_local ? Wl : 0;
-  TRY(check4(dk, "dk", true));
-  TRY(check4(dv, "dv", true));
-  TRY(band_bwd_dq(q, k, v, dout, dtau_local, bias, out, mass, dq, ws, sh, wl, scale, flags | TENSION_NORM_MASS,
-                  stream, true));
-  return band_bwd_dkv(q, k, v, dout, dtau_local, bias, out, mass, dk, dv, ws, sh, wl, scale,
-                      flags | TENSION_NORM_MASS, stream, true);
+  TRY(band_bwd_dq(q, k, v, dout, dtau_local, bias, dq, ws, sh, Wl, scale, flags, stream, true));
+  return band_bwd_dkv(q, k, v, dout, dtau_local, bias, dk, dv, ws, sh, Wl, scale, flags, stream, true);
 }
 
 int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const tension_buf* v_new,
                         const tension_buf* k_cache, const tension_buf* v_cache, const tension_buf* out,
                         const tension_buf* tau, const int32_t* pos_in, int32_t* pos_out, int64_t N, int64_t H,
                         int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
-  if (N < 0 || H < 0 || D <= 0 || D > 256 || W < 1 || N * H > 0x3fffffff)
+  if (N < 0 || H < 0 || D <= 0 || D > 256 || W < 1 || W > 0x3fffffff || N * H > 0x3fffffff)
     return fail(TENSION_ERR_ARG, "decode: bad sizes N=%lld H=%lld D=%lld W=%lld", (long long)N, (long long)H,
                 (long long)D, (long long)W);
   if (!(std::isfinite(scale) && scale != 0.0)) return fail(TENSION_ERR_ARG, "scale must be finite and non-zero");
-  TRY(check3(q, "q", true, true));
-  TRY(check3(k_new, "k_new", true, true));
-  TRY(check3(v_new, "v_new", true, true));
-  TRY(check3(out, "out", true, true));
-  TRY(check4(k_cache, "k_cache", true));
-  TRY(check4(v_cache, "v_cache", true));
-  if (tau) TRY(check3(tau, "tau", true, true));
+  if (N * H == 0) return ok();
+  TRY(check_buf(q, "q", true, 2));
+  TRY(check_buf(k_new, "k_new", true, 2));
+  TRY(check_buf(v_new, "v_new", true, 2));
+  TRY(check_buf(out, "out", true, 2));
+  TRY(check_buf(k_cache, "k_cache", true, 3));
+  TRY(check_buf(v_cache, "v_cache", true, 3));
+  TRY(check_buf(tau, "tau", false, 2));
   if (!pos_in) return fail(TENSION_ERR_ARG, "pos_in is required");
   if (pos_out && pos_out == pos_in) return fail(TENSION_ERR_ARG, "pos_out must not alias pos_in");
   if (k_cache->dtype != k_new->dtype || v_cache->dtype != v_new->dtype)
     return fail(TENSION_ERR_ARG, "cache and new-token dtypes must match");
-  if (N * H == 0) return ok();
   DecodeParams p;
   memset(&p, 0, sizeof p);
   p.q = make_buf(q); p.kn = make_buf(k_new); p.vn = make_buf(v_new);
@@ -380,16 +352,17 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
 int tension_rope(const tension_buf* x, const tension_buf* y, const float* cos, const float* sin,
                  int64_t table_rows, int64_t B, int64_t T, int64_t H, int64_t D, int64_t pos_offset,
                  int32_t inverse, tension_stream_t stream) {
-  TRY(check_shape(Shape{B, T, H, D}, 1.0));
+  bool empty = false;
+  TRY(check_shape(Shape{B, T, H, D}, 1.0, &empty));
   if (D % 2) return fail(TENSION_ERR_ARG, "rope: head dim must be even");
   if (pos_offset < 0) return fail(TENSION_ERR_ARG, "rope: negative position offset");
   if (pos_offset + T > table_rows)
     return fail(TENSION_ERR_ARG, "rope: table has %lld rows, positions up to %lld requested",
                 (long long)table_rows, (long long)(pos_offset + T));
-  TRY(check4(x, "x", true));
-  TRY(check4(y, "y", true));
+  if (empty) return ok();
+  TRY(check_buf(x, "x", true, 3));
+  TRY(check_buf(y, "y", true, 3));
   if (!cos || !sin) return fail(TENSION_ERR_ARG, "rope: cos/sin tables are required");
-  if (B * T * H == 0) return ok();
   RopeParams p;
   memset(&p, 0, sizeof p);
   p.x = make_buf(x); p.y = make_buf(y); p.cos = cos; p.sin = sin;

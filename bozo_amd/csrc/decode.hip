@@ -31,26 +31,28 @@ __global__ __launch_bounds__(kDecThreads) void decode_bf16_d64(DecodeParams p) {
   const int npass = W >> 5;
 
   const bf16* qrow = (const bf16*)p.q.p + n * p.q.s0 + h * p.q.s1;
-  const u16x8 qv = *(const u16x8*)(qrow + 8 * ch);
+  // Whole-vector bit casts only: a bit cast of one subscripted vector
+  // element (bit_cast<bf16>(v[i])) compiles to element 0 for every i.
+  const bf16x8 qv = __builtin_bit_cast(bf16x8, *(const u16x8*)(qrow + 8 * ch));
   float q[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = (float)__builtin_bit_cast(bf16, qv[i]);
+  for (int i = 0; i < 8; ++i) q[i] = (float)qv[i];
 
   const bf16* kbase = (const bf16*)p.kc.p + n * p.kc.s0 + h * p.kc.s1;
   const bf16* vbase = (const bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1;
-  u16x8 kr[kDecMaxPasses], vr[kDecMaxPasses];
+  bf16x8 kr[kDecMaxPasses], vr[kDecMaxPasses];
 #pragma unroll
   for (int i = 0; i < kDecMaxPasses; ++i) {
     if (i < npass) {
       const int slot = i * 32 + wave * 8 + rw;
-      kr[i] = *(const u16x8*)(kbase + (int64_t)slot * p.kc.s2 + 8 * ch);
+      kr[i] = __builtin_bit_cast(bf16x8, *(const u16x8*)(kbase + (int64_t)slot * p.kc.s2 + 8 * ch));
     }
   }
 #pragma unroll
   for (int i = 0; i < kDecMaxPasses; ++i) {
     if (i < npass) {
       const int slot = i * 32 + wave * 8 + rw;
-      vr[i] = *(const u16x8*)(vbase + (int64_t)slot * p.vc.s2 + 8 * ch);
+      vr[i] = __builtin_bit_cast(bf16x8, *(const u16x8*)(vbase + (int64_t)slot * p.vc.s2 + 8 * ch));
     }
   }
   const float inv_scale = (float)(1.0 / p.scale);
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_bf16_d64(DecodeParams p) {
       const int slot = i * 32 + wave * 8 + rw;
       float part = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part += q[e] * (float)__builtin_bit_cast(bf16, kr[i][e]);
+      for (int e = 0; e < 8; ++e) part += q[e] * (float)kr[i][e];
       part += __shfl_xor(part, 1);
       part += __shfl_xor(part, 2);
       part += __shfl_xor(part, 4);
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_bf16_d64(DecodeParams p) {
         st<float>(p.tau, n * p.tau.s0 + h * p.tau.s1 + ring_w(slot, pos, W), tau);
       msum += tau;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += tau * (float)__builtin_bit_cast(bf16, vr[i][e]);
+      for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vr[i][e];
     }
   }
   // fold rows within the wave (lanes with equal ch)

@@ -79,25 +79,12 @@ __global__ __launch_bounds__(128) void exact_fwd(BandParams p) {
 }
 
 // Per-query coefficients of the backward:  dtau = a_t * (dO_t . v_s) - c_t
-// (+ dTau).  raw: a = 1, c = 0; count: a = 1/max(min(t,W),1), c = 0;
-// tau-mass (out = msg/m): a = 1/m, c = (dO_t . out_t)/m while mass >= eps
-// (the clamp passes no gradient below eps).
-template <typename A>
-__device__ __forceinline__ void query_coeffs(const BandParams& p, int b, int t, int h,
-                                             A dot_dout_out, A* a, A* c) {
-  *a = A(1);
-  *c = A(0);
-  if (p.flags & TENSION_NORM_MASS) {
-    const A mass = ld<A>(p.mass, b * p.mass.s0 + (int64_t)t * p.mass.s1 + h * p.mass.s2);
-    const A m = mass > A(kMassEps) ? mass : A(kMassEps);
-    *a = A(1) / m;
-    *c = mass >= A(kMassEps) ? dot_dout_out / m : A(0);
-  } else if (p.flags & TENSION_NORM_COUNT) {
-    const int cnt = t < p.W ? t : p.W;
-    *a = A(1) / A(cnt > 1 ? cnt : 1);
-  }
-}
-
+// (+ dTau).  raw: a = 1, c = 0; count: a = 1/max(min(t,W),1), c = 0.
+// tau-mass (out = msg/m, m = max(sum tau, eps)): a = 1/m and
+// c = (dO_t . msg_t)/m^2 = sum_s tau_s (dO_t . v_s) / m^2 while the mass is
+// >= eps (the clamp passes no gradient below eps).  c is formed from the
+// recomputed fp32/f64 band sums, never from the stored (possibly bf16) out:
+// dO.v_s - dO.out cancels when a query has one dominant key.
 template <typename A, int D>
 __global__ __launch_bounds__(128) void exact_bwd_dq(BandParams p) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -111,8 +98,6 @@ __global__ __launch_bounds__(128) void exact_bwd_dq(BandParams p) {
   const int64_t qo = b * p.q.s0 + (int64_t)t * p.q.s1 + h * p.q.s2;
   const int64_t go = b * p.dout.s0 + (int64_t)t * p.dout.s1 + h * p.dout.s2;
   A q[D], g[D], dq[D];
-  A dgo = A(0);
-  const int64_t oo = b * p.out.s0 + (int64_t)t * p.out.s1 + h * p.out.s2;
 #pragma unroll
   for (int d = 0; d < D; d += 8) {
     ld8<A>(p.q, qo + d, q + d);
@@ -120,26 +105,47 @@ __global__ __launch_bounds__(128) void exact_bwd_dq(BandParams p) {
   }
 #pragma unroll
   for (int d = 0; d < D; ++d) dq[d] = A(0);
+  const A scale = (A)p.scale;
+  const int s_lo = t - p.win > 0 ? t - p.win : 0;
+  const int s_hi = t - 1 + p.diag;
+
+  A ca = A(1), cc = A(0);
   if (p.flags & TENSION_NORM_MASS) {
+    A mass = A(0), dsum = A(0);
+    for (int s = s_lo; s <= s_hi; ++s) {
+      const int64_t ko = b * p.k.s0 + (int64_t)s * p.k.s1 + h * p.k.s2;
+      const int64_t vo = b * p.v.s0 + (int64_t)s * p.v.s1 + h * p.v.s2;
+      A dot = A(0), gv = A(0);
 #pragma unroll
-    for (int d = 0; d < D; d += 8) {
-      A r[8];
-      ld8<A>(p.out, oo + d, r);
+      for (int d = 0; d < D; d += 8) {
+        A rk[8], rv[8];
+        ld8<A>(p.k, ko + d, rk);
+        ld8<A>(p.v, vo + d, rv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dgo += g[d + i] * r[i];
+        for (int i = 0; i < 8; ++i) {
+          dot += q[d + i] * rk[i];
+          gv += g[d + i] * rv[i];
+        }
+      }
+      A x = dot / scale;
+      if (p.bias.p) x += ld<A>(p.bias, bias_off(p, b, t, s));
+      const A tau = sigmoid_exact(x);
+      mass += tau;
+      dsum += tau * gv;
     }
+    const A m = mass > A(kMassEps) ? mass : A(kMassEps);
+    ca = A(1) / m;
+    cc = mass >= A(kMassEps) ? dsum / (m * m) : A(0);
+  } else if (p.flags & TENSION_NORM_COUNT) {
+    const int cnt = t < p.W ? t : p.W;
+    ca = A(1) / A(cnt > 1 ? cnt : 1);
   }
-  A ca, cc;
-  query_coeffs<A>(p, b, t, h, dgo, &ca, &cc);
   if (p.ws && (p.flags & TENSION_NORM_MASS)) {
     const int64_t n = (int64_t)p.B * p.T * p.H;
     const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
     ((A*)p.ws)[wi] = ca;
     ((A*)p.ws)[n + wi] = cc;
   }
-  const A scale = (A)p.scale;
-  const int s_lo = t - p.win > 0 ? t - p.win : 0;
-  const int s_hi = t - 1 + p.diag;
   for (int s = s_lo; s <= s_hi; ++s) {
     const int64_t ko = b * p.k.s0 + (int64_t)s * p.k.s1 + h * p.k.s2;
     const int64_t vo = b * p.v.s0 + (int64_t)s * p.v.s1 + h * p.v.s2;

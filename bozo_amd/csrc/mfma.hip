@@ -198,6 +198,22 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd(BandParams p) {
 
 // ------------------------------------------------------------------ dQ
 
+// S^T and dP^T of one 64-key block for this wave's 16 queries (C layout:
+// lane (g, c) holds keys 16j + 4g + r of query c).
+__device__ __forceinline__ void scores_block(const bf16* Ks, const bf16* Vs, const bf16x8* qf,
+                                             const bf16x8* gf, int g, int c, f32x4* s, f32x4* dp) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f32x4 a = {}, d = {};
+    a = mfma(lds8(Ks + (16 * j + c) * kPitch + 8 * g), qf[0], a);
+    a = mfma(lds8(Ks + (16 * j + c) * kPitch + 32 + 8 * g), qf[1], a);
+    d = mfma(lds8(Vs + (16 * j + c) * kPitch + 8 * g), gf[0], d);
+    d = mfma(lds8(Vs + (16 * j + c) * kPitch + 32 + 8 * g), gf[1], d);
+    s[j] = a;
+    dp[j] = d;
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Ks[kTile * kPitch];
   __shared__ __attribute__((aligned(16))) bf16 Vs[kTile * kPitch];
@@ -223,57 +239,76 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandParams p) {
   gf[1] = load8(gb_ + (int64_t)tr * p.dout.s1 + 32 + 8 * g);
   if (!qok) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; gf[0] = bf16x8{}; gf[1] = bf16x8{}; }
 
-  // per-query coefficients a, c (dtau = a * dP - c + dTau)
-  float ca = 1.f, cc = 0.f;
-  if (p.flags & TENSION_NORM_MASS) {
-    const bf16* orow = (const bf16*)p.out.p + b * p.out.s0 + (int64_t)tr * p.out.s1 + h * p.out.s2;
-    const bf16x8 o0 = load8(orow + 8 * g), o1 = load8(orow + 32 + 8 * g);
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) part += (float)gf[0][i] * (float)o0[i] + (float)gf[1][i] * (float)o1[i];
-    part = wave_sum_g(part);
-    const float mass = ld<float>(p.mass, b * p.mass.s0 + (int64_t)tr * p.mass.s1 + h * p.mass.s2);
-    const float m = mass > kMassEps ? mass : kMassEps;
-    ca = 1.f / m;
-    cc = mass >= kMassEps ? part / m : 0.f;
-  } else if (p.flags & TENSION_NORM_COUNT) {
-    const int cnt = tq < p.W ? tq : p.W;
-    ca = 1.f / (float)(cnt > 1 ? cnt : 1);
-  }
-  if (p.ws && (p.flags & TENSION_NORM_MASS) && qok && g == 0) {
-    const int64_t n = (int64_t)p.B * p.T * p.H;
-    const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
-    ((float*)p.ws)[wi] = ca;
-    ((float*)p.ws)[n + wi] = cc;
-  }
-
   const float inv_scale = (float)(1.0 / p.scale);
-  f32x4 acc[4] = {};
   int s_lo = t0 - p.win;
   if (s_lo < 0) s_lo = 0;
   int s_hi = t0 + kTile - 2 + p.diag;
   if (s_hi > T - 1) s_hi = T - 1;
-  for (int kb0 = s_lo & ~(kTile - 1); kb0 <= s_hi; kb0 += kTile) {
+  const int kb_first = s_lo & ~(kTile - 1);
+
+  // Per-query coefficients (dtau = a * dP - c + dTau).  Tau-mass: a = 1/m,
+  // c = sum_s tau dP / m^2, both from a first pass over the band in fp32 (no
+  // use of the bf16 forward output, whose rounding would not cancel in
+  // dP - c when one key dominates a query).
+  float ca = 1.f, cc = 0.f;
+  if (p.flags & TENSION_NORM_MASS) {
+    float msum = 0.f, dsum = 0.f;
+    for (int kb0 = kb_first; kb0 <= s_hi; kb0 += kTile) {
+      __syncthreads();
+      stage_tile(kb_, p.k.s1, kb0, T, Ks, nullptr, tid);
+      stage_tile(vb_, p.v.s1, kb0, T, Vs, nullptr, tid);
+      __syncthreads();
+      f32x4 s[4], dp[4];
+      scores_block(Ks, Vs, qf, gf, g, c, s, dp);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * j + 4 * g + r;
+          const bool ok = qok && band_valid(p, tq, key);
+          float x = s[j][r] * inv_scale;
+          if (ok && p.bias.p) x += ld<float>(p.bias, bias_off(p, b, tq, key));
+          const float pv = ok ? sigmoid_fast(x) : 0.f;
+          msum += pv;
+          dsum += pv * dp[j][r];
+        }
+      }
+    }
+    msum = wave_sum_g(msum);
+    dsum = wave_sum_g(dsum);
+    const float m = msum > kMassEps ? msum : kMassEps;
+    ca = 1.f / m;
+    cc = msum >= kMassEps ? dsum * ca * ca : 0.f;
+    if (p.ws && qok && g == 0) {
+      const int64_t n = (int64_t)p.B * p.T * p.H;
+      const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
+      ((float*)p.ws)[wi] = ca;
+      ((float*)p.ws)[n + wi] = cc;
+    }
+  } else if (p.flags & TENSION_NORM_COUNT) {
+    const int cnt = tq < p.W ? tq : p.W;
+    ca = 1.f / (float)(cnt > 1 ? cnt : 1);
+  }
+
+  f32x4 acc[4] = {};
+  for (int kb0 = kb_first; kb0 <= s_hi; kb0 += kTile) {
     __syncthreads();
     stage_tile(kb_, p.k.s1, kb0, T, Ks, Kt, tid);
     stage_tile(vb_, p.v.s1, kb0, T, Vs, nullptr, tid);
     __syncthreads();
+    f32x4 s[4], dp[4];
+    scores_block(Ks, Vs, qf, gf, g, c, s, dp);
     float gd[4][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      f32x4 s = {}, dp = {};
-      s = mfma(lds8(Ks + (16 * j + c) * kPitch + 8 * g), qf[0], s);
-      s = mfma(lds8(Ks + (16 * j + c) * kPitch + 32 + 8 * g), qf[1], s);
-      dp = mfma(lds8(Vs + (16 * j + c) * kPitch + 8 * g), gf[0], dp);
-      dp = mfma(lds8(Vs + (16 * j + c) * kPitch + 32 + 8 * g), gf[1], dp);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = qok && band_valid(p, tq, key);
-        float x = s[r] * inv_scale;
+        float x = s[j][r] * inv_scale;
         if (ok && p.bias.p) x += ld<float>(p.bias, bias_off(p, b, tq, key));
         const float pv = sigmoid_fast(x);
-        float dt = dp[r] * ca - cc;
+        float dt = dp[j][r] * ca - cc;
         if (ok && p.dtau.p) {
           const int col = tau_col(p, tq, key);
           if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, tq, h, col));

@@ -59,10 +59,6 @@ def _acc_code(*ts: Tensor) -> int:
     return L.F64 if any(t.dtype == torch.float64 for t in ts) else L.F32
 
 
-def _mass_dtype(*ts: Tensor) -> torch.dtype:
-    return torch.float64 if any(t.dtype == torch.float64 for t in ts) else torch.float32
-
-
 def _side(t: Optional[Tensor], like: Tensor) -> Optional[Tensor]:
     """Side inputs (bias) are kept in float32, as the reference does
     (ops.py:93), or float64 for float64 calls."""
@@ -106,10 +102,9 @@ class _CausalTensionFn(torch.autograd.Function):
         if Bias is not None and tuple(Bias.shape) != (B, T, W):
             raise ValueError(f"bias must be [B, T, W]=[{B}, {T}, {W}], got {tuple(Bias.shape)}")
         tau = torch.empty(B, T, H, W, dtype=Q.dtype, device=Q.device) if return_tau else None
-        mass = (torch.empty(B, T, H, dtype=_mass_dtype(Q, K, V), device=Q.device)
-                if flags & L.NORM_MASS else None)
-        out = _window_fwd(Q, K, V, W, scale, tau, Bias, flags, mass)
-        ctx.save_for_backward(Q, K, V, Bias, out if mass is not None else None, mass)
+        out = _window_fwd(Q, K, V, W, scale, tau, Bias, flags, None)
+        # the backward recomputes tau (and the tau mass) from the inputs
+        ctx.save_for_backward(Q, K, V, Bias)
         ctx.W, ctx.scale, ctx.flags = W, scale, flags
         ctx.return_tau = return_tau
         if return_tau:
@@ -118,7 +113,7 @@ class _CausalTensionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        Q, K, V, Bias, out, mass = ctx.saved_tensors
+        Q, K, V, Bias = ctx.saved_tensors
         B, T, H, D = Q.shape
         dOut = _rows(grads[0])
         dTau = _rows(grads[1]) if ctx.return_tau else None
@@ -131,8 +126,8 @@ class _CausalTensionFn(torch.autograd.Function):
         ws = _ws(lib.tension_window_bwd_workspace(B, T, H, _acc_code(Q, K, V), ctx.flags), Q.device)
         with torch.cuda.device(Q.device):
             L.check(lib.tension_window_bwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias), L.buf(out),
-                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.W,
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias),
+                L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.W,
                 float(ctx.scale), ctx.flags, _stream(Q)), "tension_window_bwd")
         return dQ, dK, dV, None, None, None, None, None
 
@@ -181,13 +176,12 @@ class _GlobalTensionFn(torch.autograd.Function):
             raise ValueError(f"global bias must be [B, T, T]=[{B}, {T}, {T}], got {tuple(Bias.shape)}")
         Wl = 0 if W_local is None else min(int(W_local), T)
         tl = torch.empty(B, T, H, Wl, dtype=Q.dtype, device=Q.device) if Wl > 0 else None
-        mass = torch.empty(B, T, H, dtype=_mass_dtype(Q, K, V), device=Q.device)
         out = torch.empty_like(Q)
         with torch.cuda.device(Q.device):
             L.check(L.lib().tension_global_fwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), L.buf(mass),
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), None,
                 B, T, H, D, Wl, float(scale), 0, _stream(Q)), "tension_global_fwd")
-        ctx.save_for_backward(Q, K, V, Bias, out, mass)
+        ctx.save_for_backward(Q, K, V, Bias)
         ctx.scale, ctx.Wl = scale, Wl
         if tl is not None:
             return out, tl
@@ -195,7 +189,7 @@ class _GlobalTensionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        Q, K, V, Bias, out, mass = ctx.saved_tensors
+        Q, K, V, Bias = ctx.saved_tensors
         B, T, H, D = Q.shape
         dOut = _rows(grads[0])
         if dOut is None:
@@ -206,8 +200,8 @@ class _GlobalTensionFn(torch.autograd.Function):
         ws = _ws(lib.tension_global_bwd_workspace(B, T, H, _acc_code(Q, K, V), 0), Q.device)
         with torch.cuda.device(Q.device):
             L.check(lib.tension_global_bwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias), L.buf(out),
-                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.Wl,
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias),
+                L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.Wl,
                 float(ctx.scale), 0, _stream(Q)), "tension_global_bwd")
         return dQ, dK, dV, None, None, None
 

@@ -79,7 +79,6 @@ typedef struct tension_buf {
  *   q,k,v,out: [B,T,H,D]; tau (nullable, out): [B,T,H,W], written fully
  *   (zeros on empty slots); bias (nullable): [B,T,W];
  *   mass (nullable, out): [B,T,H] = sum_w tau (unclamped), f32 or f64.
- *   Required when TENSION_NORM_MASS is set (the backward reads it).
  * ------------------------------------------------------------------------- */
 int tension_window_fwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* v, const tension_buf* out,
@@ -96,28 +95,31 @@ int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H,
  * Local window backward.  Replaces `_bwd_dq_kernel` + `_bwd_dkv_kernel`
  * (kernel.py:130-341) launched by `_CausalTensionFn.backward`
  * (ops.py:126-187).  Launches tension_window_bwd_dq then
- * tension_window_bwd_dkv on `stream`.
- *   dout: grad of out (or of raw msg when no NORM flag); dtau (nullable):
- *   grad of tau; bias: same as forward.  out/mass: the forward's outputs,
- *   required with TENSION_NORM_MASS.  dq/dk/dv written (not accumulated).
- *   workspace: tension_window_bwd_workspace() bytes, or NULL if that is 0.
+ * tension_window_bwd_dkv on `stream`.  Recomputes tau from q, k (and
+ * bias); nothing from the forward is needed besides the inputs.
+ *   dout: grad of out (of the raw msg without a NORM flag, of the
+ *   normalised output with one); dtau (nullable): grad of tau [B,T,H,W];
+ *   bias: as in the forward (sigma' is taken at the biased argument,
+ *   kernel.py:24-29; bias gets no gradient).  dq/dk/dv are written, not
+ *   accumulated, in their own dtypes.
+ *   workspace: tension_window_bwd_workspace() bytes (NULL if that is 0);
+ *   with TENSION_NORM_MASS it carries per-query coefficients from the dq
+ *   kernel to the dkv kernel.
  * ------------------------------------------------------------------------- */
 int tension_window_bwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* v, const tension_buf* dout,
                        const tension_buf* dtau, const tension_buf* bias,
-                       const tension_buf* out, const tension_buf* mass,
                        const tension_buf* dq, const tension_buf* dk,
                        const tension_buf* dv, void* workspace, int64_t B,
                        int64_t T, int64_t H, int64_t D, int64_t W,
                        double scale, int32_t flags, tension_stream_t stream);
 
-/* The two halves of tension_window_bwd, one kernel each (same arguments).
- * _dq also fills the per-query workspace that _dkv reads, so on one stream
- * _dq must precede _dkv.  Counterparts: kernel.py:130-227 / 232-341. */
+/* The two halves of tension_window_bwd, one kernel each.  _dq fills the
+ * workspace that _dkv reads, so on one stream _dq must precede _dkv.
+ * Counterparts: kernel.py:130-227 (dQ) and kernel.py:232-341 (dK/dV). */
 int tension_window_bwd_dq(const tension_buf* q, const tension_buf* k,
                           const tension_buf* v, const tension_buf* dout,
                           const tension_buf* dtau, const tension_buf* bias,
-                          const tension_buf* out, const tension_buf* mass,
                           const tension_buf* dq, void* workspace, int64_t B,
                           int64_t T, int64_t H, int64_t D, int64_t W,
                           double scale, int32_t flags, tension_stream_t stream);
@@ -135,7 +137,8 @@ int tension_window_bwd_dkv(const tension_buf* q, const tension_buf* k,
  * the reference has no kernel for it.
  *   bias (nullable): [B,T,T] indexed [b,t,s].
  *   tau_local (nullable, out): [B,T,H,Wl] with slot j = key s = T-1-j
- *   (model.py:231-237), zero where s > t.  mass (out, required): [B,T,H].
+ *   (model.py:231-237), zero where s > t.  mass (nullable, out): [B,T,H]
+ *   = sum_s tau (unclamped).
  * ------------------------------------------------------------------------- */
 int tension_global_fwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* v, const tension_buf* out,
@@ -147,12 +150,12 @@ int tension_global_fwd(const tension_buf* q, const tension_buf* k,
 int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H,
                                      int32_t dtype_acc, int32_t flags);
 
-/* Backward of tension_global_fwd: dout (grad of out), dtau_local (nullable,
- * grad of tau_local [B,T,H,Wl]), out/mass from the forward. */
+/* Backward of tension_global_fwd: dout (grad of out), dtau_local
+ * (nullable, grad of tau_local [B,T,H,Wl]); recomputes tau like the local
+ * backward.  workspace: tension_global_bwd_workspace() bytes (required). */
 int tension_global_bwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* v, const tension_buf* dout,
                        const tension_buf* dtau_local, const tension_buf* bias,
-                       const tension_buf* out, const tension_buf* mass,
                        const tension_buf* dq, const tension_buf* dk,
                        const tension_buf* dv, void* workspace, int64_t B,
                        int64_t T, int64_t H, int64_t D, int64_t Wl,
