@@ -11,12 +11,13 @@ backward (dQ, dK, dV) of one batch.
 
 Method: NSETS independent input sets (more than the 256 MB Infinity Cache
 in total) are generated on the GPU and rotated, so every step reads its
-inputs from HBM.  Each step (1 forward + 2 backward kernels, launched through
-the public autograd op) is captured once per input set in a HIP graph; the
-timed region replays K graphs between two events after a synchronize.  The
-dominant kernel is then timed alone the same way (graph of its launches on
-the same stream) for the roofline entry; ``rocprofv3 --kernel-trace --stats``
-of this command gives the per-kernel durations in profiles/.
+inputs from HBM.  The steps (1 forward + 2 backward kernels each, launched
+through the public autograd op) are captured in HIP graphs, NSETS steps per
+graph; the timed region runs exactly K steps between two events after a
+synchronize.  Each kernel is then timed alone the same way (graphs of its
+launches over the rotated sets, on the same stream) for the roofline entry;
+``rocprofv3 --kernel-trace --marker-trace --stats`` of this command, read
+back with ``--summarize``, gives the per-kernel durations in profiles/.
 
 The CPU baseline times the reference's CPU path (unfold gather + tau-mass +
 autograd, restated in oracle/torch_ref.py) in float32 on the host cores, on
@@ -78,32 +79,58 @@ def make_window_sets(n, B, T, H, D, dev, seed):
     return sets
 
 
-def capture(fn, warm=2):
+def capture(fns, warm=2):
+    """One HIP graph that runs fns[0](), fns[1](), ... in order (eager warm-up
+    on a side stream first, as graph capture requires)."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(warm):
-            fn()
+            for fn in fns:
+                fn()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for fn in fns:
+            fn()
     torch.cuda.synchronize()
     return g
 
 
-def time_graphs(graphs, steps, warmup):
-    for i in range(warmup):
-        graphs[i % len(graphs)].replay()
+class Runner:
+    """Replays units of work (one step, or one kernel launch) over the
+    rotated input sets.  `ring` runs one unit on each of the NSETS sets in a
+    single graph, so the hipGraphLaunch cost is paid once per NSETS units;
+    `singles[i]` runs the unit on set i alone (for counts that are not a
+    multiple of NSETS)."""
+
+    def __init__(self, fns, warm=2):
+        self.ring = capture(fns, warm)
+        self.singles = [capture([f], 0) for f in fns]
+        self.n = len(fns)
+
+    def run(self, units):
+        for _ in range(units // self.n):
+            self.ring.replay()
+        for i in range(units % self.n):
+            self.singles[i].replay()
+
+
+def time_units(runner, units, warmup, phase):
+    """ms per unit over exactly `units` units; the timed region runs inside a
+    roctx range named `phase` (rocprofv3 --marker-trace attributes the kernel
+    dispatches of the range to it)."""
+    runner.run(warmup)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.nvtx.range_push(phase)
     e0.record()
-    for i in range(steps):
-        graphs[i % len(graphs)].replay()
+    runner.run(units)
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps  # ms per replay
+    torch.cuda.nvtx.range_pop()
+    return e0.elapsed_time(e1) / units
 
 
 def window_step_fn(s, W, scale, normalize, return_tau=False):
@@ -206,9 +233,9 @@ def bench_window(args, dev):
     flops = (4 + 8) * D * P
     sets = make_window_sets(NSETS, B, T, H, D, dev, seed=1)
 
-    log(f"[bench] capturing {NSETS} step graphs (B{B} H{H} T{T} d{D} W{W} bf16, tau-mass)")
-    graphs = [capture(window_step_fn(s, W, scale, "mass")) for s in sets]
-    ms = time_graphs(graphs, args.steps, args.warmup)
+    log(f"[bench] capturing step graphs (B{B} H{H} T{T} d{D} W{W} bf16, tau-mass)")
+    steps = Runner([window_step_fn(s, W, scale, "mass") for s in sets])
+    ms = time_units(steps, args.steps, args.warmup, "step")
     log(f"[bench] fwd+bwd {ms * 1e3:.1f} us/step")
 
     # per-kernel durations (same stream, graph of one launch per set)
@@ -224,8 +251,9 @@ def bench_window(args, dev):
         if name == "dkv":  # its workspace must hold what dq wrote
             for f in kfns:
                 f["dq"]()
-        gs = [capture(f[name], warm=1) for f in kfns]
-        kms = time_graphs(gs, max(NSETS * 10, args.steps), NSETS)
+        kr = Runner([f[name] for f in kfns], warm=1)
+        kms = time_units(kr, max(NSETS * 10, args.steps), NSETS, f"kernel:{name}")
+        del kr
         per_kernel[name] = {"us": round(kms * 1e3, 2),
                             "alg_bytes": kbytes[name],
                             "GBps": round(kbytes[name] / (kms * 1e-3) / 1e9, 1)}
@@ -271,17 +299,116 @@ def bench_window(args, dev):
             result["roofline"]["traffic"] = tr.get("bytes_per_launch")
 
     # secondary variants: raw contract, and tau materialised + dTau (export path)
-    del graphs
-    raw_graphs = [capture(window_step_fn(s, W, scale, None)) for s in sets]
-    result["variants"] = {"raw_out_ms": round(time_graphs(raw_graphs, args.steps, args.warmup), 5)}
-    del raw_graphs
+    del steps
+    raw = Runner([window_step_fn(s, W, scale, None) for s in sets])
+    result["variants"] = {"raw_out_ms": round(time_units(raw, args.steps, args.warmup, "step:raw"), 5)}
+    del raw
     g = torch.Generator(device=dev).manual_seed(7)
     for s in sets:
         s["dTau"] = (torch.randn(B, T, H, W, device=dev, generator=g) * 0.1).to(torch.bfloat16)
-    tau_graphs = [capture(window_step_fn(s, W, scale, "mass", return_tau=True)) for s in sets]
-    result["variants"]["tau_materialised_ms"] = round(time_graphs(tau_graphs, args.steps, args.warmup), 5)
-    del tau_graphs
+    tau = Runner([window_step_fn(s, W, scale, "mass", return_tau=True) for s in sets])
+    result["variants"]["tau_materialised_ms"] = round(
+        time_units(tau, args.steps, args.warmup, "step:tau"), 5)
+    del tau
     return result
+
+
+def profile_kernels(n, dev):
+    """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
+    of each band kernel on rotated config-2 sets, then a plain device copy of
+    known size (256 MiB read + 256 MiB written) whose FETCH_SIZE/WRITE_SIZE
+    readings calibrate the counters into bytes."""
+    from bozo_amd import _lib as L
+    B, H, T, D, W = 8, 12, 1024, 64, 64
+    sets = make_window_sets(NSETS, B, T, H, D, dev, seed=1)
+    fns = [kernel_fns(s, W, math.sqrt(D), L.NORM_MASS) for s in sets]
+    for name in ("fwd", "dq", "dkv"):
+        for i in range(n):
+            fns[i % NSETS][0][name]()
+        torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] profile-kernels: {n} launches each of fwd/dq/dkv, 4 copies of 256 MiB")
+
+
+def _phase_regions(cur):
+    """(name, start, end) of the roctx ranges bench.py pushes, from a rocpd db."""
+    out = []
+    try:
+        rows = cur.execute("select e.extdata, r.start, r.end from rocpd_region r "
+                           "join rocpd_event e on e.id = r.event_id").fetchall()
+    except Exception:  # noqa: BLE001 - older/newer schema: fall back to one phase
+        return out
+    for ext, a, b in rows:
+        try:
+            msg = json.loads(ext or "{}").get("message", "")
+        except ValueError:
+            msg = ""
+        if msg.startswith("step") or msg.startswith("kernel:"):
+            out.append((msg, a, b))
+    return out
+
+
+def summarize(paths):
+    """Per-phase kernel statistics and calibrated HBM traffic from rocprofv3
+    rocpd databases (the *_results.db of --kernel-trace [--marker-trace] or
+    --pmc FETCH_SIZE / --pmc WRITE_SIZE runs of this script)."""
+    import glob
+    import sqlite3
+    import statistics
+    dbs = []
+    for path in paths:
+        dbs += [path] if path.endswith(".db") else sorted(glob.glob(os.path.join(path, "**", "*.db"),
+                                                                    recursive=True))
+    counters = {}  # counter -> kernel -> mean value per dispatch
+    for db in dbs:
+        cur = sqlite3.connect(db).cursor()
+        kern = cur.execute("select name, start, end from kernels").fetchall()
+        pmc = cur.execute("select name, counter_name, avg(counter_value), count(*) from pmc_events "
+                          "group by name, counter_name").fetchall()
+        if pmc:
+            for n, cn, v, cnt in pmc:
+                counters.setdefault(cn, {})[n.split("(")[0]] = (v, cnt)
+            continue
+        phases = _phase_regions(cur) or [("all", min(k[1] for k in kern), max(k[2] for k in kern))]
+        print(f"# kernel durations: {os.path.basename(os.path.dirname(db))}/{os.path.basename(db)}")
+        print("| phase | kernel | dispatches | mean us | median us | min us | max us |")
+        print("|---|---|---|---|---|---|---|")
+        for pname, a, b in phases:
+            by = {}
+            for n, s0, s1 in kern:
+                if s0 >= a and s1 <= b:
+                    by.setdefault(n.split("(")[0], []).append((s1 - s0) / 1e3)
+            tot = sum(sum(x) for x in by.values())
+            for n, d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+                if sum(d) < 0.01 * tot:
+                    continue
+                print(f"| {pname} | {n} | {len(d)} | {statistics.mean(d):.2f} | {statistics.median(d):.2f} "
+                      f"| {min(d):.2f} | {max(d):.2f} |")
+        print()
+    if counters:
+        print("# counters (KiB per dispatch for FETCH_SIZE / WRITE_SIZE)")
+        print("| kernel | counter | mean per dispatch | dispatches |")
+        print("|---|---|---|---|")
+        for cn, by in counters.items():
+            for n, (v, cnt) in by.items():
+                print(f"| {n[:70]} | {cn} | {v:.1f} | {cnt} |")
+        copy = "__amd_rocclr_copyBuffer"
+        fe, wr = counters.get("FETCH_SIZE", {}), counters.get("WRITE_SIZE", {})
+        if copy in fe and copy in wr:
+            known_kib = 256 * 1024  # the profile driver copies 256 MiB
+            sf, sw = known_kib / fe[copy][0], known_kib / wr[copy][0]
+            print(f"\ncopy-kernel calibration: FETCH_SIZE x{sf:.3f}, WRITE_SIZE x{sw:.3f}")
+            print("\n| kernel | HBM read MB | HBM write MB | total MB per launch |")
+            print("|---|---|---|---|")
+            for n in sorted(set(fe) & set(wr)):
+                if n == copy or "tension::" not in n:
+                    continue
+                r, w = fe[n][0] * sf * 1024 / 1e6, wr[n][0] * sw * 1024 / 1e6
+                print(f"| {n} | {r:.2f} | {w:.2f} | {r + w:.2f} |")
 
 
 def main():
@@ -291,7 +418,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
+                    help="only launch each band kernel N times (counter collection)")
+    ap.add_argument("--summarize", metavar="PATH", nargs="+",
+                    help="print per-phase kernel stats / calibrated traffic of rocprofv3 output "
+                         "dirs or .db files and exit")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(every box has one GPU); run with --gpus 1", file=sys.stderr)
@@ -301,6 +436,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.profile_kernels:
+        profile_kernels(args.profile_kernels, dev)
+        return
     result = bench_window(args, dev)
     if not args.no_cpu:
         log("[bench] CPU baseline ...")

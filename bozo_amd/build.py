@@ -23,7 +23,8 @@ LIBNAME = "libtension_hip.so"
 ARCH = os.environ.get("TENSION_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = [
-    "capi.hip", "exact.hip", "mfma.hip", "decode.hip",
+    "capi.hip", "exact.hip", "decode.hip",
+    "mfma.hip", "mfma_fwd.hip", "mfma_dq.hip", "mfma_dkv.hip",
     "exact_fwd_f32.hip", "exact_dq_f32.hip", "exact_dkv_f32.hip",
     "exact_fwd_f64.hip", "exact_dq_f64.hip", "exact_dkv_f64.hip",
 ]

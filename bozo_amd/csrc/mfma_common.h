@@ -1,0 +1,232 @@
+// Building blocks of the bf16 MFMA band kernels (gfx950, head dim 64).
+//
+// Work unit: a 64-row tile of one (b, h) pair, 256 threads = 4 wave64s.
+// Products use v_mfma_f32_16x16x32_bf16 (A 16x32, B 32x16, C 16x16 fp32).
+// Operand layout for lane l, g = l/16, c = l%16:
+//   A: row c,  k = 8g..8g+7        B: column c, k = 8g..8g+7
+//   C: rows 4g..4g+3, column c
+// A permutation of k applied to both A and B leaves the product unchanged;
+// the P.V-type products rely on that (see lds_tr8 / pack_b).
+#pragma once
+
+#include "band.h"
+
+namespace tension {
+
+constexpr int kTile = 64;
+constexpr int kThreads = 256;
+constexpr int kPitch = 72;  // row-major LDS tile: row pitch in bf16 (64 + 8 pad)
+constexpr int kTileElems = kTile * kPitch;
+constexpr int kTElems = kTile * kTile;  // transposed LDS tile: 64 x 64, unpadded
+
+// Transposed tiles hold element (d, r) -- feature d, tile row r -- in LDS row
+// d, with the 32-bit row pairs of each LDS row permuted by an XOR swizzle:
+// pair p = r/2 is stored at word (p ^ tr_swz(d)).  tr_swz is even, so the
+// four rows 4i..4i+3 read by one 8-byte A-operand load stay contiguous.
+// Bank analysis (4-byte banks): the tile stores write, per 32 lanes, pairs
+// p = pr (4 values) of rows d = 8ch + e (ch = 0..7): p ^ tr_swz(d) takes 32
+// distinct values; the A-operand loads read, per 16 lanes, rows d = 16m + c
+// (c = 0..15) at one p: p ^ tr_swz(d) = p ^ 2c ^ const spans all 32 banks
+// in 8-byte pairs.  Both are conflict-free (the unswizzled pitch-72 layout
+// put the 32 stores of an instruction into 8 banks).
+__device__ __forceinline__ int tr_swz(int d) { return (2 * (d & 15)) ^ (4 * ((d >> 4) & 3)); }
+
+enum { NORM_RAW = 0, NORM_MASS_ = 1, NORM_COUNT_ = 2 };
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 load8(const bf16* p) {
+  return __builtin_bit_cast(bf16x8, *(const u16x8*)p);
+}
+
+__device__ __forceinline__ bf16x8 lds8(const bf16* p) {
+  return __builtin_bit_cast(bf16x8, *(const u16x8*)p);
+}
+
+// A operand from a transposed LDS tile: LDS row `row` (a feature d), tile
+// rows {4g..4g+3} and {16+4g..16+4g+3} of the 32-row group starting at k0.
+__device__ __forceinline__ bf16x8 lds_tr8(const bf16* base, int row, int k0, int g) {
+  const int sw = tr_swz(row);
+  const int p0 = (k0 >> 1) + 2 * g;
+  const u16x4 lo = *(const u16x4*)(base + row * kTile + 2 * (p0 ^ sw));
+  const u16x4 hi = *(const u16x4*)(base + row * kTile + 2 * ((p0 + 8) ^ sw));
+  u16x8 r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// B operand from two 16-key groups of fp32 C-layout values.
+__device__ __forceinline__ bf16x8 pack_b(const float* lo4, const float* hi4) {
+  bf16x8 r;
+  r[0] = (bf16)lo4[0]; r[1] = (bf16)lo4[1]; r[2] = (bf16)lo4[2]; r[3] = (bf16)lo4[3];
+  r[4] = (bf16)hi4[0]; r[5] = (bf16)hi4[1]; r[6] = (bf16)hi4[2]; r[7] = (bf16)hi4[3];
+  return r;
+}
+
+// One 64-row tile of a [.., T, .., 64] bf16 tensor in flight from HBM to LDS.
+// Thread tid holds 16 bytes of rows r0+2p and r0+2p+1 (p = tid/8, d-chunk
+// tid%8): eight lanes cover one 128-byte row, so every global load
+// instruction is fully coalesced.  Rows outside [0, T) read as zero.
+struct TileRegs {
+  u16x8 a, b;
+};
+
+__device__ __forceinline__ TileRegs tile_load(const bf16* base, int64_t rs, int r0, int T, int tid) {
+  const int pr = tid >> 3, ch = tid & 7;
+  const int ra = r0 + 2 * pr, rb = ra + 1;
+  TileRegs x;
+  x.a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  x.b = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  if (ra >= 0 && ra < T) x.a = *(const u16x8*)(base + (int64_t)ra * rs + 8 * ch);
+  if (rb >= 0 && rb < T) x.b = *(const u16x8*)(base + (int64_t)rb * rs + 8 * ch);
+  return x;
+}
+
+__device__ __forceinline__ void tile_store_rows(const TileRegs& x, bf16* rm, int tid) {
+  const int pr = tid >> 3, ch = tid & 7;
+  *(u16x8*)(rm + (2 * pr) * kPitch + 8 * ch) = x.a;
+  *(u16x8*)(rm + (2 * pr + 1) * kPitch + 8 * ch) = x.b;
+}
+
+// Transposed, swizzled copy (see tr_swz): rows 2p and 2p+1 of feature d
+// packed into one 32-bit LDS word.
+__device__ __forceinline__ void tile_store_trans(const TileRegs& x, bf16* rt, int tid) {
+  const int pr = tid >> 3, ch = tid & 7;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int d = 8 * ch + e;
+    const uint32_t w = (uint32_t)x.a[e] | ((uint32_t)x.b[e] << 16);
+    *(uint32_t*)(rt + d * kTile + 2 * (pr ^ tr_swz(d))) = w;
+  }
+}
+
+__device__ __forceinline__ float wave_sum_g(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+struct TileId {
+  int b, h, tile;
+};
+
+__device__ __forceinline__ TileId tile_id(const BandParams& p, bool heavy_first) {
+  const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+  TileId r;
+  const int bh = id / p.ntiles;
+  int tile = id % p.ntiles;
+  if (heavy_first) tile = p.ntiles - 1 - tile;
+  r.b = bh / p.H;
+  r.h = bh % p.H;
+  r.tile = tile;
+  return r;
+}
+
+// sigma(x) for x = s * inv_scale + bias, with k2 = -log2(e) * inv_scale and
+// the bias pre-multiplied by -log2(e):  1 / (1 + 2^(s*k2 + bias2)).
+__device__ __forceinline__ float sigmoid_scaled(float s, float k2, float bias2) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(s, k2, bias2)));
+}
+
+// Per-query normalisation factor of the forward output.
+template <int NORM>
+__device__ __forceinline__ float out_factor(float msum, int t, int W) {
+  if (NORM == NORM_MASS_) return 1.f / (msum > kMassEps ? msum : kMassEps);
+  if (NORM == NORM_COUNT_) {
+    const int cnt = t < W ? t : W;
+    return 1.f / (float)(cnt > 1 ? cnt : 1);
+  }
+  return 1.f;
+}
+
+__device__ __forceinline__ void store_row4x4(bf16* row, const f32x4* acc, float f, int g) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    u16x4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+    *(u16x4*)(row + 16 * m + 4 * g) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS tiles (gfx950): 64 rows x 128 bytes, unpadded, filled by
+// global_load_lds (16 bytes per lane; lane L of a wave instruction lands at
+// LDS base + 16 L) and read either as rows (ds_read_b128) or transposed
+// (ds_read_b64_tr_b16).  The 16-byte chunk c of row r sits at chunk position
+// c ^ sw16(r); with sw16(r) = 2(r & 3) + ((r >> 2) & 1):
+//   * row reads (lane (g, c) -> row 16j + c, chunk 4kk + g): the 8 lanes of
+//     a 128-byte LDS cycle see sw16 = {0,2,4,6,1,3,5,7}: 8 distinct chunks;
+//   * transposed reads (lane (g, j) -> row 4g + j/4, 8 bytes at column
+//     16m + 4 (j & 3)): the 16 lanes touch rows with distinct (r & 3) and
+//     chunk pairs (2m, 2m+1) ^ sw16(r) that differ in bits 1..2: 8 distinct
+//     chunks.
+// Both are free of LDS bank conflicts.
+// ---------------------------------------------------------------------------
+
+constexpr int kDTile = kTile * kTile;  // bf16 elements of one direct tile
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int sw16(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// Asynchronously copy rows [r0, r0+64) of a [.., T, .., 64] bf16 tensor into
+// a direct tile.  Rows outside [0, T) are clamped into range: the kernels
+// mask every pair whose key or query lies outside the band, and the rows
+// they multiply by a zero weight are finite rows of the same tensor.  Each
+// wave issues two 1 KB instructions (rows 8(4n + wave) .. +7, n = 0, 1).
+__device__ __forceinline__ void tile_async(const bf16* base, int64_t rs, int r0, int T, bf16* tile,
+                                           int wave, int lane) {
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int q = (n * 4 + wave) * 64 + lane;  // 16-byte chunk slot in the tile
+    const int r = q >> 3;
+    const int c = (q & 7) ^ sw16(r);           // logical chunk stored in that slot
+    int gr = r0 + r;
+    gr = gr < 0 ? 0 : (gr > T - 1 ? T - 1 : gr);
+    __builtin_amdgcn_global_load_lds((const void*)(base + (int64_t)gr * rs + 8 * c),
+                                     (lds_void*)(tile + (n * 4 + wave) * 512), 16, 0, 0);
+  }
+}
+
+// Wait until at most n vector-memory operations of this wave are in flight
+// (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at
+// their maximum, i.e. not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Row read: 8 consecutive features of tile row `row` starting at logical
+// chunk `chunk` (A / B operand of a product that contracts over features).
+__device__ __forceinline__ bf16x8 dt_row8(const bf16* tile, int row, int chunk) {
+  return __builtin_bit_cast(bf16x8, *(const u16x8*)(tile + row * kTile + 8 * (chunk ^ sw16(row))));
+}
+
+// Transposed read: the A operand (16 features x 8 tile rows) of a product
+// that contracts over tile rows.  Lane (g, j) addresses row k0 + 4g + j/4
+// (and +16), features 16m + 4(j & 3) .. +3; ds_read_b64_tr_b16 hands lane
+// (g, c) the values of rows k0+4g .. k0+4g+3 (and +16) at feature 16m + c,
+// i.e. tile rows {4g..4g+3, 16+4g..16+4g+3} -- the pairing pack_b() uses.
+__device__ __forceinline__ bf16x8 dt_tr8(const bf16* tile, int m, int k0, int g, int j) {
+  const int col = 16 * m + 4 * (j & 3);
+  const int r1 = k0 + 4 * g + (j >> 2), r2 = r1 + 16;
+  const bf16* a1 = tile + r1 * kTile + 8 * ((col >> 3) ^ sw16(r1)) + (col & 4);
+  const bf16* a2 = tile + r2 * kTile + 8 * ((col >> 3) ^ sw16(r2)) + (col & 4);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a1);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a2);
+  u16x8 r;
+  r[0] = (unsigned short)lo[0]; r[1] = (unsigned short)lo[1];
+  r[2] = (unsigned short)lo[2]; r[3] = (unsigned short)lo[3];
+  r[4] = (unsigned short)hi[0]; r[5] = (unsigned short)hi[1];
+  r[6] = (unsigned short)hi[2]; r[7] = (unsigned short)hi[3];
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+}  // namespace tension
