@@ -411,6 +411,55 @@ def summarize(paths):
                 print(f"| {n} | {r:.2f} | {w:.2f} | {r + w:.2f} |")
 
 
+def bench_global(dev, steps, warmup):
+    """Config 3: global block B4 H12 T2048 d64 bf16, fwd+bwd (MFMA-bound)."""
+    from bozo_amd import global_tension
+    B, H, T, D = 4, 12, 2048, 64
+    g = torch.Generator(device=dev).manual_seed(2)
+    sets = []
+    for _ in range(2):
+        q, k, v = ((torch.randn(B, T, H, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+                   .requires_grad_(True) for _ in range(3))
+        sets.append(dict(Q=q, K=k, V=v, dO=torch.randn(B, T, H, D, device=dev, generator=g)
+                         .to(torch.bfloat16)))
+
+    def step_fn(s):
+        def fn():
+            out = global_tension(s["Q"], s["K"], s["V"], math.sqrt(D))
+            return torch.autograd.grad(out, (s["Q"], s["K"], s["V"]), s["dO"])
+        return fn
+    run = Runner([step_fn(s) for s in sets])
+    ms = time_units(run, steps, warmup, "global")
+    pairs = B * H * T * (T + 1) // 2
+    flops = 12 * D * pairs
+    return {"config": "global block B4 H12 T2048 d64 bf16 fwd+bwd (config 3)",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "alg_flops": flops, "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+            "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+
+def bench_decode(dev, reps):
+    """Config 4: streaming decode, 64 sequences x H16 x d64, W=256 bf16 ring
+    caches pre-filled with W tokens; 512 steps captured in one HIP graph."""
+    from bozo_amd import TensionDecodeCache
+    N, H, D, W, S = 64, 16, 64, 256, 512
+    g = torch.Generator(device=dev).manual_seed(3)
+    cache = TensionDecodeCache(N, H, D, W, dtype=torch.bfloat16, device=dev)
+    cache.k.copy_((torch.randn(N, H, W, D, device=dev, generator=g) * 0.5).to(torch.bfloat16))
+    cache.v.copy_((torch.randn(N, H, W, D, device=dev, generator=g) * 0.5).to(torch.bfloat16))
+    cache.pos[cache.cur].fill_(W)
+    q, k, v = ((torch.randn(S, N, H, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+               for _ in range(3))
+    run = Runner([lambda: [cache.step(q[i], k[i], v[i]) for i in range(S)]], warm=1)
+    ms = time_units(run, reps, 1, "decode") / S
+    step_bytes = 2 * N * H * W * D * 2 + 4 * N * H * D * 2
+    return {"config": "decode 64 seqs H16 d64 W256 bf16, 512 steps per graph (config 4)",
+            "us_per_step": round(ms * 1e3, 3), "steps_per_s": round(1e3 / ms, 1),
+            "alg_bytes_per_step": step_bytes,
+            "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -440,6 +489,13 @@ def main():
         profile_kernels(args.profile_kernels, dev)
         return
     result = bench_window(args, dev)
+    log("[bench] global block (config 3) ...")
+    others = [bench_global(dev, 20, 3)]
+    log(f"[bench] {others[-1]}")
+    log("[bench] decode (config 4) ...")
+    others.append(bench_decode(dev, 4))
+    log(f"[bench] {others[-1]}")
+    result["other_configs"] = others
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(1, 1024, 12, 64, 64, args.cpu_seconds)
