@@ -347,7 +347,7 @@ def _phase_regions(cur):
             msg = json.loads(ext or "{}").get("message", "")
         except ValueError:
             msg = ""
-        if msg.startswith("step") or msg.startswith("kernel:"):
+        if msg.startswith(("step", "kernel:", "global", "decode")):
             out.append((msg, a, b))
     return out
 

@@ -29,6 +29,7 @@ struct BandParams {
   double scale;
   int flags;
   int ntiles;     // 64-row tiles per (b,h) (MFMA kernels)
+  int chunk;      // consecutive tiles per workgroup (MFMA ring kernels)
 };
 
 __device__ __forceinline__ bool band_valid(const BandParams& p, int t, int s) {

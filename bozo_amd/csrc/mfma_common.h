@@ -230,3 +230,45 @@ __device__ __forceinline__ bf16x8 dt_tr8(const bf16* tile, int m, int k0, int g,
 }
 
 }  // namespace tension
+
+namespace tension {
+
+// ---------------------------------------------------------------------------
+// Wave-level band geometry.  A wave owns 16 query rows [qa, qb] of a tile;
+// the union of their bands is [ulo, uhi] and the intersection [ilo, ihi].
+// A 16-key sub-block outside the union is skipped outright, one inside the
+// intersection needs no per-element mask, and only the sub-blocks crossing
+// a band edge are masked (W = 64: per wave 5 of the 8 sub-blocks of the
+// tile's two key blocks are computed, 2 of them masked).  All of it is
+// wave-uniform (scalar branches).
+// ---------------------------------------------------------------------------
+struct WaveBand {
+  int ulo, uhi, ilo, ihi;
+};
+
+__device__ __forceinline__ WaveBand wave_band(const BandParams& p, int qa) {
+  WaveBand w;
+  int qb = qa + 15;
+  if (qb > p.T - 1) qb = p.T - 1;
+  if (qb < qa) {  // every row of this wave is past the sequence end
+    w.ulo = 1;
+    w.uhi = 0;
+    w.ilo = 1;
+    w.ihi = 0;
+    return w;
+  }
+  w.ulo = qa - p.win > 0 ? qa - p.win : 0;
+  w.uhi = qb - 1 + p.diag;
+  w.ilo = qb - p.win > 0 ? qb - p.win : 0;
+  w.ihi = qa - 1 + p.diag;
+  return w;
+}
+
+// 0: skip, 1: masked, 2: fully inside the band of every row of the wave
+__device__ __forceinline__ int sub_kind(const WaveBand& w, int k0) {
+  if (k0 + 15 < w.ulo || k0 > w.uhi) return 0;
+  if (k0 >= w.ilo && k0 + 15 <= w.ihi) return 2;
+  return 1;
+}
+
+}  // namespace tension

@@ -1,21 +1,169 @@
 // bf16 MFMA band forward (local window and global block), head dim 64.
 //
-// One workgroup per 64-query tile; the four waves split the queries (16
-// each).  For every 64-key block of the tile's band:
+// The four waves of a workgroup split a 64-query tile (16 queries each).
+// For every 64-key block of the tile's band:
 //   S^T = K Q^T   (A = K rows read from LDS, B = this wave's Q fragment)
 //   P   = sigma(S/scale + bias) on the band, 0 elsewhere      (fp32)
 //   O^T += V^T P^T (A = V^T read transposed from the row-major V tile,
 //                   B = P^T packed straight from the C layout of S^T)
 // S^T leaves lane (g, c) holding keys 16j+4g+r of query c, which is already
 // the B-operand layout of the P.V product once two 16-key groups are packed,
-// so no shuffle of P is needed.
+// so no shuffle of P is needed.  16-key sub-blocks outside the wave's band
+// are skipped (see WaveBand).
 //
-// K/V blocks stream HBM -> LDS with global_load_lds into a two-deep ring of
-// tiles: the blocks n and n+1 are in flight while block n-1 is computed,
-// and no register or LDS-store instruction touches the stream.
+// Two kernels share that block routine:
+//   mfma_fwd_ring (local windows W <= 64): a workgroup owns `chunk`
+//     consecutive query tiles of one (b,h).  Tile t needs key blocks t-1
+//     and t; a three-slot ring of LDS tiles holds them while block t+1
+//     streams in (global_load_lds), so each K/V block is fetched once per
+//     chunk and its HBM latency overlaps the previous tile's arithmetic.
+//     The slots are distinct LDS arrays selected at compile time, which lets
+//     the compiler see that reads of one slot do not wait on the DMA into
+//     another.
+//   mfma_fwd (any band, including the global block): one tile per workgroup,
+//     key blocks streamed through a two-deep ring.
 #include "mfma_common.h"
 
 namespace tension {
+
+template <bool BIAS, bool TAU>
+__device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, const bf16* Vs, int kb0,
+                                          const WaveBand& wb, int lo, int hi, int b, int h, int tq,
+                                          int g, int c, const bf16x8* qf, float k2, f32x4* acc,
+                                          float& msum) {
+  float pr[4][4];
+  int kind[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    kind[j] = sub_kind(wb, kb0 + 16 * j);
+    if (kind[j] == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pr[j][r] = 0.f;
+      continue;
+    }
+    f32x4 s = {};
+    s = mfma(dt_row8(Ks, 16 * j + c, g), qf[0], s);
+    s = mfma(dt_row8(Ks, 16 * j + c, 4 + g), qf[1], s);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = kb0 + 16 * j + 4 * g + r;
+      // kind 2 covers every valid row of the wave; rows past T (hi < lo)
+      // stay masked so no tau store or bias load leaves the tensors
+      const bool ok = (kind[j] == 2 && hi >= lo) || (key >= lo && key <= hi);
+      float b2 = 0.f;
+      if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+      const float pv = ok ? sigmoid_scaled(s[r], k2, b2) : 0.f;
+      if (TAU && ok) {
+        const int col = tau_col(p, tq, key);
+        if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), pv);
+      }
+      msum += pv;
+      pr[j][r] = pv;
+    }
+  }
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    if (kind[2 * kk] == 0 && kind[2 * kk + 1] == 0) continue;
+    const bf16x8 pb = pack_b(pr[2 * kk], pr[2 * kk + 1]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Vs, m, 32 * kk, g, c), pb, acc[m]);
+  }
+}
+
+template <int NORM, bool TAU>
+__device__ __forceinline__ void fwd_epilogue(const BandParams& p, int b, int h, int tq, int g,
+                                             const f32x4* acc, float msum) {
+  msum = wave_sum_g(msum);
+  if (tq >= p.T) return;
+  bf16* orow = (bf16*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
+  store_row4x4(orow, acc, out_factor<NORM>(msum, tq, p.W), g);
+  if (p.mass.p && g == 0)
+    st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, msum);
+  if (TAU) {
+    const int e = tau_empty_bound(p, tq);
+    for (int col = g; col < e; col += 4) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), 0.f);
+  }
+}
+
+__device__ __forceinline__ void load_qfrag(const bf16* qb_, int64_t rs, int tq, int T, int g, bf16x8* qf) {
+  const int tr = tq < T ? tq : T - 1;
+  qf[0] = load8(qb_ + (int64_t)tr * rs + 8 * g);
+  qf[1] = load8(qb_ + (int64_t)tr * rs + 32 + 8 * g);
+}
+
+// ------------------------------------------------------------------ ring kernel (W <= 64)
+
+template <int NORM, bool BIAS, bool TAU>
+__global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 K0[kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 K1[kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 K2[kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 V0[kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 V1[kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 V2[kDTile];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, c = lane & 15;
+  const int nch = (p.ntiles + p.chunk - 1) / p.chunk;
+  const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+  const int bh = id / nch;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int t_first = (id % nch) * p.chunk;
+  const int t_end = t_first + p.chunk < p.ntiles ? t_first + p.chunk : p.ntiles;
+
+  const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const float k2 = -kLog2e * (float)(1.0 / p.scale);
+
+  // key block gb (rows 64 gb ..) into a slot pair
+  auto fetch = [&](int gb, bf16* Kd, bf16* Vd) {
+    if (gb >= 0 && gb < p.ntiles) {
+      tile_async(kb_, p.k.s1, gb * kTile, T, Kd, wave, lane);
+      tile_async(vb_, p.v.s1, gb * kTile, T, Vd, wave, lane);
+    }
+  };
+
+  bf16x8 qf[2], qn[2];
+  load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
+  fetch(t_first - 1, K0, V0);
+  fetch(t_first, K1, V1);
+
+  // tile t = t_first + lt uses key blocks t-1 (slot lt % 3) and t (slot
+  // (lt+1) % 3); block t+1 goes to slot (lt+2) % 3, freed by tile t-1.
+  auto tile_step = [&](int lt, const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb,
+                       bf16* Kn, bf16* Vn) -> bool {
+    const int t = t_first + lt;
+    if (t >= t_end) return false;
+    wait_vm<0>();
+    __syncthreads();
+    const bool more = t + 1 < t_end;
+    if (more) {
+      load_qfrag(qb_, p.q.s1, (t + 1) * kTile + wave * 16 + c, T, g, qn);
+      fetch(t + 1, Kn, Vn);
+    }
+    const int t0 = t * kTile;
+    const int tq = t0 + wave * 16 + c;
+    const int lo = tq - p.win > 0 ? tq - p.win : 0;
+    const int hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
+    const WaveBand wb = wave_band(p, t0 + wave * 16);
+    if (tq >= T) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; }
+    f32x4 acc[4] = {};
+    float msum = 0.f;
+    if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
+    fwd_block<BIAS, TAU>(p, Kb, Vb, t0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
+    fwd_epilogue<NORM, TAU>(p, b, h, tq, g, acc, msum);
+    if (more) { qf[0] = qn[0]; qf[1] = qn[1]; }
+    return true;
+  };
+
+  for (int lt = 0;; lt += 3) {
+    if (!tile_step(lt, K0, V0, K1, V1, K2, V2)) break;
+    if (!tile_step(lt + 1, K1, V1, K2, V2, K0, V0)) break;
+    if (!tile_step(lt + 2, K2, V2, K0, V0, K1, V1)) break;
+  }
+}
+
+// ------------------------------------------------------------------ streaming kernel
 
 template <int NORM, bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads) void mfma_fwd(BandParams p) {
@@ -27,10 +175,9 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd(BandParams p) {
   const int b = id.b, h = id.h, T = p.T;
   const int t0 = id.tile * kTile;
   const int tq = t0 + wave * 16 + c;
-  const bool qok = tq < T;
-  // keys of this lane's query: [lo, hi] (empty for rows past T)
   const int lo = tq - p.win > 0 ? tq - p.win : 0;
-  const int hi = qok ? tq - 1 + p.diag : -1;
+  const int hi = tq < T ? tq - 1 + p.diag : -1;
+  const WaveBand wb = wave_band(p, t0 + wave * 16);
 
   const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
@@ -44,96 +191,59 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd(BandParams p) {
   const int nblk = s_hi < kb_first ? 0 : (s_hi - kb_first) / kTile + 1;
 
   bf16x8 qf[2];
-  {
-    const int tr = qok ? tq : T - 1;
-    qf[0] = load8(qb_ + (int64_t)tr * p.q.s1 + 8 * g);
-    qf[1] = load8(qb_ + (int64_t)tr * p.q.s1 + 32 + 8 * g);
-  }
-  // each block is 4 load instructions per wave (2 for K, 2 for V)
+  load_qfrag(qb_, p.q.s1, tq, T, g, qf);
   tile_async(kb_, p.k.s1, kb_first, T, Kb[0], wave, lane);
   tile_async(vb_, p.v.s1, kb_first, T, Vb[0], wave, lane);
   if (nblk > 1) {
     tile_async(kb_, p.k.s1, kb_first + kTile, T, Kb[1], wave, lane);
     tile_async(vb_, p.v.s1, kb_first + kTile, T, Vb[1], wave, lane);
   }
-  if (!qok) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; }
-
-  const float inv_scale = (float)(1.0 / p.scale);
-  const float k2 = -kLog2e * inv_scale;
+  if (tq >= T) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; }
+  const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 acc[4] = {};
   float msum = 0.f;
-
   for (int blk = 0; blk < nblk; ++blk) {
     const int kb0 = kb_first + blk * kTile;
-    const bf16* Ks = Kb[blk & 1];
-    const bf16* Vs = Vb[blk & 1];
     if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
     __syncthreads();
-    float pr[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f32x4 s = {};
-      s = mfma(dt_row8(Ks, 16 * j + c, g), qf[0], s);
-      s = mfma(dt_row8(Ks, 16 * j + c, 4 + g), qf[1], s);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb0 + 16 * j + 4 * g + r;
-        const bool ok = key >= lo && key <= hi;
-        float b2 = 0.f;
-        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
-        const float pv = ok ? sigmoid_scaled(s[r], k2, b2) : 0.f;
-        if (TAU && ok) {
-          const int col = tau_col(p, tq, key);
-          if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), pv);
-        }
-        msum += pv;
-        pr[j][r] = pv;
-      }
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 pb = pack_b(pr[2 * kk], pr[2 * kk + 1]);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Vs, m, 32 * kk, g, c), pb, acc[m]);
-    }
+    fwd_block<BIAS, TAU>(p, Kb[blk & 1], Vb[blk & 1], kb0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
     if (blk + 2 < nblk) {
       __syncthreads();  // every wave is done with this ring slot
       tile_async(kb_, p.k.s1, kb0 + 2 * kTile, T, Kb[blk & 1], wave, lane);
       tile_async(vb_, p.v.s1, kb0 + 2 * kTile, T, Vb[blk & 1], wave, lane);
     }
   }
-  msum = wave_sum_g(msum);
-  if (!qok) return;
-  bf16* orow = (bf16*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
-  store_row4x4(orow, acc, out_factor<NORM>(msum, tq, p.W), g);
-  if (p.mass.p && g == 0)
-    st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, msum);
-  if (TAU) {
-    const int e = tau_empty_bound(p, tq);
-    for (int col = g; col < e; col += 4) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), 0.f);
+  fwd_epilogue<NORM, TAU>(p, b, h, tq, g, acc, msum);
+}
+
+// ------------------------------------------------------------------ launch
+
+template <int NORM, bool BIAS, bool TAU>
+static void go(const BandParams& p, hipStream_t st, unsigned nwg, bool ring) {
+  if (ring) {
+    const unsigned n = (unsigned)((int64_t)p.B * p.H * ((p.ntiles + p.chunk - 1) / p.chunk));
+    hipLaunchKernelGGL((mfma_fwd_ring<NORM, BIAS, TAU>), dim3(n), dim3(kThreads), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((mfma_fwd<NORM, BIAS, TAU>), dim3(nwg), dim3(kThreads), 0, st, p);
   }
 }
 
-template <int NORM, bool BIAS, bool TAU>
-static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
-  hipLaunchKernelGGL((mfma_fwd<NORM, BIAS, TAU>), dim3(nwg), dim3(kThreads), 0, st, p);
-}
-
 template <int NORM>
-static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, bool tau) {
+static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, bool tau, bool ring) {
   if (bias) {
-    if (tau) go<NORM, true, true>(p, st, nwg); else go<NORM, true, false>(p, st, nwg);
+    if (tau) go<NORM, true, true>(p, st, nwg, ring); else go<NORM, true, false>(p, st, nwg, ring);
   } else {
-    if (tau) go<NORM, false, true>(p, st, nwg); else go<NORM, false, false>(p, st, nwg);
+    if (tau) go<NORM, false, true>(p, st, nwg, ring); else go<NORM, false, false>(p, st, nwg, ring);
   }
 }
 
 void launch_mfma_fwd(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
   const bool bias = p.bias.p != nullptr, tau = p.tau.p != nullptr;
+  const bool ring = !p.glob && p.win <= kTile && p.chunk > 0;
   switch (norm) {
-    case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, tau); break;
-    case NORM_COUNT_: go_n<NORM_COUNT_>(p, st, nwg, bias, tau); break;
-    default: go_n<NORM_RAW>(p, st, nwg, bias, tau); break;
+    case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, tau, ring); break;
+    case NORM_COUNT_: go_n<NORM_COUNT_>(p, st, nwg, bias, tau, ring); break;
+    default: go_n<NORM_RAW>(p, st, nwg, bias, tau, ring); break;
   }
 }
 
