@@ -295,8 +295,7 @@ def bench_window(args, dev):
     if os.path.exists(tfile):
         with open(tfile) as f:
             tr = json.load(f)
-        if tr.get("kernel") == result["roofline"]["kernel"]:
-            result["roofline"]["traffic"] = tr.get("bytes_per_launch")
+        result["roofline"]["traffic"] = tr.get("bytes_per_launch", {}).get(result["roofline"]["kernel"])
 
     # secondary variants: raw contract, and tau materialised + dTau (export path)
     del steps
