@@ -11,8 +11,8 @@ backward (dQ, dK, dV) of one batch.
 
 Method: NSETS independent input sets (more than the 256 MB Infinity Cache
 in total) are generated on the GPU and rotated, so every step reads its
-inputs from HBM.  The steps (1 forward + 2 backward kernels each, launched
-through the public autograd op) are captured in HIP graphs, NSETS steps per
+inputs from HBM.  The steps (1 forward + 1 fused backward kernel each,
+launched through the public autograd op) are captured in HIP graphs, NSETS steps per
 graph; the timed region runs exactly K steps between two events after a
 synchronize.  Each kernel is then timed alone the same way (graphs of its
 launches over the rotated sets, on the same stream) for the roofline entry;
@@ -147,8 +147,10 @@ def window_step_fn(s, W, scale, normalize, return_tau=False):
 
 
 def kernel_fns(s, W, scale, flags):
-    """One launch of each of the three kernels on set s, through the C ABI
-    entry points that launch exactly one kernel each."""
+    """One launch of each band kernel on set s, through C ABI entry points
+    that launch exactly one kernel each: the forward, the fused backward
+    (tension_window_bwd for W <= 64), and the split backward's dQ and dK/dV
+    kernels (used for wider windows and the global block)."""
     from bozo_amd import _lib as L
     B, T, H, D = s["Q"].shape
     Q, K, V, dO = (s[n].detach() for n in ("Q", "K", "V", "dO"))
@@ -172,7 +174,11 @@ def kernel_fns(s, W, scale, flags):
     def dkvf():
         L.check(lib.tension_window_bwd_dkv(bq, bk, bv, bdo, None, None, bdk, bdv, ws.data_ptr(),
                                            B, T, H, D, W, scale, flags, L.stream_handle()), "dkv")
-    return {"fwd": fwd, "dq": dqf, "dkv": dkvf}, keep
+
+    def bwdf():
+        L.check(lib.tension_window_bwd(bq, bk, bv, bdo, None, None, bdq, bdk, bdv, ws.data_ptr(),
+                                       B, T, H, D, W, scale, flags, L.stream_handle()), "bwd")
+    return {"fwd": fwd, "bwd": bwdf, "dq": dqf, "dkv": dkvf}, keep
 
 
 def kernel_bytes(B, T, H, D, W, el=2):
@@ -182,6 +188,7 @@ def kernel_bytes(B, T, H, D, W, el=2):
     vec = B * T * H * 4                # one [B,T,H] fp32 tensor
     return {
         "fwd": 3 * act + act,                    # Q,K,V -> out
+        "bwd": 4 * act + 3 * act,                # Q,K,V,dO -> dQ,dK,dV (fused)
         "dq": 4 * act + act + 2 * vec,           # Q,K,V,dO -> dQ, ws(a,c)
         "dkv": 4 * act + 2 * vec + 2 * act,      # Q,K,V,dO,ws -> dK,dV
     }
@@ -247,7 +254,7 @@ def bench_window(args, dev):
         keep.append(kp)
     kbytes = kernel_bytes(B, T, H, D, W)
     per_kernel = {}
-    for name in ("fwd", "dq", "dkv"):
+    for name in ("fwd", "bwd", "dq", "dkv"):
         if name == "dkv":  # its workspace must hold what dq wrote
             for f in kfns:
                 f["dq"]()
@@ -258,11 +265,14 @@ def bench_window(args, dev):
                             "alg_bytes": kbytes[name],
                             "GBps": round(kbytes[name] / (kms * 1e-3) / 1e9, 1)}
         log(f"[bench] kernel {name}: {kms * 1e3:.2f} us, {per_kernel[name]['GBps']} GB/s algorithmic")
-    dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
+    # the step runs fwd + fused bwd; dq/dkv are the split backward, reported
+    # for comparison only
+    dom = max(("fwd", "bwd"), key=lambda k: per_kernel[k]["us"])
     d = per_kernel[dom]
+    kname = {"fwd": "mfma_fwd", "bwd": "mfma_bwd_fused", "dq": "mfma_bwd_dq", "dkv": "mfma_bwd_dkv"}
 
     # compulsory HBM bytes of one fwd+bwd: read Q,K,V, write out; read Q,K,V,dO,
-    # write dQ,dK,dV (the a/c workspace is produced and consumed inside bwd)
+    # write dQ,dK,dV
     step_bytes = 11 * B * T * H * D * 2
     result = {
         "metric": METRIC,
@@ -280,7 +290,7 @@ def bench_window(args, dev):
         "config": {"workload": "windowed sigmoid-tension fwd+bwd, tau-mass normalised (config 2)",
                    "B": B, "H": H, "T": T, "head_dim": D, "window": W, "global_batch": B,
                    "seq_len": T, "parallelism": "none (1 GPU)", "input_sets_rotated": NSETS},
-        "roofline": {"bound": "hbm", "kernel": f"mfma_bwd_{dom}" if dom != "fwd" else "mfma_fwd",
+        "roofline": {"bound": "hbm", "kernel": kname[dom],
                      "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["GBps"] / HBM_PEAK_GBS, 4), "traffic": None},
         "step": {"alg_bytes": step_bytes,
@@ -321,7 +331,7 @@ def profile_kernels(n, dev):
     B, H, T, D, W = 8, 12, 1024, 64, 64
     sets = make_window_sets(NSETS, B, T, H, D, dev, seed=1)
     fns = [kernel_fns(s, W, math.sqrt(D), L.NORM_MASS) for s in sets]
-    for name in ("fwd", "dq", "dkv"):
+    for name in ("fwd", "bwd", "dq", "dkv"):
         for i in range(n):
             fns[i % NSETS][0][name]()
         torch.cuda.synchronize()
@@ -330,7 +340,7 @@ def profile_kernels(n, dev):
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"[bench] profile-kernels: {n} launches each of fwd/dq/dkv, 4 copies of 256 MiB")
+    log(f"[bench] profile-kernels: {n} launches each of fwd/bwd/dq/dkv, 4 copies of 256 MiB")
 
 
 def _phase_regions(cur):

@@ -286,6 +286,22 @@ int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension
                        const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H,
                        int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
   const Shape sh{B, T, H, D};
+  if (W >= 1 && W <= 64) {
+    // one fused kernel (no workspace traffic) when the MFMA path applies
+    bool empty = false;
+    TRY(check_bwd(q, k, v, dout, dtau, bias, sh, W, scale, flags, ws, false, &empty));
+    if (empty) return ok();
+    TRY(check_buf(dq, "dq", true, 3));
+    TRY(check_buf(dk, "dk", true, 3));
+    TRY(check_buf(dv, "dv", true, 3));
+    if (mfma_ok_bwd(q, k, v, dout, bias, dq, dk, sh.D, flags) && aligned_bf16_rows(dv)) {
+      BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, W, scale, flags, false);
+      p.dq = make_buf(dq);
+      p.dk = make_buf(dk);
+      p.dv = make_buf(dv);
+      return run_band(3, true, false, p, stream, "tension_window_bwd");
+    }
+  }
   TRY(band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, sh, W, scale, flags, stream, false));
   return band_bwd_dkv(q, k, v, dout, dtau, bias, dk, dv, ws, sh, W, scale, flags, stream, false);
 }

@@ -7,6 +7,13 @@ namespace tension {
 void launch_mfma_fwd(const BandParams& p, hipStream_t st, unsigned nwg, int norm);
 void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm);
 void launch_mfma_dkv(const BandParams& p, hipStream_t st, unsigned nwg, int norm);
+void launch_mfma_bwd_fused(const BandParams& p, hipStream_t st, unsigned nwg, int norm);
+
+// Workgroups the fused backward aims for: two resident per CU (256 CUs;
+// 68 KB of LDS each).
+#ifndef TENSION_BWD_WG_TARGET
+#define TENSION_BWD_WG_TARGET 512
+#endif
 
 int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* err) {
   BandParams p = p_in;
@@ -21,6 +28,18 @@ int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* e
   const int norm = (p.flags & TENSION_NORM_MASS)    ? NORM_MASS_
                    : (p.flags & TENSION_NORM_COUNT) ? NORM_COUNT_
                                                     : NORM_RAW;
+  if (phase == 3) {
+    // fused backward (local window <= 64): p.chunk = runs of tiles per (b,h)
+    const int64_t bh = (int64_t)p.B * p.H;
+    int64_t runs = (TENSION_BWD_WG_TARGET + bh / 2) / bh;
+    if (runs < 1) runs = 1;
+    if (runs > p.ntiles) runs = p.ntiles;
+    if (bh * runs > 0x7fffffff) return -1;
+    p.chunk = (int)runs;
+    launch_mfma_bwd_fused(p, st, (unsigned)(bh * runs), norm);
+    *err = hipGetLastError();
+    return 0;
+  }
   switch (phase) {
     case 0: launch_mfma_fwd(p, st, (unsigned)nwg, norm); break;
     case 1: launch_mfma_dq(p, st, (unsigned)nwg, norm); break;

@@ -1,0 +1,358 @@
+// bf16 MFMA band backward in one kernel (local windows W <= 64, head dim 64):
+// dQ, dK and dV from a single pass over Q, K, V and dO, without atomics.
+//
+// A workgroup owns a run [tA, tB) of consecutive 64-row tiles of one (b, h):
+// it writes dQ of query tiles tA..tB-1 and dK/dV of key blocks tA..tB-1.
+// With W <= 64, query tile t sees key blocks t-1 and t, and key block k is
+// seen by query tiles k and k+1, so step t (t = tA .. tB-1) completes dQ of
+// tile t and dK/dV of block t-1; one extra "halo" step over query tile tB
+// completes block tB-1 (the halo's dQ belongs to the next run and is not
+// written).
+//
+// Step t, with K/V blocks t-1, t and the Q/dO tile t in LDS:
+//   phase 1 (query-centric; wave w owns queries 16w..16w+15 of the tile):
+//     S^T = K Q^T, dP^T = V dO^T over the 80-key band of its 16 queries
+//     (five 16-key groups), P = sigma(S/scale + bias), the normalisation
+//     coefficients a_t, c_t of those queries (in-wave: no workspace),
+//     G = (a dP - c + dTau) P (1 - P),  dQ^T += K^T G^T  (registers),
+//     and P' = a P, G into the exchange tiles X (bf16).
+//   phase 2 (key-centric; wave w owns keys 16w..16w+15 of block t-1 and of
+//     block t):  dV^T += dO^T P',  dK^T += Q^T G, with P' and G read back
+//     transposed (ds_read_b64_tr_b16) from X and dO^T, Q^T from the tiles.
+//     Block t-1 is complete after this phase and is written out.
+// The next step's K/V block, Q/dO tile and Q/dO fragments are loaded into
+// registers at the start of a step and stored to LDS behind the barriers.
+//
+// Exchange layout: for query group j and band slot sl (key group j + sl of
+// the 128 keys of blocks t-1, t), a [16 query][16 key] bf16 sub-tile with a
+// 32-byte row.  Phase-1 stores (lane (g,c): query c, keys 4g..4g+3) and
+// phase-2 transposed reads (16 lanes: 4 rows x 16 keys) each touch 512
+// contiguous bytes per wave instruction.
+#include "mfma_common.h"
+
+namespace tension {
+
+constexpr int kXSlots = 5;                    // 16-key groups in the band of 16 queries (W <= 64)
+constexpr int kXSub = 16 * 16;                // bf16 elements of one sub-tile
+constexpr int kXElems = 4 * kXSlots * kXSub;  // one exchange tensor (4 query groups)
+
+__device__ __forceinline__ void x_put(bf16* X, int j, int sl, int g, int c, const float* v4) {
+  u16x4 o;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)v4[r]);
+  *(u16x4*)(X + (j * kXSlots + sl) * kXSub + c * 16 + 4 * g) = o;
+}
+
+// B operand of a product contracting over the 32 queries of groups j0, j0+1:
+// lane (g, c) gets key c of the sub-tiles, queries {4g..4g+3} of group j0
+// and of group j0+1 (the tile-row order dt_tr8 gives the A operand).  An
+// absent sub-tile (no slot of that query group covers the key group) reads
+// as zeros.
+__device__ __forceinline__ bf16x8 x_pair(const bf16* X, int j0, int sl0, bool ok0, int sl1, bool ok1, int g,
+                                         int l16) {
+  const int off = (4 * g + (l16 >> 2)) * 16 + 4 * (l16 & 3);
+  s16x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+  if (ok0) lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + (j0 * kXSlots + sl0) * kXSub + off));
+  if (ok1)
+    hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + ((j0 + 1) * kXSlots + sl1) * kXSub + off));
+  u16x8 r;
+  r[0] = (unsigned short)lo[0]; r[1] = (unsigned short)lo[1];
+  r[2] = (unsigned short)lo[2]; r[3] = (unsigned short)lo[3];
+  r[4] = (unsigned short)hi[0]; r[5] = (unsigned short)hi[1];
+  r[6] = (unsigned short)hi[2]; r[7] = (unsigned short)hi[3];
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+template <int NORM, bool BIAS, bool DTAU>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_bwd_fused(BandParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 Kt[2][kDTile];  // key block k in slot k & 1
+  __shared__ __attribute__((aligned(16))) bf16 Vt[2][kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 Qt[kDTile];     // query tile of the step
+  __shared__ __attribute__((aligned(16))) bf16 Ot[kDTile];     // dO tile of the step
+  __shared__ __attribute__((aligned(16))) bf16 XP[kXElems];    // P' = a P
+  __shared__ __attribute__((aligned(16))) bf16 XG[kXElems];    // G
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index is uniform across the wave; readfirstlane lets the
+  // compiler see that, so every branch on it is a scalar branch
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int nch = p.chunk;  // runs per (b, h)
+  const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+  const int bh = id / nch, run = id % nch;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int tA = (int)((int64_t)run * p.ntiles / nch);
+  const int tB = (int)((int64_t)(run + 1) * p.ntiles / nch);
+  const int tE = tB < p.ntiles ? tB : tB - 1;  // last step (the halo when tB < ntiles)
+
+  const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const bf16* ob_ = (const bf16*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  const float inv_scale = (float)(1.0 / p.scale);
+  const float k2 = -kLog2e * inv_scale;
+
+  // ---- prologue: blocks tA-1 (if any) and tA, tile tA
+  {
+    TileRegs k0 = tile_load(kb_, p.k.s1, tA * kTile, T, tid);
+    TileRegs v0 = tile_load(vb_, p.v.s1, tA * kTile, T, tid);
+    TileRegs q0 = tile_load(qb_, p.q.s1, tA * kTile, T, tid);
+    TileRegs o0 = tile_load(ob_, p.dout.s1, tA * kTile, T, tid);
+    if (tA >= 1) {
+      TileRegs km = tile_load(kb_, p.k.s1, (tA - 1) * kTile, T, tid);
+      TileRegs vm = tile_load(vb_, p.v.s1, (tA - 1) * kTile, T, tid);
+      tile_store_direct(km, Kt[(tA - 1) & 1], tid);
+      tile_store_direct(vm, Vt[(tA - 1) & 1], tid);
+    }
+    tile_store_direct(k0, Kt[tA & 1], tid);
+    tile_store_direct(v0, Vt[tA & 1], tid);
+    tile_store_direct(q0, Qt, tid);
+    tile_store_direct(o0, Ot, tid);
+  }
+  bf16x8 qf[2], gf[2];
+  {
+    const int tq = tA * kTile + 16 * w + c;
+    const int tr = tq < T ? tq : T - 1;
+    qf[0] = load8(qb_ + (int64_t)tr * p.q.s1 + 8 * g);
+    qf[1] = load8(qb_ + (int64_t)tr * p.q.s1 + 32 + 8 * g);
+    gf[0] = load8(ob_ + (int64_t)tr * p.dout.s1 + 8 * g);
+    gf[1] = load8(ob_ + (int64_t)tr * p.dout.s1 + 32 + 8 * g);
+    if (tq >= T) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; gf[0] = bf16x8{}; gf[1] = bf16x8{}; }
+  }
+  __syncthreads();
+
+  // dK/dV of block t-1 (key group w), carried from step t-1 to step t
+  f32x4 dk_old[4] = {}, dv_old[4] = {};
+
+  for (int t = tA; t <= tE; ++t) {
+    const bool halo = t >= tB;
+    const bool more = t < tE;
+    // ---- prefetch of step t+1 into registers
+    TileRegs kn, vn, qn, on;
+    bf16x8 qfn[2], gfn[2];
+    if (more) {
+      const int r0 = (t + 1) * kTile;
+      kn = tile_load(kb_, p.k.s1, r0, T, tid);
+      vn = tile_load(vb_, p.v.s1, r0, T, tid);
+      qn = tile_load(qb_, p.q.s1, r0, T, tid);
+      on = tile_load(ob_, p.dout.s1, r0, T, tid);
+      const int tq = r0 + 16 * w + c;
+      const int tr = tq < T ? tq : T - 1;
+      qfn[0] = load8(qb_ + (int64_t)tr * p.q.s1 + 8 * g);
+      qfn[1] = load8(qb_ + (int64_t)tr * p.q.s1 + 32 + 8 * g);
+      gfn[0] = load8(ob_ + (int64_t)tr * p.dout.s1 + 8 * g);
+      gfn[1] = load8(ob_ + (int64_t)tr * p.dout.s1 + 32 + 8 * g);
+      if (tq >= T) { qfn[0] = bf16x8{}; qfn[1] = bf16x8{}; gfn[0] = bf16x8{}; gfn[1] = bf16x8{}; }
+    }
+
+    // ---- phase 1: queries 16w..16w+15 of tile t
+    const bf16* Kold = Kt[(t + 1) & 1];  // block t-1
+    const bf16* Vold = Vt[(t + 1) & 1];
+    const bf16* Knew = Kt[t & 1];        // block t
+    const bf16* Vnew = Vt[t & 1];
+    const int tq = t * kTile + 16 * w + c;
+    const int lo = tq - p.win > 0 ? tq - p.win : 0;
+    const int hi = tq < T ? tq - 1 : -1;
+    const WaveBand wb = wave_band(p, t * kTile + 16 * w);
+    float pv[kXSlots][4];
+    f32x4 dpv[kXSlots];
+    int kind[kXSlots];
+    float msum = 0.f, dsum = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < kXSlots; ++sl) {
+      const int gg = w + sl;  // key group among the 8 of blocks t-1, t
+      const int blk = gg >> 2, j = gg & 3;
+      const int kb0 = (t - 1 + blk) * kTile + 16 * j;
+      kind[sl] = sub_kind(wb, kb0);
+      // the halo's new-block keys only feed its (unwritten) dQ; with tau-mass
+      // normalisation they still enter the coefficients
+      if (halo && blk == 1 && NORM != NORM_MASS_) kind[sl] = 0;
+      if (kind[sl] == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pv[sl][r] = 0.f;
+        dpv[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
+        continue;
+      }
+      const bf16* Ks = blk ? Knew : Kold;
+      const bf16* Vs = blk ? Vnew : Vold;
+      f32x4 s = {}, d = {};
+      s = mfma(dt_row8(Ks, 16 * j + c, g), qf[0], s);
+      s = mfma(dt_row8(Ks, 16 * j + c, 4 + g), qf[1], s);
+      d = mfma(dt_row8(Vs, 16 * j + c, g), gf[0], d);
+      d = mfma(dt_row8(Vs, 16 * j + c, 4 + g), gf[1], d);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 4 * g + r;
+        const bool ok = (kind[sl] == 2 && hi >= lo) || (key >= lo && key <= hi);
+        float b2 = 0.f;
+        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+        const float x = ok ? sigmoid_scaled(s[r], k2, b2) : 0.f;
+        pv[sl][r] = x;
+        if (NORM == NORM_MASS_) {
+          msum += x;
+          dsum += x * d[r];
+        }
+      }
+      dpv[sl] = d;
+    }
+    float ca = 1.f, cc = 0.f;
+    if (NORM == NORM_MASS_) {
+      msum = wave_sum_g(msum);
+      dsum = wave_sum_g(dsum);
+      const float m = msum > kMassEps ? msum : kMassEps;
+      ca = 1.f / m;
+      cc = msum >= kMassEps ? dsum * ca * ca : 0.f;
+    } else if (NORM == NORM_COUNT_) {
+      const int cnt = tq < p.W ? tq : p.W;
+      ca = 1.f / (float)(cnt > 1 ? cnt : 1);
+    }
+    // G overwrites dP in place (dpv), P' = a P overwrites P (pv)
+#pragma unroll
+    for (int sl = 0; sl < kXSlots; ++sl) {
+      const int gg = w + sl;
+      const int kb0 = (t - 1 + (gg >> 2)) * kTile + 16 * (gg & 3);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 4 * g + r;
+        const bool ok = kind[sl] != 0 && ((kind[sl] == 2 && hi >= lo) || (key >= lo && key <= hi));
+        float dt = dpv[sl][r] * ca - cc;
+        if (DTAU && ok) dt += ld<float>(p.dtau, tau_off(p.dtau, b, tq, h, key - tq + p.W));
+        const float x = pv[sl][r];
+        dpv[sl][r] = ok ? dt * x * (1.f - x) : 0.f;
+        pv[sl][r] = x * ca;
+      }
+      const float gd4[4] = {dpv[sl][0], dpv[sl][1], dpv[sl][2], dpv[sl][3]};
+      x_put(XP, w, sl, g, c, pv[sl]);
+      x_put(XG, w, sl, g, c, gd4);
+    }
+    if (!halo) {
+      // dQ^T += K^T G^T over 32-key pairs (key groups 2i, 2i+1); slot sl is
+      // key group w + sl, so the pairing depends on the parity of w
+      f32x4 acc[4] = {};
+      auto dq_pair = [&](int i, const f32x4& lo4, const f32x4& hi4) {
+        const bf16* Ks = (i >> 1) ? Knew : Kold;
+        const float l[4] = {lo4[0], lo4[1], lo4[2], lo4[3]};
+        const float u[4] = {hi4[0], hi4[1], hi4[2], hi4[3]};
+        const bf16x8 pb = pack_b(l, u);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Ks, m, 32 * (i & 1), g, c), pb, acc[m]);
+      };
+      const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
+      if ((w & 1) == 0) {
+        if (kind[0] | kind[1]) dq_pair(w >> 1, dpv[0], dpv[1]);
+        if (kind[2] | kind[3]) dq_pair((w >> 1) + 1, dpv[2], dpv[3]);
+        if (kind[4]) dq_pair((w >> 1) + 2, dpv[4], zz);
+      } else {
+        if (kind[0]) dq_pair(w >> 1, zz, dpv[0]);
+        if (kind[1] | kind[2]) dq_pair((w >> 1) + 1, dpv[1], dpv[2]);
+        if (kind[3] | kind[4]) dq_pair((w >> 1) + 2, dpv[3], dpv[4]);
+      }
+      if (tq < T) {
+        bf16* drow = (bf16*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2;
+        store_row4x4(drow, acc, inv_scale, g);
+      }
+    }
+    __syncthreads();  // X written; every wave is done with block t-1
+
+    if (more) {  // block t+1 replaces block t-1
+      tile_store_direct(kn, Kt[(t + 1) & 1], tid);
+      tile_store_direct(vn, Vt[(t + 1) & 1], tid);
+    }
+
+    // ---- phase 2: keys 16w..16w+15 of block t-1 (key group w) and of
+    // block t (key group 4+w).  Query group j covers key groups j..j+4.
+    const bool own_old = t >= 1 && t - 1 >= tA;
+    const bool own_new = !halo;
+    f32x4 dk_new[4] = {}, dv_new[4] = {};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int j0 = 2 * kk;
+      const bool need_old = own_old && j0 <= w;
+      const bool need_new = own_new && j0 + 1 >= w;
+      if (!need_old && !need_new) continue;
+      bf16x8 aq[4], ao[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        aq[m] = dt_tr8(Qt, m, 32 * kk, g, c);
+        ao[m] = dt_tr8(Ot, m, 32 * kk, g, c);
+      }
+      if (need_old) {
+        const bf16x8 bp = x_pair(XP, j0, w - j0, true, w - j0 - 1, w >= j0 + 1, g, c);
+        const bf16x8 bg = x_pair(XG, j0, w - j0, true, w - j0 - 1, w >= j0 + 1, g, c);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          dv_old[m] = mfma(ao[m], bp, dv_old[m]);
+          dk_old[m] = mfma(aq[m], bg, dk_old[m]);
+        }
+      }
+      if (need_new) {
+        const bf16x8 bp = x_pair(XP, j0, 4 + w - j0, j0 >= w, 3 + w - j0, true, g, c);
+        const bf16x8 bg = x_pair(XG, j0, 4 + w - j0, j0 >= w, 3 + w - j0, true, g, c);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          dv_new[m] = mfma(ao[m], bp, dv_new[m]);
+          dk_new[m] = mfma(aq[m], bg, dk_new[m]);
+        }
+      }
+    }
+    if (own_old) {
+      const int tk = (t - 1) * kTile + 16 * w + c;
+      if (tk < T) {
+        bf16* dkrow = (bf16*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2;
+        bf16* dvrow = (bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2;
+        store_row4x4(dkrow, dk_old, inv_scale, g);
+        store_row4x4(dvrow, dv_old, 1.f, g);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      dk_old[m] = dk_new[m];
+      dv_old[m] = dv_new[m];
+    }
+    __syncthreads();  // phase 2 is done with X and the Q/dO tiles
+
+    if (more) {
+      tile_store_direct(qn, Qt, tid);
+      tile_store_direct(on, Ot, tid);
+      qf[0] = qfn[0]; qf[1] = qfn[1];
+      gf[0] = gfn[0]; gf[1] = gfn[1];
+    }
+  }
+  // the last block of the sequence has no halo step: it is complete after
+  // its own step (no query tile follows it)
+  if (tE == tB - 1) {
+    const int t = tB;  // block tB-1 plays "old" of a step that does not exist
+    const int tk = (t - 1) * kTile + 16 * w + c;
+    if (tk < T) {
+      bf16* dkrow = (bf16*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2;
+      bf16* dvrow = (bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2;
+      store_row4x4(dkrow, dk_old, inv_scale, g);
+      store_row4x4(dvrow, dv_old, 1.f, g);
+    }
+  }
+}
+
+template <int NORM, bool BIAS, bool DTAU>
+static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
+  hipLaunchKernelGGL((mfma_bwd_fused<NORM, BIAS, DTAU>), dim3(nwg), dim3(kThreads), 0, st, p);
+}
+
+template <int NORM>
+static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, bool dtau) {
+  if (bias) {
+    if (dtau) go<NORM, true, true>(p, st, nwg); else go<NORM, true, false>(p, st, nwg);
+  } else {
+    if (dtau) go<NORM, false, true>(p, st, nwg); else go<NORM, false, false>(p, st, nwg);
+  }
+}
+
+// p.chunk = runs per (b, h); grid = B * H * p.chunk
+void launch_mfma_bwd_fused(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
+  const bool bias = p.bias.p != nullptr, dtau = p.dtau.p != nullptr;
+  switch (norm) {
+    case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, dtau); break;
+    case NORM_COUNT_: go_n<NORM_COUNT_>(p, st, nwg, bias, dtau); break;
+    default: go_n<NORM_RAW>(p, st, nwg, bias, dtau); break;
+  }
+}
+
+}  // namespace tension

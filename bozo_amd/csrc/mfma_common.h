@@ -203,6 +203,16 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Register-staged rows (tile_load) into a direct tile: thread tid writes the
+// 16-byte chunk ch of rows 2p and 2p+1 at chunk position ch ^ sw16(row).
+// Eight lanes fill one 128-byte row, a wave 1 KB of consecutive rows.
+__device__ __forceinline__ void tile_store_direct(const TileRegs& x, bf16* tile, int tid) {
+  const int pr = tid >> 3, ch = tid & 7;
+  const int ra = 2 * pr, rb = ra + 1;
+  *(u16x8*)(tile + ra * kTile + 8 * (ch ^ sw16(ra))) = x.a;
+  *(u16x8*)(tile + rb * kTile + 8 * (ch ^ sw16(rb))) = x.b;
+}
+
 // Row read: 8 consecutive features of tile row `row` starting at logical
 // chunk `chunk` (A / B operand of a product that contracts over features).
 __device__ __forceinline__ bf16x8 dt_row8(const bf16* tile, int row, int chunk) {

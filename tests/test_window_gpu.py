@@ -318,3 +318,24 @@ def test_errors(dev):
         causal_tension(Q, Q, Q, 4, 4.0, bias=torch.zeros(1, 8, 5, device=dev))
     with pytest.raises(ValueError):
         causal_tension(Q, Q, Q, 0, 4.0)
+
+
+# ------------------------------------------------------------ fused backward runs
+
+@pytest.mark.parametrize("B,H,T,W", [
+    (1, 1, 1024, 64),   # 16 runs of one tile per (b,h): a halo step in every run
+    (2, 48, 400, 64),   # 5 runs of 1-2 tiles, ragged last tile
+    (64, 17, 65, 33),   # one run per (b,h) (no halo), W < 64
+    (3, 2, 333, 17),
+])
+@pytest.mark.parametrize("normalize", [None, "mass", "count"])
+def test_fused_backward_runs_bf16(dev, B, H, T, W, normalize):
+    """The bf16 backward for W <= 64 is one kernel that splits every (b,h)
+    sequence into runs of tiles and recomputes the tile after each run; the
+    grid size, and so the run length, depends on B*H."""
+    inp = make_inputs(B, T, H, 64, seed=B * 1000 + T + W, std=0.5, dtype=torch.bfloat16,
+                      bias_std=0.5, bias_shape=(B, T, W))
+    use_bias = normalize == "mass"
+    hip = hip_run(inp, W, 8.0, dev, normalize=normalize, use_bias=use_bias)
+    ref = oracle_run(inp, W, 8.0, normalize=normalize, use_bias=use_bias)
+    compare(hip, ref, torch.bfloat16, False)
