@@ -161,21 +161,28 @@ def kernel_fns(s, W, scale, flags):
     lib = L.lib()
     bq, bk, bv, bo, bdo = (L.buf(t) for t in (Q, K, V, out, dO))
     bdq, bdk, bdv = L.buf(dq), L.buf(dk), L.buf(dv)
-    keep = (out, dq, dk, dv, ws)
+    # the ctypes buffers hold raw pointers only: every closure references
+    # `keep`, so the tensors live as long as any launcher does (graph
+    # capture empties torch's cache, which would unmap freed outputs)
+    keep = (Q, K, V, dO, out, dq, dk, dv, ws)
 
     def fwd():
+        _ = keep  # holds the tensors behind the raw pointers
         L.check(lib.tension_window_fwd(bq, bk, bv, bo, None, None, None, B, T, H, D, W, scale, flags,
                                        L.stream_handle()), "fwd")
 
     def dqf():
+        _ = keep  # holds the tensors behind the raw pointers
         L.check(lib.tension_window_bwd_dq(bq, bk, bv, bdo, None, None, bdq, ws.data_ptr(),
                                           B, T, H, D, W, scale, flags, L.stream_handle()), "dq")
 
     def dkvf():
+        _ = keep  # holds the tensors behind the raw pointers
         L.check(lib.tension_window_bwd_dkv(bq, bk, bv, bdo, None, None, bdk, bdv, ws.data_ptr(),
                                            B, T, H, D, W, scale, flags, L.stream_handle()), "dkv")
 
     def bwdf():
+        _ = keep  # holds the tensors behind the raw pointers
         L.check(lib.tension_window_bwd(bq, bk, bv, bdo, None, None, bdq, bdk, bdv, ws.data_ptr(),
                                        B, T, H, D, W, scale, flags, L.stream_handle()), "bwd")
     return {"fwd": fwd, "bwd": bwdf, "dq": dqf, "dkv": dkvf}, keep

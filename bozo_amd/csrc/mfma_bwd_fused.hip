@@ -63,8 +63,14 @@ __device__ __forceinline__ bf16x8 x_pair(const bf16* X, int j0, int sl0, bool ok
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// Two waves per SIMD (two workgroups per CU): registers capped at 256.
+#ifndef TENSION_BWD_WAVES_PER_EU
+#define TENSION_BWD_WAVES_PER_EU 2
+#endif
+
 template <int NORM, bool BIAS, bool DTAU>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_bwd_fused(BandParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_BWD_WAVES_PER_EU, TENSION_BWD_WAVES_PER_EU)))
+void mfma_bwd_fused(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Kt[2][kDTile];  // key block k in slot k & 1
   __shared__ __attribute__((aligned(16))) bf16 Vt[2][kDTile];
   __shared__ __attribute__((aligned(16))) bf16 Qt[kDTile];     // query tile of the step
