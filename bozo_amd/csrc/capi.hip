@@ -56,6 +56,12 @@ int check_buf(const tension_buf* b, const char* what, bool required, int unit) {
 
 bool is_f64(const tension_buf* b) { return b && b->dtype == TENSION_F64; }
 
+// Kernels that address one (b, h) sequence through a 32-bit buffer view need
+// every row offset up to T + 128 rows to fit in 32 bits.
+bool rows_fit_u32(const tension_buf* b, int64_t T) {
+  return b && b->s[1] > 0 && (T + 128) * b->s[1] * 2 < ((int64_t)1 << 32);
+}
+
 bool any_f64(const tension_buf* a, const tension_buf* b, const tension_buf* c) {
   return is_f64(a) || is_f64(b) || is_f64(c);
 }
@@ -294,7 +300,9 @@ int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension
     TRY(check_buf(dq, "dq", true, 3));
     TRY(check_buf(dk, "dk", true, 3));
     TRY(check_buf(dv, "dv", true, 3));
-    if (mfma_ok_bwd(q, k, v, dout, bias, dq, dk, sh.D, flags) && aligned_bf16_rows(dv)) {
+    bool fit = true;
+    for (const tension_buf* t : {q, k, v, dout, dq, dk, dv}) fit = fit && rows_fit_u32(t, sh.T);
+    if (fit && mfma_ok_bwd(q, k, v, dout, bias, dq, dk, sh.D, flags) && aligned_bf16_rows(dv)) {
       BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, W, scale, flags, false);
       p.dq = make_buf(dq);
       p.dk = make_buf(dk);

@@ -90,22 +90,30 @@ void mfma_bwd_fused(BandParams p) {
   const int tB = (int)((int64_t)(run + 1) * p.ntiles / nch);
   const int tE = tB < p.ntiles ? tB : tB - 1;  // last step (the halo when tB < ntiles)
 
-  const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
-  const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
-  const bf16* ob_ = (const bf16*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  // per-sequence buffer views: rows >= T load as zeros, stores past T drop
+  const SeqBuf sq = seq_view(p.q, b, h, T), sk = seq_view(p.k, b, h, T);
+  const SeqBuf sv = seq_view(p.v, b, h, T), so = seq_view(p.dout, b, h, T);
+  const SeqBuf sdq = seq_view(p.dq, b, h, T), sdk = seq_view(p.dk, b, h, T);
+  const SeqBuf sdv = seq_view(p.dv, b, h, T);
+  // thread tid moves 16 bytes (chunk tid % 8) of tile rows 2p, 2p+1 (p = tid / 8)
+  const uint32_t lq = (uint32_t)(2 * (tid >> 3)) * sq.rs2 + 16 * (tid & 7);
+  const uint32_t lk = (uint32_t)(2 * (tid >> 3)) * sk.rs2 + 16 * (tid & 7);
+  const uint32_t lv = (uint32_t)(2 * (tid >> 3)) * sv.rs2 + 16 * (tid & 7);
+  const uint32_t lo_ = (uint32_t)(2 * (tid >> 3)) * so.rs2 + 16 * (tid & 7);
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
 
   // ---- prologue: blocks tA-1 (if any) and tA, tile tA
   {
-    TileRegs k0 = tile_load(kb_, p.k.s1, tA * kTile, T, tid);
-    TileRegs v0 = tile_load(vb_, p.v.s1, tA * kTile, T, tid);
-    TileRegs q0 = tile_load(qb_, p.q.s1, tA * kTile, T, tid);
-    TileRegs o0 = tile_load(ob_, p.dout.s1, tA * kTile, T, tid);
+    const uint32_t r0 = (uint32_t)(tA * kTile);
+    TileRegs k0 = seq_tile_load(sk, r0 * sk.rs2, lk);
+    TileRegs v0 = seq_tile_load(sv, r0 * sv.rs2, lv);
+    TileRegs q0 = seq_tile_load(sq, r0 * sq.rs2, lq);
+    TileRegs o0 = seq_tile_load(so, r0 * so.rs2, lo_);
     if (tA >= 1) {
-      TileRegs km = tile_load(kb_, p.k.s1, (tA - 1) * kTile, T, tid);
-      TileRegs vm = tile_load(vb_, p.v.s1, (tA - 1) * kTile, T, tid);
+      const uint32_t rm = r0 - kTile;
+      TileRegs km = seq_tile_load(sk, rm * sk.rs2, lk);
+      TileRegs vm = seq_tile_load(sv, rm * sv.rs2, lv);
       tile_store_direct(km, Kt[(tA - 1) & 1], tid);
       tile_store_direct(vm, Vt[(tA - 1) & 1], tid);
     }
@@ -114,17 +122,13 @@ void mfma_bwd_fused(BandParams p) {
     tile_store_direct(q0, Qt, tid);
     tile_store_direct(o0, Ot, tid);
   }
-  bf16x8 qf[2], gf[2];
-  {
-    const int tq = tA * kTile + 16 * w + c;
-    const int tr = tq < T ? tq : T - 1;
-    qf[0] = load8(qb_ + (int64_t)tr * p.q.s1 + 8 * g);
-    qf[1] = load8(qb_ + (int64_t)tr * p.q.s1 + 32 + 8 * g);
-    gf[0] = load8(ob_ + (int64_t)tr * p.dout.s1 + 8 * g);
-    gf[1] = load8(ob_ + (int64_t)tr * p.dout.s1 + 32 + 8 * g);
-    if (tq >= T) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; gf[0] = bf16x8{}; gf[1] = bf16x8{}; }
-  }
   __syncthreads();
+  // this wave's Q/dO fragments (query 16w + c, features 8g.., 32+8g..)
+  bf16x8 qf[2], gf[2];
+  qf[0] = dt_row8(Qt, 16 * w + c, g);
+  qf[1] = dt_row8(Qt, 16 * w + c, 4 + g);
+  gf[0] = dt_row8(Ot, 16 * w + c, g);
+  gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
 
   // dK/dV of block t-1 (key group w), carried from step t-1 to step t
   f32x4 dk_old[4] = {}, dv_old[4] = {};
@@ -134,20 +138,12 @@ void mfma_bwd_fused(BandParams p) {
     const bool more = t < tE;
     // ---- prefetch of step t+1 into registers
     TileRegs kn, vn, qn, on;
-    bf16x8 qfn[2], gfn[2];
     if (more) {
-      const int r0 = (t + 1) * kTile;
-      kn = tile_load(kb_, p.k.s1, r0, T, tid);
-      vn = tile_load(vb_, p.v.s1, r0, T, tid);
-      qn = tile_load(qb_, p.q.s1, r0, T, tid);
-      on = tile_load(ob_, p.dout.s1, r0, T, tid);
-      const int tq = r0 + 16 * w + c;
-      const int tr = tq < T ? tq : T - 1;
-      qfn[0] = load8(qb_ + (int64_t)tr * p.q.s1 + 8 * g);
-      qfn[1] = load8(qb_ + (int64_t)tr * p.q.s1 + 32 + 8 * g);
-      gfn[0] = load8(ob_ + (int64_t)tr * p.dout.s1 + 8 * g);
-      gfn[1] = load8(ob_ + (int64_t)tr * p.dout.s1 + 32 + 8 * g);
-      if (tq >= T) { qfn[0] = bf16x8{}; qfn[1] = bf16x8{}; gfn[0] = bf16x8{}; gfn[1] = bf16x8{}; }
+      const uint32_t r0 = (uint32_t)((t + 1) * kTile);
+      kn = seq_tile_load(sk, r0 * sk.rs2, lk);
+      vn = seq_tile_load(sv, r0 * sv.rs2, lv);
+      qn = seq_tile_load(sq, r0 * sq.rs2, lq);
+      on = seq_tile_load(so, r0 * so.rs2, lo_);
     }
 
     // ---- phase 1: queries 16w..16w+15 of tile t
@@ -158,6 +154,7 @@ void mfma_bwd_fused(BandParams p) {
     const int tq = t * kTile + 16 * w + c;
     const int lo = tq - p.win > 0 ? tq - p.win : 0;
     const int hi = tq < T ? tq - 1 : -1;
+    const bool rowok = hi >= lo;  // the query has at least one key
     const WaveBand wb = wave_band(p, t * kTile + 16 * w);
     float pv[kXSlots][4];
     f32x4 dpv[kXSlots];
@@ -185,13 +182,17 @@ void mfma_bwd_fused(BandParams p) {
       s = mfma(dt_row8(Ks, 16 * j + c, 4 + g), qf[1], s);
       d = mfma(dt_row8(Vs, 16 * j + c, g), gf[0], d);
       d = mfma(dt_row8(Vs, 16 * j + c, 4 + g), gf[1], d);
+      const bool full = kind[sl] == 2;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 4 * g + r;
-        const bool ok = (kind[sl] == 2 && hi >= lo) || (key >= lo && key <= hi);
+        const bool ok = full ? rowok : ((key >= lo) & (key <= hi));
         float b2 = 0.f;
         if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
-        const float x = ok ? sigmoid_scaled(s[r], k2, b2) : 0.f;
+        // computed on every lane (finite inputs) and selected: a conditional
+        // sigmoid becomes a branch per element
+        const float sg = sigmoid_scaled(s[r], k2, b2);
+        const float x = ok ? sg : 0.f;
         pv[sl][r] = x;
         if (NORM == NORM_MASS_) {
           msum += x;
@@ -219,7 +220,7 @@ void mfma_bwd_fused(BandParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 4 * g + r;
-        const bool ok = kind[sl] != 0 && ((kind[sl] == 2 && hi >= lo) || (key >= lo && key <= hi));
+        const bool ok = kind[sl] != 0 && (kind[sl] == 2 ? rowok : ((key >= lo) & (key <= hi)));
         float dt = dpv[sl][r] * ca - cc;
         if (DTAU && ok) dt += ld<float>(p.dtau, tau_off(p.dtau, b, tq, h, key - tq + p.W));
         const float x = pv[sl][r];
@@ -252,10 +253,7 @@ void mfma_bwd_fused(BandParams p) {
         if (kind[1] | kind[2]) dq_pair((w >> 1) + 1, dpv[1], dpv[2]);
         if (kind[3] | kind[4]) dq_pair((w >> 1) + 2, dpv[3], dpv[4]);
       }
-      if (tq < T) {
-        bf16* drow = (bf16*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2;
-        store_row4x4(drow, acc, inv_scale, g);
-      }
+      seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
     }
     __syncthreads();  // X written; every wave is done with block t-1
 
@@ -301,13 +299,9 @@ void mfma_bwd_fused(BandParams p) {
       }
     }
     if (own_old) {
-      const int tk = (t - 1) * kTile + 16 * w + c;
-      if (tk < T) {
-        bf16* dkrow = (bf16*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2;
-        bf16* dvrow = (bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2;
-        store_row4x4(dkrow, dk_old, inv_scale, g);
-        store_row4x4(dvrow, dv_old, 1.f, g);
-      }
+      const uint32_t tk = (uint32_t)((t - 1) * kTile + 16 * w + c);
+      seq_store_row4x4(sdk, tk * sdk.rs2, dk_old, inv_scale, g);
+      seq_store_row4x4(sdv, tk * sdv.rs2, dv_old, 1.f, g);
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -317,23 +311,23 @@ void mfma_bwd_fused(BandParams p) {
     __syncthreads();  // phase 2 is done with X and the Q/dO tiles
 
     if (more) {
+      // each wave stores exactly its own 16 rows (16w..16w+15) of the next
+      // Q/dO tile, so it reads its fragments back without a barrier (LDS
+      // accesses of one wave complete in order)
       tile_store_direct(qn, Qt, tid);
       tile_store_direct(on, Ot, tid);
-      qf[0] = qfn[0]; qf[1] = qfn[1];
-      gf[0] = gfn[0]; gf[1] = gfn[1];
+      qf[0] = dt_row8(Qt, 16 * w + c, g);
+      qf[1] = dt_row8(Qt, 16 * w + c, 4 + g);
+      gf[0] = dt_row8(Ot, 16 * w + c, g);
+      gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
     }
   }
   // the last block of the sequence has no halo step: it is complete after
   // its own step (no query tile follows it)
   if (tE == tB - 1) {
-    const int t = tB;  // block tB-1 plays "old" of a step that does not exist
-    const int tk = (t - 1) * kTile + 16 * w + c;
-    if (tk < T) {
-      bf16* dkrow = (bf16*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2;
-      bf16* dvrow = (bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2;
-      store_row4x4(dkrow, dk_old, inv_scale, g);
-      store_row4x4(dvrow, dv_old, 1.f, g);
-    }
+    const uint32_t tk = (uint32_t)((tB - 1) * kTile + 16 * w + c);
+    seq_store_row4x4(sdk, tk * sdk.rs2, dk_old, inv_scale, g);
+    seq_store_row4x4(sdv, tk * sdv.rs2, dv_old, 1.f, g);
   }
 }
 

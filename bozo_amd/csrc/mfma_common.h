@@ -203,6 +203,58 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// ---------------------------------------------------------------------------
+// Buffer views of one (b, h) sequence: a raw buffer resource whose range ends
+// at the last byte of row T-1, so loads of rows >= T return zeros and stores
+// to them are dropped by the hardware range check (no branches, 32-bit
+// offsets).  The host only takes this path when (T-1) * row_stride * 2 + 128
+// fits in 32 bits.
+// ---------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+constexpr int kBufWord3 = 0x00020000;  // raw 32-bit data format (gfx9 buffer descriptor word 3)
+
+struct SeqBuf {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t rs2;  // row stride in bytes
+};
+
+__device__ __forceinline__ SeqBuf seq_view(const Buf& t, int b, int h, int T) {
+  SeqBuf s;
+  const bf16* base = (const bf16*)t.p + b * t.s0 + h * t.s2;
+  const uint32_t bytes = (uint32_t)(((int64_t)(T - 1) * t.s1 + 64) * 2);
+  s.r = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, kBufWord3);
+  s.rs2 = (uint32_t)(t.s1 * 2);
+  return s;
+}
+
+// 16 bytes at byte offset `off` of the sequence (zeros past row T-1).
+__device__ __forceinline__ u16x8 seq_load16(const SeqBuf& s, uint32_t off) {
+  return __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(s.r, (int)off, 0, 0));
+}
+
+// Rows 2p, 2p+1 of the 64-row tile starting at byte offset row0 (see
+// tile_load for the thread mapping); lane_off = (2p) * rs2 + 16 ch.
+__device__ __forceinline__ TileRegs seq_tile_load(const SeqBuf& s, uint32_t row0, uint32_t lane_off) {
+  TileRegs x;
+  x.a = seq_load16(s, row0 + lane_off);
+  x.b = seq_load16(s, row0 + lane_off + s.rs2);
+  return x;
+}
+
+// Four fp32 C-layout rows (features 16m + 4g .. +3, m = 0..3) of one output
+// row, scaled by f, as bf16 at byte offset `row` (dropped past row T-1).
+__device__ __forceinline__ void seq_store_row4x4(const SeqBuf& s, uint32_t row, const f32x4* acc, float f,
+                                                 int g) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    u16x4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), s.r, (int)(row + 2 * (16 * m + 4 * g)), 0, 0);
+  }
+}
+
 // Register-staged rows (tile_load) into a direct tile: thread tid writes the
 // 16-byte chunk ch of rows 2p and 2p+1 at chunk position ch ^ sw16(row).
 // Eight lanes fill one 128-byte row, a wave 1 KB of consecutive rows.

@@ -128,10 +128,11 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
-        const bool ok = key >= lo && key <= hi;
+        const bool ok = (key >= lo) & (key <= hi);
         float b2 = 0.f;
         if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
-        pv[j][r] = ok ? sigmoid_scaled(s[j][r], k2, b2) : 0.f;
+        const float sg = sigmoid_scaled(s[j][r], k2, b2);  // select, not branch
+        pv[j][r] = ok ? sg : 0.f;
       }
     }
   };

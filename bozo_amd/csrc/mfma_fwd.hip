@@ -49,10 +49,13 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
       const int key = kb0 + 16 * j + 4 * g + r;
       // kind 2 covers every valid row of the wave; rows past T (hi < lo)
       // stay masked so no tau store or bias load leaves the tensors
-      const bool ok = (kind[j] == 2 && hi >= lo) || (key >= lo && key <= hi);
+      const bool ok = kind[j] == 2 ? hi >= lo : ((key >= lo) & (key <= hi));
       float b2 = 0.f;
       if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
-      const float pv = ok ? sigmoid_scaled(s[r], k2, b2) : 0.f;
+      // computed on every lane (finite inputs) and selected: a conditional
+      // sigmoid becomes a branch per element
+      const float sg = sigmoid_scaled(s[r], k2, b2);
+      const float pv = ok ? sg : 0.f;
       if (TAU && ok) {
         const int col = tau_col(p, tq, key);
         if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), pv);
@@ -101,7 +104,8 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 V0[kDTile];
   __shared__ __attribute__((aligned(16))) bf16 V1[kDTile];
   __shared__ __attribute__((aligned(16))) bf16 V2[kDTile];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar branches on it
   const int g = lane >> 4, c = lane & 15;
   const int nch = (p.ntiles + p.chunk - 1) / p.chunk;
   const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
     const int lo = tq - p.win > 0 ? tq - p.win : 0;
     const int hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
     const WaveBand wb = wave_band(p, t0 + wave * 16);
-    if (tq >= T) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; }
+    // rows past T hold row T-1 (finite) and are masked out entirely
     f32x4 acc[4] = {};
     float msum = 0.f;
     if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
