@@ -43,6 +43,24 @@ __device__ __forceinline__ void x_put(bf16* X, int j, int sl, int g, int c, cons
   *(u16x4*)(X + (j * kXSlots + sl) * kXSub + c * 16 + 4 * g) = o;
 }
 
+__device__ __forceinline__ void x_put_bits(bf16* X, int j, int sl, int g, int c, u16x4 v) {
+  *(u16x4*)(X + (j * kXSlots + sl) * kXSub + c * 16 + 4 * g) = v;
+}
+
+__device__ __forceinline__ u16x4 bf16x4_bits(float a, float b, float c, float d) {
+  u16x4 o;
+  o[0] = bf16_bits((bf16)a); o[1] = bf16_bits((bf16)b);
+  o[2] = bf16_bits((bf16)c); o[3] = bf16_bits((bf16)d);
+  return o;
+}
+
+__device__ __forceinline__ bf16x8 join_bits(u16x4 lo, u16x4 hi) {
+  u16x8 r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 // B operand of a product contracting over the 32 queries of groups j0, j0+1:
 // lane (g, c) gets key c of the sub-tiles, queries {4g..4g+3} of group j0
 // and of group j0+1 (the tile-row order dt_tr8 gives the A operand).  An
@@ -68,9 +86,16 @@ __device__ __forceinline__ bf16x8 x_pair(const bf16* X, int j0, int sl0, bool ok
 #define TENSION_BWD_WAVES_PER_EU 2
 #endif
 
-template <int NORM, bool BIAS, bool DTAU>
+// FAST (W = 64, T a multiple of 64, no bias / dTau): the band of every
+// 16-query group is the same five key groups -- slot 0 the old block's
+// diagonal group (key >= query - 64, i.e. 4g + r >= c within the group),
+// slots 1..3 entirely valid, slot 4 the new block's diagonal group (key <=
+// query - 1, i.e. 4g + r < c) -- so the masks are two per-lane constants and
+// no per-element index arithmetic is needed.
+template <int NORM, bool BIAS, bool DTAU, bool FAST>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_BWD_WAVES_PER_EU, TENSION_BWD_WAVES_PER_EU)))
 void mfma_bwd_fused(BandParams p) {
+  static_assert(!FAST || (!BIAS && !DTAU), "the fast path has no bias / dTau");
   __shared__ __attribute__((aligned(16))) bf16 Kt[2][kDTile];  // key block k in slot k & 1
   __shared__ __attribute__((aligned(16))) bf16 Vt[2][kDTile];
   __shared__ __attribute__((aligned(16))) bf16 Qt[kDTile];     // query tile of the step
@@ -95,11 +120,9 @@ void mfma_bwd_fused(BandParams p) {
   const SeqBuf sv = seq_view(p.v, b, h, T), so = seq_view(p.dout, b, h, T);
   const SeqBuf sdq = seq_view(p.dq, b, h, T), sdk = seq_view(p.dk, b, h, T);
   const SeqBuf sdv = seq_view(p.dv, b, h, T);
-  // thread tid moves 16 bytes (chunk tid % 8) of tile rows 2p, 2p+1 (p = tid / 8)
-  const uint32_t lq = (uint32_t)(2 * (tid >> 3)) * sq.rs2 + 16 * (tid & 7);
-  const uint32_t lk = (uint32_t)(2 * (tid >> 3)) * sk.rs2 + 16 * (tid & 7);
-  const uint32_t lv = (uint32_t)(2 * (tid >> 3)) * sv.rs2 + 16 * (tid & 7);
-  const uint32_t lo_ = (uint32_t)(2 * (tid >> 3)) * so.rs2 + 16 * (tid & 7);
+  // thread tid moves 16 bytes of two staged tile rows (staged_row)
+  const uint32_t lq = seq_lane_off(sq, tid), lk = seq_lane_off(sk, tid);
+  const uint32_t lv = seq_lane_off(sv, tid), lo_ = seq_lane_off(so, tid);
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
 
@@ -132,6 +155,13 @@ void mfma_bwd_fused(BandParams p) {
 
   // dK/dV of block t-1 (key group w), carried from step t-1 to step t
   f32x4 dk_old[4] = {}, dv_old[4] = {};
+  // FAST: diagonal-group masks (1 valid, 0 not) for keys 4g + r of query c
+  float mo[4], mn[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mo[r] = 4 * g + r >= c ? 1.f : 0.f;
+    mn[r] = 1.f - mo[r];
+  }
 
   for (int t = tA; t <= tE; ++t) {
     const bool halo = t >= tB;
@@ -165,7 +195,12 @@ void mfma_bwd_fused(BandParams p) {
       const int gg = w + sl;  // key group among the 8 of blocks t-1, t
       const int blk = gg >> 2, j = gg & 3;
       const int kb0 = (t - 1 + blk) * kTile + 16 * j;
-      kind[sl] = sub_kind(wb, kb0);
+      if (FAST) {
+        const bool live = blk == 1 || t >= 1;
+        kind[sl] = live ? (sl == 0 || sl == kXSlots - 1 ? 1 : 2) : 0;
+      } else {
+        kind[sl] = sub_kind(wb, kb0);
+      }
       // the halo's new-block keys only feed its (unwritten) dQ; with tau-mass
       // normalisation they still enter the coefficients
       if (halo && blk == 1 && NORM != NORM_MASS_) kind[sl] = 0;
@@ -182,6 +217,21 @@ void mfma_bwd_fused(BandParams p) {
       s = mfma(dt_row8(Ks, 16 * j + c, 4 + g), qf[1], s);
       d = mfma(dt_row8(Vs, 16 * j + c, g), gf[0], d);
       d = mfma(dt_row8(Vs, 16 * j + c, 4 + g), gf[1], d);
+      if (FAST) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = sigmoid_scaled(s[r], k2, 0.f);
+          if (sl == 0) x *= mo[r];
+          if (sl == kXSlots - 1) x *= mn[r];
+          pv[sl][r] = x;
+          if (NORM == NORM_MASS_) {
+            msum += x;
+            dsum = fmaf(x, d[r], dsum);
+          }
+        }
+        dpv[sl] = d;
+        continue;
+      }
       const bool full = kind[sl] == 2;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -212,6 +262,43 @@ void mfma_bwd_fused(BandParams p) {
       const int cnt = tq < p.W ? tq : p.W;
       ca = 1.f / (float)(cnt > 1 ? cnt : 1);
     }
+    if (FAST) {
+      // G = (a dP - c) P (1 - P): zero wherever P is masked to zero
+      u16x4 gb[kXSlots];
+#pragma unroll
+      for (int sl = 0; sl < kXSlots; ++sl) {
+        float gq[4], pq[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = pv[sl][r];
+          gq[r] = fmaf(dpv[sl][r], ca, -cc) * fmaf(-x, x, x);
+          pq[r] = x * ca;
+        }
+        gb[sl] = bf16x4_bits(gq[0], gq[1], gq[2], gq[3]);
+        x_put_bits(XP, w, sl, g, c, bf16x4_bits(pq[0], pq[1], pq[2], pq[3]));
+        x_put_bits(XG, w, sl, g, c, gb[sl]);
+      }
+      if (!halo) {
+        f32x4 acc[4] = {};
+        auto dq_pair = [&](int i, u16x4 lo4, u16x4 hi4) {
+          const bf16* Ks = (i >> 1) ? Knew : Kold;
+          const bf16x8 pb = join_bits(lo4, hi4);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Ks, m, 32 * (i & 1), g, c), pb, acc[m]);
+        };
+        const u16x4 z = {0, 0, 0, 0};
+        if ((w & 1) == 0) {
+          if (kind[0] | kind[1]) dq_pair(w >> 1, gb[0], gb[1]);
+          if (kind[2] | kind[3]) dq_pair((w >> 1) + 1, gb[2], gb[3]);
+          if (kind[4]) dq_pair((w >> 1) + 2, gb[4], z);
+        } else {
+          if (kind[0]) dq_pair(w >> 1, z, gb[0]);
+          if (kind[1] | kind[2]) dq_pair((w >> 1) + 1, gb[1], gb[2]);
+          if (kind[3] | kind[4]) dq_pair((w >> 1) + 2, gb[3], gb[4]);
+        }
+        seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
+      }
+    } else {
     // G overwrites dP in place (dpv), P' = a P overwrites P (pv)
 #pragma unroll
     for (int sl = 0; sl < kXSlots; ++sl) {
@@ -255,6 +342,7 @@ void mfma_bwd_fused(BandParams p) {
       }
       seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
     }
+    }  // !FAST
     __syncthreads();  // X written; every wave is done with block t-1
 
     if (more) {  // block t+1 replaces block t-1
@@ -331,17 +419,21 @@ void mfma_bwd_fused(BandParams p) {
   }
 }
 
-template <int NORM, bool BIAS, bool DTAU>
+template <int NORM, bool BIAS, bool DTAU, bool FAST>
 static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
-  hipLaunchKernelGGL((mfma_bwd_fused<NORM, BIAS, DTAU>), dim3(nwg), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((mfma_bwd_fused<NORM, BIAS, DTAU, FAST>), dim3(nwg), dim3(kThreads), 0, st, p);
 }
 
 template <int NORM>
 static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, bool dtau) {
   if (bias) {
-    if (dtau) go<NORM, true, true>(p, st, nwg); else go<NORM, true, false>(p, st, nwg);
+    if (dtau) go<NORM, true, true, false>(p, st, nwg); else go<NORM, true, false, false>(p, st, nwg);
+  } else if (dtau) {
+    go<NORM, false, true, false>(p, st, nwg);
+  } else if (p.win == kTile && p.T % kTile == 0) {
+    go<NORM, false, false, true>(p, st, nwg);
   } else {
-    if (dtau) go<NORM, false, true>(p, st, nwg); else go<NORM, false, false>(p, st, nwg);
+    go<NORM, false, false, false>(p, st, nwg);
   }
 }
 

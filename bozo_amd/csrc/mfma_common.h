@@ -155,16 +155,23 @@ __device__ __forceinline__ void store_row4x4(bf16* row, const f32x4* acc, float 
 // ---------------------------------------------------------------------------
 // Direct-to-LDS tiles (gfx950): 64 rows x 128 bytes, unpadded, filled by
 // global_load_lds (16 bytes per lane; lane L of a wave instruction lands at
-// LDS base + 16 L) and read either as rows (ds_read_b128) or transposed
-// (ds_read_b64_tr_b16).  The 16-byte chunk c of row r sits at chunk position
-// c ^ sw16(r); with sw16(r) = 2(r & 3) + ((r >> 2) & 1):
-//   * row reads (lane (g, c) -> row 16j + c, chunk 4kk + g): the 8 lanes of
-//     a 128-byte LDS cycle see sw16 = {0,2,4,6,1,3,5,7}: 8 distinct chunks;
-//   * transposed reads (lane (g, j) -> row 4g + j/4, 8 bytes at column
-//     16m + 4 (j & 3)): the 16 lanes touch rows with distinct (r & 3) and
-//     chunk pairs (2m, 2m+1) ^ sw16(r) that differ in bits 1..2: 8 distinct
-//     chunks.
-// Both are free of LDS bank conflicts.
+// LDS base + 16 L) or by register-staged stores, and read either as rows
+// (ds_read_b128) or transposed (ds_read_b64_tr_b16).  The 16-byte chunk c of
+// row r sits at chunk position c ^ dsw(r), dsw(r) = f(r >> 1) with
+// f(W) = 2 (W & 3) + ((W >> 2) & 1): the swizzle is a function of the
+// 256-byte window (row pair) W = r >> 1, which is what the 64 four-byte LDS
+// banks cover.  A 16-lane group is conflict-free iff its 16-byte chunks land
+// on distinct positions (r & 1) * 8 + pos of the window:
+//   * row reads (lane (g, c) -> row 16j + c, chunk g or 4+g): windows
+//     8j + c/2 give f = {0,2,4,6,1,3,5,7}, so g ^ f is distinct per row
+//     parity: 16 distinct positions;
+//   * transposed reads (lane (g, j) -> row k0 + 4g + j/4, 8 bytes of chunk
+//     2m + (j & 3)/2): rows in windows A, A+1 (A even) whose f differ by 2,
+//     so the chunk pairs {2m, 2m+1} ^ f never coincide (and the four windows
+//     of 32 lanes differ by 0, 2, 4, 6);
+//   * stores: a DMA instruction writes 1 KB of consecutive LDS, and the
+//     staged stores (tile_store_direct) give each 16-lane group one whole
+//     window.
 // ---------------------------------------------------------------------------
 
 constexpr int kDTile = kTile * kTile;  // bf16 elements of one direct tile
@@ -173,7 +180,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ int sw16(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+__device__ __forceinline__ int dsw(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
 // Asynchronously copy rows [r0, r0+64) of a [.., T, .., 64] bf16 tensor into
 // a direct tile.  Rows outside [0, T) are clamped into range: the kernels
@@ -186,7 +193,7 @@ __device__ __forceinline__ void tile_async(const bf16* base, int64_t rs, int r0,
   for (int n = 0; n < 2; ++n) {
     const int q = (n * 4 + wave) * 64 + lane;  // 16-byte chunk slot in the tile
     const int r = q >> 3;
-    const int c = (q & 7) ^ sw16(r);           // logical chunk stored in that slot
+    const int c = (q & 7) ^ dsw(r);           // logical chunk stored in that slot
     int gr = r0 + r;
     gr = gr < 0 ? 0 : (gr > T - 1 ? T - 1 : gr);
     __builtin_amdgcn_global_load_lds((const void*)(base + (int64_t)gr * rs + 8 * c),
@@ -233,12 +240,15 @@ __device__ __forceinline__ u16x8 seq_load16(const SeqBuf& s, uint32_t off) {
   return __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(s.r, (int)off, 0, 0));
 }
 
-// Rows 2p, 2p+1 of the 64-row tile starting at byte offset row0 (see
-// tile_load for the thread mapping); lane_off = (2p) * rs2 + 16 ch.
+// Byte offset of this thread's first staged row and chunk (staged_row).
+__device__ __forceinline__ uint32_t seq_lane_off(const SeqBuf& s, int tid);
+
+// The two staged rows (staged_row, +8) of the 64-row tile that starts at
+// byte offset row0.
 __device__ __forceinline__ TileRegs seq_tile_load(const SeqBuf& s, uint32_t row0, uint32_t lane_off) {
   TileRegs x;
   x.a = seq_load16(s, row0 + lane_off);
-  x.b = seq_load16(s, row0 + lane_off + s.rs2);
+  x.b = seq_load16(s, row0 + lane_off + 8 * s.rs2);
   return x;
 }
 
@@ -255,20 +265,27 @@ __device__ __forceinline__ void seq_store_row4x4(const SeqBuf& s, uint32_t row, 
   }
 }
 
-// Register-staged rows (tile_load) into a direct tile: thread tid writes the
-// 16-byte chunk ch of rows 2p and 2p+1 at chunk position ch ^ sw16(row).
-// Eight lanes fill one 128-byte row, a wave 1 KB of consecutive rows.
+// Register-staged rows into a direct tile.  Thread tid owns the 16-byte
+// chunk ch = tid % 8 of rows ra = 16 (tid / 64) + (tid / 8) % 8 and ra + 8:
+// wave w stores exactly rows 16w .. 16w+15, and each 16-lane group writes
+// one whole 256-byte window (rows ra, ra + 1).
+__device__ __forceinline__ int staged_row(int tid) { return 16 * (tid >> 6) + ((tid >> 3) & 7); }
+
+__device__ __forceinline__ uint32_t seq_lane_off(const SeqBuf& s, int tid) {
+  return (uint32_t)staged_row(tid) * s.rs2 + 16 * (tid & 7);
+}
+
 __device__ __forceinline__ void tile_store_direct(const TileRegs& x, bf16* tile, int tid) {
-  const int pr = tid >> 3, ch = tid & 7;
-  const int ra = 2 * pr, rb = ra + 1;
-  *(u16x8*)(tile + ra * kTile + 8 * (ch ^ sw16(ra))) = x.a;
-  *(u16x8*)(tile + rb * kTile + 8 * (ch ^ sw16(rb))) = x.b;
+  const int ch = tid & 7;
+  const int ra = staged_row(tid), rb = ra + 8;
+  *(u16x8*)(tile + ra * kTile + 8 * (ch ^ dsw(ra))) = x.a;
+  *(u16x8*)(tile + rb * kTile + 8 * (ch ^ dsw(rb))) = x.b;
 }
 
 // Row read: 8 consecutive features of tile row `row` starting at logical
 // chunk `chunk` (A / B operand of a product that contracts over features).
 __device__ __forceinline__ bf16x8 dt_row8(const bf16* tile, int row, int chunk) {
-  return __builtin_bit_cast(bf16x8, *(const u16x8*)(tile + row * kTile + 8 * (chunk ^ sw16(row))));
+  return __builtin_bit_cast(bf16x8, *(const u16x8*)(tile + row * kTile + 8 * (chunk ^ dsw(row))));
 }
 
 // Transposed read: the A operand (16 features x 8 tile rows) of a product
@@ -279,8 +296,8 @@ __device__ __forceinline__ bf16x8 dt_row8(const bf16* tile, int row, int chunk) 
 __device__ __forceinline__ bf16x8 dt_tr8(const bf16* tile, int m, int k0, int g, int j) {
   const int col = 16 * m + 4 * (j & 3);
   const int r1 = k0 + 4 * g + (j >> 2), r2 = r1 + 16;
-  const bf16* a1 = tile + r1 * kTile + 8 * ((col >> 3) ^ sw16(r1)) + (col & 4);
-  const bf16* a2 = tile + r2 * kTile + 8 * ((col >> 3) ^ sw16(r2)) + (col & 4);
+  const bf16* a1 = tile + r1 * kTile + 8 * ((col >> 3) ^ dsw(r1)) + (col & 4);
+  const bf16* a2 = tile + r2 * kTile + 8 * ((col >> 3) ^ dsw(r2)) + (col & 4);
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a1);
   const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a2);
   u16x8 r;

@@ -88,6 +88,41 @@ __device__ __forceinline__ void fwd_epilogue(const BandParams& p, int b, int h, 
   }
 }
 
+// A finished output row (bf16) held back until the next tile's wait: on
+// gfx9 stores count in vmcnt, so a store issued before the wait for the
+// next key block would make that wait cover the store's completion too.
+struct OutRow {
+  u16x4 v[4];
+  int tq;
+  float msum;
+};
+
+template <int NORM, bool TAU>
+__device__ __forceinline__ OutRow fwd_finish(const BandParams& p, int b, int h, int tq, int g, const f32x4* acc,
+                                             float msum) {
+  OutRow o;
+  o.msum = wave_sum_g(msum);
+  o.tq = tq;
+  const float f = out_factor<NORM>(o.msum, tq, p.W);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o.v[m][r] = bf16_bits((bf16)(acc[m][r] * f));
+  if (TAU && tq < p.T) {
+    const int e = tau_empty_bound(p, tq);
+    for (int col = g; col < e; col += 4) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), 0.f);
+  }
+  return o;
+}
+
+__device__ __forceinline__ void fwd_store(const BandParams& p, int b, int h, int g, const OutRow& o) {
+  if (o.tq >= p.T) return;
+  bf16* orow = (bf16*)p.out.p + b * p.out.s0 + (int64_t)o.tq * p.out.s1 + h * p.out.s2;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) *(u16x4*)(orow + 16 * m + 4 * g) = o.v[m];
+  if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)o.tq * p.mass.s1 + h * p.mass.s2, o.msum);
+}
+
 __device__ __forceinline__ void load_qfrag(const bf16* qb_, int64_t rs, int tq, int T, int g, bf16x8* qf) {
   const int tr = tq < T ? tq : T - 1;
   qf[0] = load8(qb_ + (int64_t)tr * rs + 8 * g);
@@ -131,6 +166,8 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
   load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
   fetch(t_first - 1, K0, V0);
   fetch(t_first, K1, V1);
+  OutRow pend;             // the previous tile's output, stored after the next wait
+  bool has_pend = false;
 
   // tile t = t_first + lt uses key blocks t-1 (slot lt % 3) and t (slot
   // (lt+1) % 3); block t+1 goes to slot (lt+2) % 3, freed by tile t-1.
@@ -140,6 +177,7 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
     if (t >= t_end) return false;
     wait_vm<0>();
     __syncthreads();
+    if (has_pend) fwd_store(p, b, h, g, pend);
     const bool more = t + 1 < t_end;
     if (more) {
       load_qfrag(qb_, p.q.s1, (t + 1) * kTile + wave * 16 + c, T, g, qn);
@@ -155,7 +193,8 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
     float msum = 0.f;
     if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
     fwd_block<BIAS, TAU>(p, Kb, Vb, t0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
-    fwd_epilogue<NORM, TAU>(p, b, h, tq, g, acc, msum);
+    pend = fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, msum);
+    has_pend = true;
     if (more) { qf[0] = qn[0]; qf[1] = qn[1]; }
     return true;
   };
@@ -165,6 +204,7 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
     if (!tile_step(lt + 1, K1, V1, K2, V2, K0, V0)) break;
     if (!tile_step(lt + 2, K2, V2, K0, V0, K1, V1)) break;
   }
+  if (has_pend) fwd_store(p, b, h, g, pend);
 }
 
 // ------------------------------------------------------------------ streaming kernel
