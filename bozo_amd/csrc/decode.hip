@@ -16,6 +16,16 @@ __device__ __forceinline__ int ring_w(int slot, int pos, int W) {
   return w < 0 ? w + W : w;
 }
 
+// Cache rows are read once per step: non-temporal loads keep them from
+// displacing reusable lines in L2.
+__device__ __forceinline__ u16x8 cache_load(const bf16* p) {
+#ifdef TENSION_DECODE_TEMPORAL
+  return *(const u16x8*)p;
+#else
+  return __builtin_nontemporal_load((const u16x8*)p);
+#endif
+}
+
 // Fast path: bf16 q / cache / out, D = 64, W % 32 == 0, W <= 512.
 constexpr int kDecThreads = 256;
 constexpr int kDecMaxPasses = 16;  // W <= 16 * 32
@@ -45,14 +55,14 @@ __global__ __launch_bounds__(kDecThreads) void decode_bf16_d64(DecodeParams p) {
   for (int i = 0; i < kDecMaxPasses; ++i) {
     if (i < npass) {
       const int slot = i * 32 + wave * 8 + rw;
-      kr[i] = __builtin_bit_cast(bf16x8, *(const u16x8*)(kbase + (int64_t)slot * p.kc.s2 + 8 * ch));
+      kr[i] = __builtin_bit_cast(bf16x8, cache_load(kbase + (int64_t)slot * p.kc.s2 + 8 * ch));
     }
   }
 #pragma unroll
   for (int i = 0; i < kDecMaxPasses; ++i) {
     if (i < npass) {
       const int slot = i * 32 + wave * 8 + rw;
-      vr[i] = __builtin_bit_cast(bf16x8, *(const u16x8*)(vbase + (int64_t)slot * p.vc.s2 + 8 * ch));
+      vr[i] = __builtin_bit_cast(bf16x8, cache_load(vbase + (int64_t)slot * p.vc.s2 + 8 * ch));
     }
   }
   const float inv_scale = (float)(1.0 / p.scale);

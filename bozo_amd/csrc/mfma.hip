@@ -22,8 +22,12 @@ int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* e
   // ring kernels: consecutive tiles per workgroup, sized so the grid still
   // offers about three workgroups per CU (256 CUs)
   p.chunk = 1;
+#ifdef TENSION_FWD_CHUNK
+  p.chunk = TENSION_FWD_CHUNK;
+#else
   while (p.chunk < 4 && (int64_t)p.B * p.H * ((p.ntiles + 2 * p.chunk - 1) / (2 * p.chunk)) >= 768)
     p.chunk *= 2;
+#endif
   if (nwg <= 0 || nwg > 0x7fffffff) return -1;
   const int norm = (p.flags & TENSION_NORM_MASS)    ? NORM_MASS_
                    : (p.flags & TENSION_NORM_COUNT) ? NORM_COUNT_

@@ -163,9 +163,20 @@ void mfma_bwd_fused(BandParams p) {
     mn[r] = 1.f - mo[r];
   }
 
+#ifdef TENSION_TRACE
+  unsigned long long* trace = (unsigned long long*)p.ws;
+  auto mark = [&](int t, int k) {
+    if (lane == 0 && t - tA < 8) trace[(((int64_t)blockIdx.x * 4 + w) * 8 + (t - tA)) * 6 + k] = __builtin_amdgcn_s_memtime();
+  };
+  unsigned long long* rt = trace + (int64_t)gridDim.x * 4 * 8 * 6;
+  if (lane == 0) rt[((int64_t)blockIdx.x * 4 + w) * 2] = __builtin_amdgcn_s_memrealtime();
+#else
+  auto mark = [](int, int) {};
+#endif
   for (int t = tA; t <= tE; ++t) {
     const bool halo = t >= tB;
     const bool more = t < tE;
+    mark(t, 0);
     // ---- prefetch of step t+1 into registers
     TileRegs kn, vn, qn, on;
     if (more) {
@@ -343,12 +354,15 @@ void mfma_bwd_fused(BandParams p) {
       seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
     }
     }  // !FAST
+    mark(t, 1);
     __syncthreads();  // X written; every wave is done with block t-1
+    mark(t, 2);
 
     if (more) {  // block t+1 replaces block t-1
       tile_store_direct(kn, Kt[(t + 1) & 1], tid);
       tile_store_direct(vn, Vt[(t + 1) & 1], tid);
     }
+    mark(t, 3);
 
     // ---- phase 2: keys 16w..16w+15 of block t-1 (key group w) and of
     // block t (key group 4+w).  Query group j covers key groups j..j+4.
@@ -396,6 +410,7 @@ void mfma_bwd_fused(BandParams p) {
       dk_old[m] = dk_new[m];
       dv_old[m] = dv_new[m];
     }
+    mark(t, 4);
     __syncthreads();  // phase 2 is done with X and the Q/dO tiles
 
     if (more) {
@@ -409,7 +424,11 @@ void mfma_bwd_fused(BandParams p) {
       gf[0] = dt_row8(Ot, 16 * w + c, g);
       gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
     }
+    mark(t, 5);
   }
+#ifdef TENSION_TRACE
+  if (lane == 0) rt[((int64_t)blockIdx.x * 4 + w) * 2 + 1] = __builtin_amdgcn_s_memrealtime();
+#endif
   // the last block of the sequence has no halo step: it is complete after
   // its own step (no query tile follows it)
   if (tE == tB - 1) {
