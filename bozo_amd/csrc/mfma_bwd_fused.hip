@@ -28,58 +28,11 @@
 // 32-byte row.  Phase-1 stores (lane (g,c): query c, keys 4g..4g+3) and
 // phase-2 transposed reads (16 lanes: 4 rows x 16 keys) each touch 512
 // contiguous bytes per wave instruction.
-#include "mfma_common.h"
+#include <type_traits>
+
+#include "mfma_xchg.h"
 
 namespace tension {
-
-constexpr int kXSlots = 5;                    // 16-key groups in the band of 16 queries (W <= 64)
-constexpr int kXSub = 16 * 16;                // bf16 elements of one sub-tile
-constexpr int kXElems = 4 * kXSlots * kXSub;  // one exchange tensor (4 query groups)
-
-__device__ __forceinline__ void x_put(bf16* X, int j, int sl, int g, int c, const float* v4) {
-  u16x4 o;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)v4[r]);
-  *(u16x4*)(X + (j * kXSlots + sl) * kXSub + c * 16 + 4 * g) = o;
-}
-
-__device__ __forceinline__ void x_put_bits(bf16* X, int j, int sl, int g, int c, u16x4 v) {
-  *(u16x4*)(X + (j * kXSlots + sl) * kXSub + c * 16 + 4 * g) = v;
-}
-
-__device__ __forceinline__ u16x4 bf16x4_bits(float a, float b, float c, float d) {
-  u16x4 o;
-  o[0] = bf16_bits((bf16)a); o[1] = bf16_bits((bf16)b);
-  o[2] = bf16_bits((bf16)c); o[3] = bf16_bits((bf16)d);
-  return o;
-}
-
-__device__ __forceinline__ bf16x8 join_bits(u16x4 lo, u16x4 hi) {
-  u16x8 r;
-  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-  return __builtin_bit_cast(bf16x8, r);
-}
-
-// B operand of a product contracting over the 32 queries of groups j0, j0+1:
-// lane (g, c) gets key c of the sub-tiles, queries {4g..4g+3} of group j0
-// and of group j0+1 (the tile-row order dt_tr8 gives the A operand).  An
-// absent sub-tile (no slot of that query group covers the key group) reads
-// as zeros.
-__device__ __forceinline__ bf16x8 x_pair(const bf16* X, int j0, int sl0, bool ok0, int sl1, bool ok1, int g,
-                                         int l16) {
-  const int off = (4 * g + (l16 >> 2)) * 16 + 4 * (l16 & 3);
-  s16x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
-  if (ok0) lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + (j0 * kXSlots + sl0) * kXSub + off));
-  if (ok1)
-    hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + ((j0 + 1) * kXSlots + sl1) * kXSub + off));
-  u16x8 r;
-  r[0] = (unsigned short)lo[0]; r[1] = (unsigned short)lo[1];
-  r[2] = (unsigned short)lo[2]; r[3] = (unsigned short)lo[3];
-  r[4] = (unsigned short)hi[0]; r[5] = (unsigned short)hi[1];
-  r[6] = (unsigned short)hi[2]; r[7] = (unsigned short)hi[3];
-  return __builtin_bit_cast(bf16x8, r);
-}
 
 // Two waves per SIMD (two workgroups per CU): registers capped at 256.
 #ifndef TENSION_BWD_WAVES_PER_EU
@@ -163,20 +116,97 @@ void mfma_bwd_fused(BandParams p) {
     mn[r] = 1.f - mo[r];
   }
 
-#ifdef TENSION_TRACE
-  unsigned long long* trace = (unsigned long long*)p.ws;
-  auto mark = [&](int t, int k) {
-    if (lane == 0 && t - tA < 8) trace[(((int64_t)blockIdx.x * 4 + w) * 8 + (t - tA)) * 6 + k] = __builtin_amdgcn_s_memtime();
+  // FAST phase 1 with all five slots live (steps t >= 1; the halo only with
+  // tau-mass normalisation): slot sl is key group w + sl of blocks t-1, t;
+  // slot 0 is the old block's diagonal group, slot 4 the new block's
+  auto phase1_live = [&](int t, auto dq_tag) {
+    constexpr bool DQ = decltype(dq_tag)::value;
+    const bf16* Kold = Kt[(t + 1) & 1];
+    const bf16* Vold = Vt[(t + 1) & 1];
+    const bf16* Knew = Kt[t & 1];
+    const bf16* Vnew = Vt[t & 1];
+    f32x4 sv[kXSlots], dv[kXSlots];
+#pragma unroll
+    for (int sl = 0; sl < kXSlots; ++sl) {
+      const int gg = w + sl;
+      const bf16* Ks = (gg >> 2) ? Knew : Kold;
+      const bf16* Vs = (gg >> 2) ? Vnew : Vold;
+      const int row = 16 * (gg & 3) + c;
+      f32x4 a = {}, d = {};
+      a = mfma(dt_row8(Ks, row, g), qf[0], a);
+      a = mfma(dt_row8(Ks, row, 4 + g), qf[1], a);
+      d = mfma(dt_row8(Vs, row, g), gf[0], d);
+      d = mfma(dt_row8(Vs, row, 4 + g), gf[1], d);
+      sv[sl] = a;
+      dv[sl] = d;
+    }
+    float pv[kXSlots][4];
+    float ms[kXSlots], ds[kXSlots];
+#pragma unroll
+    for (int sl = 0; sl < kXSlots; ++sl) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = sigmoid_scaled(sv[sl][r], k2, 0.f);
+        if (sl == 0) x *= mo[r];
+        if (sl == kXSlots - 1) x *= mn[r];
+        pv[sl][r] = x;
+      }
+      // short sums instead of one 20-long dependent chain
+      ms[sl] = (pv[sl][0] + pv[sl][1]) + (pv[sl][2] + pv[sl][3]);
+      ds[sl] = fmaf(pv[sl][0], dv[sl][0], pv[sl][1] * dv[sl][1]) + fmaf(pv[sl][2], dv[sl][2], pv[sl][3] * dv[sl][3]);
+    }
+    const int tq = t * kTile + 16 * w + c;
+    float ca = 1.f, cc = 0.f;
+    if (NORM == NORM_MASS_) {
+      float msum = ((ms[0] + ms[1]) + (ms[2] + ms[3])) + ms[4];
+      float dsum = ((ds[0] + ds[1]) + (ds[2] + ds[3])) + ds[4];
+      msum = wave_sum_g(msum);
+      dsum = wave_sum_g(dsum);
+      ca = __builtin_amdgcn_rcpf(msum > kMassEps ? msum : kMassEps);
+      cc = msum >= kMassEps ? dsum * ca * ca : 0.f;
+    } else if (NORM == NORM_COUNT_) {
+      const int cnt = tq < p.W ? tq : p.W;
+      ca = __builtin_amdgcn_rcpf((float)(cnt > 1 ? cnt : 1));
+    }
+    u16x4 gb[kXSlots];
+#pragma unroll
+    for (int sl = 0; sl < kXSlots; ++sl) {
+      float gq[4], pq[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = pv[sl][r];
+        gq[r] = fmaf(dv[sl][r], ca, -cc) * fmaf(-x, x, x);
+        pq[r] = x * ca;
+      }
+      gb[sl] = bf16x4_bits(gq[0], gq[1], gq[2], gq[3]);
+      x_put_bits(XP, w, sl, g, c, bf16x4_bits(pq[0], pq[1], pq[2], pq[3]));
+      x_put_bits(XG, w, sl, g, c, gb[sl]);
+    }
+    if constexpr (DQ) {
+      f32x4 acc[4] = {};
+      auto dq_pair = [&](int i, u16x4 lo4, u16x4 hi4) {
+        const bf16* Ks = (i >> 1) ? Knew : Kold;
+        const bf16x8 pb = join_bits(lo4, hi4);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Ks, m, 32 * (i & 1), g, c), pb, acc[m]);
+      };
+      const u16x4 z = {0, 0, 0, 0};
+      if ((w & 1) == 0) {
+        dq_pair(w >> 1, gb[0], gb[1]);
+        dq_pair((w >> 1) + 1, gb[2], gb[3]);
+        dq_pair((w >> 1) + 2, gb[4], z);
+      } else {
+        dq_pair(w >> 1, z, gb[0]);
+        dq_pair((w >> 1) + 1, gb[1], gb[2]);
+        dq_pair((w >> 1) + 2, gb[3], gb[4]);
+      }
+      seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
+    }
   };
-  unsigned long long* rt = trace + (int64_t)gridDim.x * 4 * 8 * 6;
-  if (lane == 0) rt[((int64_t)blockIdx.x * 4 + w) * 2] = __builtin_amdgcn_s_memrealtime();
-#else
-  auto mark = [](int, int) {};
-#endif
+
   for (int t = tA; t <= tE; ++t) {
     const bool halo = t >= tB;
     const bool more = t < tE;
-    mark(t, 0);
     // ---- prefetch of step t+1 into registers
     TileRegs kn, vn, qn, on;
     if (more) {
@@ -188,6 +218,14 @@ void mfma_bwd_fused(BandParams p) {
     }
 
     // ---- phase 1: queries 16w..16w+15 of tile t
+    if (FAST && t >= 1 && (!halo || NORM == NORM_MASS_)) {
+      // every slot live: one branch-free block, so the LDS reads, MFMAs and
+      // sigmoids of different slots overlap
+      if (!halo)
+        phase1_live(t, std::true_type{});
+      else
+        phase1_live(t, std::false_type{});
+    } else {
     const bf16* Kold = Kt[(t + 1) & 1];  // block t-1
     const bf16* Vold = Vt[(t + 1) & 1];
     const bf16* Knew = Kt[t & 1];        // block t
@@ -354,15 +392,13 @@ void mfma_bwd_fused(BandParams p) {
       seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
     }
     }  // !FAST
-    mark(t, 1);
+    }  // not all live
     __syncthreads();  // X written; every wave is done with block t-1
-    mark(t, 2);
 
     if (more) {  // block t+1 replaces block t-1
       tile_store_direct(kn, Kt[(t + 1) & 1], tid);
       tile_store_direct(vn, Vt[(t + 1) & 1], tid);
     }
-    mark(t, 3);
 
     // ---- phase 2: keys 16w..16w+15 of block t-1 (key group w) and of
     // block t (key group 4+w).  Query group j covers key groups j..j+4.
@@ -410,7 +446,6 @@ void mfma_bwd_fused(BandParams p) {
       dk_old[m] = dk_new[m];
       dv_old[m] = dv_new[m];
     }
-    mark(t, 4);
     __syncthreads();  // phase 2 is done with X and the Q/dO tiles
 
     if (more) {
@@ -424,11 +459,7 @@ void mfma_bwd_fused(BandParams p) {
       gf[0] = dt_row8(Ot, 16 * w + c, g);
       gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
     }
-    mark(t, 5);
   }
-#ifdef TENSION_TRACE
-  if (lane == 0) rt[((int64_t)blockIdx.x * 4 + w) * 2 + 1] = __builtin_amdgcn_s_memrealtime();
-#endif
   // the last block of the sequence has no halo step: it is complete after
   // its own step (no query tile follows it)
   if (tE == tB - 1) {
