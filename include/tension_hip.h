@@ -94,7 +94,9 @@ int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H,
 /* ---------------------------------------------------------------------------
  * Local window backward.  Replaces `_bwd_dq_kernel` + `_bwd_dkv_kernel`
  * (kernel.py:130-341) launched by `_CausalTensionFn.backward`
- * (ops.py:126-187).  Launches tension_window_bwd_dq then
+ * (ops.py:126-187).  For windows W <= 64 with bf16 rows (head dim 64,
+ * 16-byte aligned rows) it launches one kernel that produces dQ, dK and
+ * dV in a single pass; otherwise tension_window_bwd_dq then
  * tension_window_bwd_dkv on `stream`.  Recomputes tau from q, k (and
  * bias); nothing from the forward is needed besides the inputs.
  *   dout: grad of out (of the raw msg without a NORM flag, of the
@@ -104,7 +106,9 @@ int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H,
  *   accumulated, in their own dtypes.
  *   workspace: tension_window_bwd_workspace() bytes (NULL if that is 0);
  *   with TENSION_NORM_MASS it carries per-query coefficients from the dq
- *   kernel to the dkv kernel.
+ *   kernel to the dkv kernel (the single-pass kernel forms them in
+ *   registers and leaves the workspace untouched; it is required either
+ *   way, so callers need not know which kernel runs).
  * ------------------------------------------------------------------------- */
 int tension_window_bwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* v, const tension_buf* dout,
