@@ -331,7 +331,8 @@ def bench_window(args, dev):
 
 def profile_kernels(n, dev):
     """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
-    of each band kernel on rotated config-2 sets, then a plain device copy of
+    of each band kernel on rotated config-2 sets and n config-4 decode steps
+    over 4 rotated caches, then a plain device copy of
     known size (256 MiB read + 256 MiB written) whose FETCH_SIZE/WRITE_SIZE
     readings calibrate the counters into bytes."""
     from bozo_amd import _lib as L
@@ -342,12 +343,30 @@ def profile_kernels(n, dev):
         for i in range(n):
             fns[i % NSETS][0][name]()
         torch.cuda.synchronize()
+    del fns, sets
+    # config-4 decode steps over 4 rotated caches, fresh q / k / v per step
+    from bozo_amd import TensionDecodeCache
+    N, Hd, Wd, NC = 64, 16, 256, 4
+    g = torch.Generator(device=dev).manual_seed(3)
+    caches = []
+    for _ in range(NC):
+        c = TensionDecodeCache(N, Hd, D, Wd, dtype=torch.bfloat16, device=dev)
+        c.k.normal_(0.0, 0.5, generator=g)  # in place: no device copies besides the calibration
+        c.v.normal_(0.0, 0.5, generator=g)
+        c.pos[c.cur].fill_(Wd)
+        caches.append(c)
+    qkv = [(torch.randn(n, N, Hd, D, device=dev, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        caches[i % NC].step(qkv[0][i], qkv[1][i], qkv[2][i])
+    torch.cuda.synchronize()
+    del caches, qkv
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"[bench] profile-kernels: {n} launches each of fwd/bwd/dq/dkv, 4 copies of 256 MiB")
+    log(f"[bench] profile-kernels: {n} launches each of fwd/bwd/dq/dkv and decode, 4 copies of 256 MiB")
 
 
 def _phase_regions(cur):
@@ -388,6 +407,15 @@ def summarize(paths):
         if pmc:
             for n, cn, v, cnt in pmc:
                 counters.setdefault(cn, {})[n.split("(")[0]] = (v, cnt)
+            # calibration copies: the largest copy dispatches (the 256 MiB copies;
+            # smaller set-up copies would dilute the mean)
+            for cn, in cur.execute("select distinct counter_name from pmc_events").fetchall():
+                vals = [v for v, in cur.execute(
+                    "select counter_value from pmc_events where counter_name = ? and name like ?",
+                    (cn, "__amd_rocclr_copyBuffer%")).fetchall()]
+                big = [v for v in vals if vals and v >= 0.5 * max(vals)]
+                if big:
+                    counters[cn]["__amd_rocclr_copyBuffer"] = (statistics.mean(big), len(big))
             continue
         phases = _phase_regions(cur) or [("all", min(k[1] for k in kern), max(k[2] for k in kern))]
         print(f"# kernel durations: {os.path.basename(os.path.dirname(db))}/{os.path.basename(db)}")
@@ -474,11 +502,17 @@ def bench_decode(dev, reps):
     run = Runner([lambda: [caches[i % NC].step(q[i], k[i], v[i]) for i in range(S)]], warm=1)
     ms = time_units(run, reps, 1, "decode") / S
     step_bytes = 2 * N * H * W * D * 2 + 4 * N * H * D * 2
+    traffic = None  # HBM bytes per launch from the committed rocprofv3 --pmc summary
+    tfile = os.path.join(ROOT, "profiles", "traffic_window_c2.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("bytes_per_launch", {}).get("decode_bf16_d64")
     return {"config": "decode 64 seqs H16 d64 W256 bf16, 4 rotated caches, 512 steps per graph (config 4)",
             "us_per_step": round(ms * 1e3, 3), "steps_per_s": round(1e3 / ms, 1),
             "alg_bytes_per_step": step_bytes,
             "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": traffic}
 
 
 def main():

@@ -360,14 +360,17 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   p.kc = make_buf(k_cache); p.vc = make_buf(v_cache); p.out = make_buf(out); p.tau = make_buf(tau);
   p.pos_in = pos_in; p.pos_out = pos_out;
   p.N = (int)N; p.H = (int)H; p.D = (int)D; p.W = (int)W;
-  p.scale = scale; p.flags = flags;
+  p.scale = scale; p.inv_scale = (float)(1.0 / scale); p.flags = flags;
   auto a16 = [](const tension_buf* b, bool four) {
     if (b->dtype != TENSION_BF16 || ((uintptr_t)b->ptr & 15)) return false;
     return b->s[0] % 8 == 0 && b->s[1] % 8 == 0 && (!four || b->s[2] % 8 == 0);
   };
-  const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W % 32 == 0 && W <= 512 && a16(q, false) &&
+  // the fast kernel reads each (n, h) cache slab through a buffer descriptor
+  // of W * row_stride * 2 bytes (31-bit range, rows of at least 64 elements)
+  auto slab_fits = [&](const tension_buf* b) { return b->s[2] >= 64 && W * b->s[2] * 2 < ((int64_t)1 << 31); };
+  const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 512 && a16(q, false) &&
                     a16(k_new, false) && a16(v_new, false) && a16(out, false) && a16(k_cache, true) &&
-                    a16(v_cache, true);
+                    a16(v_cache, true) && slab_fits(k_cache) && slab_fits(v_cache);
   hipError_t e = hipSuccess;
   launch_decode(fast, is_f64(q) || is_f64(k_cache) || is_f64(v_cache), p, hs(stream), &e);
   return launched(e, "tension_decode_step");

@@ -2,10 +2,10 @@
 //
 // Decode is a pure HBM stream: every step reads the whole cache of each
 // (sequence, head) once (2 * W * D * 2 bytes) and does 4*D flops per slot.
-// One workgroup owns one (n, h); eight lanes cover one 128-byte cache row so
-// each wave load instruction reads 1 KB of contiguous cache, all loads of a
-// workgroup are issued before any arithmetic, and the sums are folded with
-// cross-lane shuffles and one LDS pass.
+// One 8-wave workgroup owns one (n, h): every lane issues all of its cache
+// loads before any arithmetic, eight lanes cover one 128-byte cache row (1 KB
+// of contiguous cache per wave load instruction), and the sums are folded with
+// DPP lane moves and one LDS pass.
 #include "kernels.h"
 
 namespace tension {
@@ -16,115 +16,151 @@ __device__ __forceinline__ int ring_w(int slot, int pos, int W) {
   return w < 0 ? w + W : w;
 }
 
-// Cache rows are read once per step: non-temporal loads keep them from
-// displacing reusable lines in L2.
-__device__ __forceinline__ u16x8 cache_load(const bf16* p) {
-#ifdef TENSION_DECODE_TEMPORAL
-  return *(const u16x8*)p;
-#else
-  return __builtin_nontemporal_load((const u16x8*)p);
-#endif
+// Fast path: bf16 q / cache / out, D = 64, W <= 8 * NW * NP.
+//
+// NW waves per workgroup; pass i covers cache rows 8 * NW * i .. + 8 * NW - 1,
+// eight lanes per 128-byte row, so each wave load instruction reads 1 KB of
+// contiguous cache.  Every lane issues its NP K loads and NP V loads before
+// any arithmetic, as raw buffer loads over the (n, h) slab of W rows: rows
+// past W fall outside the descriptor's range and read as zero with no memory
+// access, so no load sits behind a branch and the compiler waits for pass i
+// alone (vmcnt) before computing on it.  The 8-lane row dot products reduce
+// through DPP lane moves instead of LDS shuffles.
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
-// Fast path: bf16 q / cache / out, D = 64, W % 32 == 0, W <= 512.
-constexpr int kDecThreads = 256;
-constexpr int kDecMaxPasses = 16;  // W <= 16 * 32
+// Sum over the aligned group of 8 lanes holding one cache row.
+__device__ __forceinline__ float row_sum8(float x) {
+  x += dpp_move<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  x += dpp_move<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  x += dpp_move<0x141>(x);  // row_half_mirror: lane i <-> 7 - i of its 8-lane half-row
+  return x;
+}
 
-__global__ __launch_bounds__(kDecThreads) void decode_bf16_d64(DecodeParams p) {
-  __shared__ float red[4][64 + 1];
-  __shared__ float mred[4];
+constexpr int kRawBufWord3 = 0x00020000;  // raw 32-bit data format (buffer descriptor word 3)
+
+// Cache rows are read once per step: non-temporal loads (buffer cache policy
+// bit nt) keep them from displacing reusable lines in L2.
+#ifdef TENSION_DECODE_TEMPORAL
+constexpr int kCacheAux = 0;
+#else
+constexpr int kCacheAux = 2;
+#endif
+
+}  // namespace
+
+template <int NW, int NP>
+__global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
+  constexpr int kRows = 8 * NW;  // cache rows per pass
+  __shared__ float red[NW * 4][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ch = lane & 7, rw = lane >> 3;  // d-chunk, row within a pass
   const int n = blockIdx.x / p.H, h = blockIdx.x % p.H;
-  const int pos = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
   const int W = p.W;
-  const int npass = W >> 5;
 
   const bf16* qrow = (const bf16*)p.q.p + n * p.q.s0 + h * p.q.s1;
-  // Whole-vector bit casts only: a bit cast of one subscripted vector
-  // element (bit_cast<bf16>(v[i])) compiles to element 0 for every i.
-  const bf16x8 qv = __builtin_bit_cast(bf16x8, *(const u16x8*)(qrow + 8 * ch));
-  float q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = (float)qv[i];
+  const u16x8 qbits = *(const u16x8*)(qrow + 8 * ch);
+  // The new token's K / V rows are appended after the reduction, but fetched
+  // now so their latency hides under the cache stream: lanes a = tid - 64 in
+  // [0, 8) hold 16-byte chunk a of k_new, [8, 16) chunk a - 8 of v_new.  The
+  // descriptors span one 128-byte row; every other lane's offset is out of
+  // range and reads zero without a memory access, so the loads need no branch.
+  const int ai = tid - 64;
+  const __amdgpu_buffer_rsrc_t knr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const bf16*)p.kn.p + n * p.kn.s0 + h * p.kn.s1), (short)0, 128, kRawBufWord3);
+  const __amdgpu_buffer_rsrc_t vnr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const bf16*)p.vn.p + n * p.vn.s0 + h * p.vn.s1), (short)0, 128, kRawBufWord3);
+  const u16x8 knew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+      knr, (ai >= 0 && ai < 8) ? 16 * ai : 128, 0, 0));
+  const u16x8 vnew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+      vnr, (ai >= 8 && ai < 16) ? 16 * (ai - 8) : 128, 0, 0));
 
+  // one descriptor per cache slab; loads of rows >= W return zeros
   const bf16* kbase = (const bf16*)p.kc.p + n * p.kc.s0 + h * p.kc.s1;
   const bf16* vbase = (const bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1;
-  bf16x8 kr[kDecMaxPasses], vr[kDecMaxPasses];
+  const __amdgpu_buffer_rsrc_t kr_ = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kbase, (short)0, (int)((int64_t)W * p.kc.s2 * 2), kRawBufWord3);
+  const __amdgpu_buffer_rsrc_t vr_ = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)vbase, (short)0, (int)((int64_t)W * p.vc.s2 * 2), kRawBufWord3);
+  const uint32_t row0 = (uint32_t)(wave * 8 + rw);
+  const uint32_t kstep = (uint32_t)(kRows * p.kc.s2 * 2), vstep = (uint32_t)(kRows * p.vc.s2 * 2);
+  const uint32_t koff = row0 * (uint32_t)(p.kc.s2 * 2) + 16 * ch;
+  const uint32_t voff = row0 * (uint32_t)(p.vc.s2 * 2) + 16 * ch;
+  u16x8 kr[NP], vr[NP];
 #pragma unroll
-  for (int i = 0; i < kDecMaxPasses; ++i) {
-    if (i < npass) {
-      const int slot = i * 32 + wave * 8 + rw;
-      kr[i] = __builtin_bit_cast(bf16x8, cache_load(kbase + (int64_t)slot * p.kc.s2 + 8 * ch));
-    }
-  }
+  for (int i = 0; i < NP; ++i)
+    kr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(kr_, (int)(koff + i * kstep), 0, kCacheAux));
 #pragma unroll
-  for (int i = 0; i < kDecMaxPasses; ++i) {
-    if (i < npass) {
-      const int slot = i * 32 + wave * 8 + rw;
-      vr[i] = __builtin_bit_cast(bf16x8, cache_load(vbase + (int64_t)slot * p.vc.s2 + 8 * ch));
-    }
-  }
-  const float inv_scale = (float)(1.0 / p.scale);
+  for (int i = 0; i < NP; ++i)
+    vr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(vr_, (int)(voff + i * vstep), 0, kCacheAux));
+
+  const int pos = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
+  const int live = pos < W ? pos : W;  // slots [0, live) hold tokens
+  // Whole-vector bit casts only: a bit cast of one subscripted vector
+  // element (bit_cast<bf16>(v[i])) compiles to element 0 for every i.
+  const bf16x8 qv = __builtin_bit_cast(bf16x8, qbits);
+  float q[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] = (float)qv[e] * p.inv_scale;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float msum = 0.f;
 #pragma unroll
-  for (int i = 0; i < kDecMaxPasses; ++i) {
-    if (i < npass) {
-      const int slot = i * 32 + wave * 8 + rw;
-      float part = 0.f;
+  for (int i = 0; i < NP; ++i) {
+    const int slot = i * kRows + (int)row0;
+    const bf16x8 kv = __builtin_bit_cast(bf16x8, kr[i]);
+    float part = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part += q[e] * (float)kr[i][e];
-      part += __shfl_xor(part, 1);
-      part += __shfl_xor(part, 2);
-      part += __shfl_xor(part, 4);
-      const bool ok = pos >= W || slot < pos;
-      const float tau = ok ? sigmoid_fast(part * inv_scale) : 0.f;
-      if (p.tau.p && ch == 0)
-        st<float>(p.tau, n * p.tau.s0 + h * p.tau.s1 + ring_w(slot, pos, W), tau);
-      msum += tau;
+    for (int e = 0; e < 8; ++e) part += q[e] * (float)kv[e];
+    part = row_sum8(part);
+    const float tau = slot < live ? sigmoid_fast(part) : 0.f;
+    if (p.tau.p && ch == 0 && slot < W)
+      st<float>(p.tau, n * p.tau.s0 + h * p.tau.s1 + ring_w(slot, pos, W), tau);
+    msum += tau;
+    const bf16x8 vv = __builtin_bit_cast(bf16x8, vr[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vr[i][e];
-    }
+    for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vv[e];
   }
-  // fold rows within the wave (lanes with equal ch)
+  // Fold row pairs (lanes 8 apart) with a DPP rotate; then lane ch of every
+  // 16-lane row holds the sums over rows rw = 2r, 2r + 1 of its wave, and the
+  // NW * 4 row partials meet in LDS.  tau, hence msum, is equal on the 8 lanes
+  // of a row, so one lane per 16-lane row stores it.
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    acc[e] += __shfl_xor(acc[e], 8);
-    acc[e] += __shfl_xor(acc[e], 16);
-    acc[e] += __shfl_xor(acc[e], 32);
-  }
-  msum += __shfl_xor(msum, 8);
-  msum += __shfl_xor(msum, 16);
-  msum += __shfl_xor(msum, 32);
-  if (rw == 0) {
+  for (int e = 0; e < 8; ++e) acc[e] += dpp_move<0x128>(acc[e]);  // row_ror:8
+  msum += dpp_move<0x128>(msum);
+  __shared__ float mred[NW * 4];
+  if ((lane & 8) == 0) {
+    const int r = wave * 4 + (lane >> 4);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[wave][8 * ch + e] = acc[e];
-    if (ch == 0) mred[wave] = msum;
+    for (int e = 0; e < 8; ++e) red[r][8 * ch + e] = acc[e];
+    if (ch == 0) mred[r] = msum;
   }
   __syncthreads();  // every cache read of this (n, h) is complete past here
   if (tid < 64) {
-    const float o = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
-    const float m = mred[0] + mred[1] + mred[2] + mred[3];
+    float o = 0.f, m = 0.f;
+#pragma unroll
+    for (int r = 0; r < NW * 4; ++r) {
+      o += red[r][tid];
+      m += mred[r];
+    }
     float inv = 1.f;
     if (p.flags & TENSION_NORM_MASS) inv = 1.f / (m > kMassEps ? m : kMassEps);
     bf16* orow = (bf16*)p.out.p + n * p.out.s0 + h * p.out.s1;
     orow[tid] = (bf16)(o * inv);
-  } else if (tid < 64 + 16) {
+  } else if (ai < 16) {
     // append k_new / v_new at slot pos % W (8 lanes x 16 bytes each)
-    const int i = tid - 64;
     const int slot = pos % W;
-    if (i < 8) {
-      const bf16* src = (const bf16*)p.kn.p + n * p.kn.s0 + h * p.kn.s1;
+    if (ai < 8) {
       bf16* dst = (bf16*)p.kc.p + n * p.kc.s0 + h * p.kc.s1 + (int64_t)slot * p.kc.s2;
-      *(u16x8*)(dst + 8 * i) = *(const u16x8*)(src + 8 * i);
+      *(u16x8*)(dst + 8 * ai) = knew;
     } else {
-      const int j = i - 8;
-      const bf16* src = (const bf16*)p.vn.p + n * p.vn.s0 + h * p.vn.s1;
       bf16* dst = (bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1 + (int64_t)slot * p.vc.s2;
-      *(u16x8*)(dst + 8 * j) = *(const u16x8*)(src + 8 * j);
+      *(u16x8*)(dst + 8 * (ai - 8)) = vnew;
     }
-  } else if (tid == 64 + 16 && h == 0 && p.pos_out) {
+  } else if (ai == 16 && h == 0 && p.pos_out) {
     p.pos_out[n] = pos + 1;
   }
 }
@@ -176,7 +212,18 @@ __global__ __launch_bounds__(64) void decode_exact(DecodeParams p) {
 
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err) {
   if (fast) {
-    hipLaunchKernelGGL(decode_bf16_d64, dim3((unsigned)(p.N * p.H)), dim3(kDecThreads), 0, st, p);
+    // fast requires D == 64, W <= 512
+    const dim3 grid((unsigned)(p.N * p.H));
+    if (p.W <= 32)
+      hipLaunchKernelGGL((decode_bf16_d64<4, 1>), grid, dim3(256), 0, st, p);
+    else if (p.W <= 64)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 1>), grid, dim3(512), 0, st, p);
+    else if (p.W <= 128)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 2>), grid, dim3(512), 0, st, p);
+    else if (p.W <= 256)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 4>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((decode_bf16_d64<8, 8>), grid, dim3(512), 0, st, p);
   } else {
     const unsigned grid = (unsigned)((p.N * p.H + 63) / 64);
     if (f64)

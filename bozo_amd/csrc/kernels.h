@@ -12,6 +12,7 @@ struct DecodeParams {
   int32_t* pos_out;
   int N, H, D, W;
   double scale;
+  float inv_scale;  // (float)(1 / scale)
   int flags;
 };
 

@@ -25,6 +25,13 @@ def seq_inputs(N, L, H, D, seed, std=0.5):
 @pytest.mark.parametrize("dtype,D,W,prefill", [
     (torch.bfloat16, 64, 64, 64),     # fast path, warm cache
     (torch.bfloat16, 64, 32, 5),      # fast path, filling cache
+    (torch.bfloat16, 64, 1, 2),       # fast path, one slot (31 rows past W)
+    (torch.bfloat16, 64, 33, 40),     # fast path, rows past W in the last pass
+    (torch.bfloat16, 64, 100, 7),     # fast path, filling, W not a multiple of 32
+    (torch.bfloat16, 64, 160, 170),   # fast path, 4 passes, 96 rows past W
+    (torch.bfloat16, 64, 288, 7),     # fast path, 8 passes
+    (torch.bfloat16, 64, 384, 390),   # fast path, 8 passes
+    (torch.bfloat16, 64, 512, 515),   # fast path, largest window
     (torch.float32, 64, 64, 70),      # exact path
     (torch.bfloat16, 32, 16, 3),      # exact path (D != 64)
 ])
