@@ -50,7 +50,7 @@ SIGNATURES = {
     "tension_window_bwd_dkv": (_i32, [BufP] * 8 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_global_fwd": (_i32, [BufP] * 7 + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_global_bwd_workspace": (_i64, [_i64, _i64, _i64, _i32, _i32]),
-    "tension_global_bwd": (_i32, [BufP] * 9 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
+    "tension_global_bwd": (_i32, [BufP] * 11 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_decode_step": (_i32, [BufP] * 7 + [_vp, _vp] + [_i64] * 4 + [_f64, _i32, _vp]),
     "tension_rope": (_i32, [BufP, BufP, _vp, _vp] + [_i64] * 6 + [_i32, _vp]),
     "tension_last_error": (ctypes.c_char_p, []),

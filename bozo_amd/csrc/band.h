@@ -22,6 +22,8 @@ struct BandParams {
   Buf out, tau, bias, mass;
   Buf dout, dtau, dq, dk, dv;
   void* ws;       // backward workspace: acc-typed a[B*T*H], c[B*T*H]
+  int coef_pre;   // tau-mass backward: a, c computed from the saved out / mass
+                  // rows (p.out, p.mass) instead of a pass over the band
   int B, T, H, D;
   int win, diag, glob;
   int W;          // local window (count normalisation)

@@ -226,7 +226,8 @@ BandParams bwd_params(const tension_buf* q, const tension_buf* k, const tension_
 
 int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
                 const tension_buf* dtau, const tension_buf* bias, const tension_buf* dq, void* ws, Shape sh,
-                int64_t Wparam, double scale, int32_t flags, tension_stream_t stream, bool global) {
+                int64_t Wparam, double scale, int32_t flags, tension_stream_t stream, bool global,
+                const tension_buf* out = nullptr, const tension_buf* mass = nullptr) {
   bool empty = false;
   TRY(check_bwd(q, k, v, dout, dtau, bias, sh, Wparam, scale, flags, ws, global, &empty));
   if (empty) return ok();
@@ -234,6 +235,15 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
   BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, Wparam, scale, flags, global);
   p.dq = make_buf(dq);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dq, nullptr, sh.D, flags);
+  if (mf && out && mass) {
+    TRY(check_buf(out, "out", true, 3));
+    TRY(check_buf(mass, "mass", true, -1));
+    if (aligned_bf16_rows(out) && mass->dtype == TENSION_F32) {
+      p.out = make_buf(out);
+      p.mass = make_buf(mass);
+      p.coef_pre = 1;
+    }
+  }
   return run_band(1, mf, any_f64(q, k, v), p, stream, global ? "tension_global_bwd(dq)" : "tension_window_bwd_dq");
 }
 
@@ -326,11 +336,12 @@ int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H, int32_t dt
 }
 
 int tension_global_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                       const tension_buf* dtau_local, const tension_buf* bias, const tension_buf* dq,
-                       const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H,
-                       int64_t D, int64_t Wl, double scale, int32_t flags, tension_stream_t stream) {
+                       const tension_buf* dtau_local, const tension_buf* bias, const tension_buf* out,
+                       const tension_buf* mass, const tension_buf* dq, const tension_buf* dk,
+                       const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H, int64_t D, int64_t Wl,
+                       double scale, int32_t flags, tension_stream_t stream) {
   const Shape sh{B, T, H, D};
-  TRY(band_bwd_dq(q, k, v, dout, dtau_local, bias, dq, ws, sh, Wl, scale, flags, stream, true));
+  TRY(band_bwd_dq(q, k, v, dout, dtau_local, bias, dq, ws, sh, Wl, scale, flags, stream, true, out, mass));
   return band_bwd_dkv(q, k, v, dout, dtau_local, bias, dk, dv, ws, sh, Wl, scale, flags, stream, true);
 }
 

@@ -126,6 +126,21 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
 
+// Lane move within a DPP row (bound_ctrl: every source lane of the controls
+// used here exists, so no lane reads the zero fill).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over an aligned group of 8 lanes (all 8 must be active).
+__device__ __forceinline__ float row_sum8(float x) {
+  x += dpp_move<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  x += dpp_move<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  x += dpp_move<0x141>(x);  // row_half_mirror: lane i <-> 7 - i of its 8-lane half-row
+  return x;
+}
+
 __device__ __forceinline__ unsigned short bf16_bits(bf16 x) {
   return __builtin_bit_cast(unsigned short, x);
 }

@@ -28,19 +28,6 @@ __device__ __forceinline__ int ring_w(int slot, int pos, int W) {
 // through DPP lane moves instead of LDS shuffles.
 namespace {
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
-}
-
-// Sum over the aligned group of 8 lanes holding one cache row.
-__device__ __forceinline__ float row_sum8(float x) {
-  x += dpp_move<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
-  x += dpp_move<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
-  x += dpp_move<0x141>(x);  // row_half_mirror: lane i <-> 7 - i of its 8-lane half-row
-  return x;
-}
-
 constexpr int kRawBufWord3 = 0x00020000;  // raw 32-bit data format (buffer descriptor word 3)
 
 // Cache rows are read once per step: non-temporal loads (buffer cache policy

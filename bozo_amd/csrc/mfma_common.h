@@ -58,6 +58,13 @@ __device__ __forceinline__ bf16x8 lds_tr8(const bf16* base, int row, int k0, int
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// Eight bf16 ones (0x3F80): an A operand whose product sums the B column.
+__device__ __forceinline__ bf16x8 ones_bf16x8() {
+  typedef unsigned short u16x8_ __attribute__((ext_vector_type(8)));
+  const u16x8_ one = {0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80};
+  return __builtin_bit_cast(bf16x8, one);
+}
+
 // B operand from two 16-key groups of fp32 C-layout values.
 __device__ __forceinline__ bf16x8 pack_b(const float* lo4, const float* hi4) {
   bf16x8 r;

@@ -12,10 +12,39 @@
 // HOLD: the band of every query spans at most two key blocks (local
 // windows W <= 64): P and dP of both blocks stay in registers and K^T of
 // both blocks in LDS, so one pass computes the coefficients and then G.
-// Otherwise the tau-mass coefficients come from a first pass over the band.
+// Otherwise the tau-mass coefficients come from a first pass over the band,
+// or (coef_pre) from the saved forward rows by coef_from_out.
 #include "mfma_common.h"
 
 namespace tension {
+
+// Tau-mass coefficients from the forward's saved rows: out_t = msg_t / m'_t
+// with m'_t = max(m_t, eps), so a_t = 1 / m'_t and
+//   c_t = sum_s P dP / m'_t^2 = (dO_t . msg_t) / m'_t^2 = (dO_t . out_t) * a_t
+// (0 when m_t < eps, as in the band pass).  Eight lanes per (b, t, h) row, 16
+// bytes of out and dO each; the grid covers whole 8-lane groups, so a group
+// is either fully inside [0, B*T*H) or fully outside.
+__global__ __launch_bounds__(256) void coef_from_out(BandParams p) {
+  const int64_t n = (int64_t)p.B * p.T * p.H;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;  // (b*T + t)*H + h
+  const int ch = threadIdx.x & 7;
+  if (row >= n) return;
+  const int h = (int)(row % p.H);
+  const int64_t bt = row / p.H;
+  const int t = (int)(bt % p.T), b = (int)(bt / p.T);
+  const bf16x8 o = load8((const bf16*)p.out.p + b * p.out.s0 + (int64_t)t * p.out.s1 + h * p.out.s2 + 8 * ch);
+  const bf16x8 d = load8((const bf16*)p.dout.p + b * p.dout.s0 + (int64_t)t * p.dout.s1 + h * p.dout.s2 + 8 * ch);
+  float dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dot += (float)o[e] * (float)d[e];
+  dot = row_sum8(dot);
+  if (ch == 0) {
+    const float m = ld<float>(p.mass, b * p.mass.s0 + (int64_t)t * p.mass.s1 + h * p.mass.s2);
+    const float a = 1.f / (m > kMassEps ? m : kMassEps);
+    ((float*)p.ws)[row] = a;
+    ((float*)p.ws)[n + row] = m >= kMassEps ? dot * a : 0.f;
+  }
+}
 
 __device__ __forceinline__ void scores_block(const bf16* Ks, const bf16* Vs, const bf16x8* qf,
                                              const bf16x8* gf, int g, int c, f32x4* s, f32x4* dp) {
@@ -171,7 +200,13 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandParams p) {
     for (int blk = 0; blk < 2; ++blk)
       if (blk < nblk) grad_block(kb_first + blk * kTile, pv[blk], dpv[blk], Kt[blk & (NKT - 1)]);
   } else {
-    if (NORM == NORM_MASS_) {
+    if (NORM == NORM_MASS_ && p.coef_pre) {
+      if (qok) {
+        const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
+        ca = ((const float*)p.ws)[wi];
+        cc = ((const float*)p.ws)[(int64_t)p.B * p.T * p.H + wi];
+      }
+    } else if (NORM == NORM_MASS_) {
       float msum = 0.f, dsum = 0.f;
       for (int kb0 = kb_first; kb0 <= s_hi; kb0 += kTile) {
         __syncthreads();
@@ -241,6 +276,10 @@ void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm)
   const bool bias = p.bias.p != nullptr, dtau = p.dtau.p != nullptr;
   // every query tile's band spans <= 2 key blocks iff the window is <= 64
   const bool hold = !p.glob && p.win <= kTile;
+  if (norm == NORM_MASS_ && !hold && p.coef_pre) {
+    const int64_t threads = (int64_t)p.B * p.T * p.H * 8;
+    hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, p);
+  }
   switch (norm) {
     case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, dtau, hold); break;
     case NORM_COUNT_: go_n<NORM_COUNT_>(p, st, nwg, bias, dtau, false); break;

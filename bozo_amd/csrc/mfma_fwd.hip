@@ -26,11 +26,17 @@
 
 namespace tension {
 
-template <bool BIAS, bool TAU>
+// MMA_MASS: the tau mass comes from the P.V product itself -- one more MFMA
+// per 32 keys with an all-ones A operand sums the bf16-rounded P that the
+// output is built from, so out = msg / mass holds exactly for the weights
+// used (the tau-mass backward takes its coefficients from out and mass).
+// The per-lane sum (msum, reduced over the lane groups afterwards) is used
+// otherwise.
+template <bool BIAS, bool TAU, bool MMA_MASS = false>
 __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, const bf16* Vs, int kb0,
                                           const WaveBand& wb, int lo, int hi, int b, int h, int tq,
                                           int g, int c, const bf16x8* qf, float k2, f32x4* acc,
-                                          float& msum) {
+                                          float& msum, f32x4* macc = nullptr) {
   float pr[4][4];
   int kind[4];
 #pragma unroll
@@ -60,7 +66,7 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
         const int col = tau_col(p, tq, key);
         if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), pv);
       }
-      msum += pv;
+      if (!MMA_MASS) msum += pv;
       pr[j][r] = pv;
     }
   }
@@ -70,13 +76,16 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
     const bf16x8 pb = pack_b(pr[2 * kk], pr[2 * kk + 1]);
 #pragma unroll
     for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Vs, m, 32 * kk, g, c), pb, acc[m]);
+    if (MMA_MASS) *macc = mfma(ones_bf16x8(), pb, *macc);
   }
 }
 
+// msum: this lane's partial tau mass (reduced over the lane groups here), or
+// with `summed` the full mass already.
 template <int NORM, bool TAU>
 __device__ __forceinline__ void fwd_epilogue(const BandParams& p, int b, int h, int tq, int g,
-                                             const f32x4* acc, float msum) {
-  msum = wave_sum_g(msum);
+                                             const f32x4* acc, float msum, bool summed = false) {
+  if (!summed) msum = wave_sum_g(msum);
   if (tq >= p.T) return;
   bf16* orow = (bf16*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
   store_row4x4(orow, acc, out_factor<NORM>(msum, tq, p.W), g);
@@ -245,19 +254,21 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd(BandParams p) {
   if (tq >= T) { qf[0] = bf16x8{}; qf[1] = bf16x8{}; }
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 acc[4] = {};
+  f32x4 macc = {};
   float msum = 0.f;
   for (int blk = 0; blk < nblk; ++blk) {
     const int kb0 = kb_first + blk * kTile;
     if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
     __syncthreads();
-    fwd_block<BIAS, TAU>(p, Kb[blk & 1], Vb[blk & 1], kb0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
+    fwd_block<BIAS, TAU, true>(p, Kb[blk & 1], Vb[blk & 1], kb0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum,
+                               &macc);
     if (blk + 2 < nblk) {
       __syncthreads();  // every wave is done with this ring slot
       tile_async(kb_, p.k.s1, kb0 + 2 * kTile, T, Kb[blk & 1], wave, lane);
       tile_async(vb_, p.v.s1, kb0 + 2 * kTile, T, Vb[blk & 1], wave, lane);
     }
   }
-  fwd_epilogue<NORM, TAU>(p, b, h, tq, g, acc, msum);
+  fwd_epilogue<NORM, TAU>(p, b, h, tq, g, acc, macc[0], true);
 }
 
 // ------------------------------------------------------------------ launch

@@ -113,7 +113,7 @@ class _CausalTensionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        Q, K, V, Bias = ctx.saved_tensors
+        Q, K, V, Bias, out, mass = ctx.saved_tensors
         B, T, H, D = Q.shape
         dOut = _rows(grads[0])
         dTau = _rows(grads[1]) if ctx.return_tau else None
@@ -177,11 +177,14 @@ class _GlobalTensionFn(torch.autograd.Function):
         Wl = 0 if W_local is None else min(int(W_local), T)
         tl = torch.empty(B, T, H, Wl, dtype=Q.dtype, device=Q.device) if Wl > 0 else None
         out = torch.empty_like(Q)
+        # the tau mass per query, kept with the output so the backward gets
+        # its per-query coefficients from these rows (no band recompute)
+        mass = torch.empty(B, T, H, dtype=torch.float32, device=Q.device)
         with torch.cuda.device(Q.device):
             L.check(L.lib().tension_global_fwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), None,
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), L.buf(mass),
                 B, T, H, D, Wl, float(scale), 0, _stream(Q)), "tension_global_fwd")
-        ctx.save_for_backward(Q, K, V, Bias)
+        ctx.save_for_backward(Q, K, V, Bias, out, mass)
         ctx.scale, ctx.Wl = scale, Wl
         if tl is not None:
             return out, tl
@@ -189,7 +192,7 @@ class _GlobalTensionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        Q, K, V, Bias = ctx.saved_tensors
+        Q, K, V, Bias, out, mass = ctx.saved_tensors
         B, T, H, D = Q.shape
         dOut = _rows(grads[0])
         if dOut is None:
@@ -200,8 +203,8 @@ class _GlobalTensionFn(torch.autograd.Function):
         ws = _ws(lib.tension_global_bwd_workspace(B, T, H, _acc_code(Q, K, V), 0), Q.device)
         with torch.cuda.device(Q.device):
             L.check(lib.tension_global_bwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias),
-                L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.Wl,
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias), L.buf(out),
+                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.Wl,
                 float(ctx.scale), 0, _stream(Q)), "tension_global_bwd")
         return dQ, dK, dV, None, None, None
 

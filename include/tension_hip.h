@@ -156,10 +156,16 @@ int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H,
 
 /* Backward of tension_global_fwd: dout (grad of out), dtau_local
  * (nullable, grad of tau_local [B,T,H,Wl]); recomputes tau like the local
- * backward.  workspace: tension_global_bwd_workspace() bytes (required). */
+ * backward.  workspace: tension_global_bwd_workspace() bytes (required).
+ *   out, mass (nullable, in): the forward's output and mass.  When both are
+ *   given (bf16 out, f32 mass, the bf16 head-dim-64 kernels), the per-query
+ *   coefficients 1/m_t and dO_t.out_t/m_t come from one pass over these rows
+ *   instead of a recompute of the whole causal band; otherwise they are
+ *   ignored and the band is recomputed. */
 int tension_global_bwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* v, const tension_buf* dout,
                        const tension_buf* dtau_local, const tension_buf* bias,
+                       const tension_buf* out, const tension_buf* mass,
                        const tension_buf* dq, const tension_buf* dk,
                        const tension_buf* dv, void* workspace, int64_t B,
                        int64_t T, int64_t H, int64_t D, int64_t Wl,

@@ -90,3 +90,36 @@ def test_gradcheck_float64(dev):
         return global_tension(q, k, v, math.sqrt(D), bias=bias, W_local=5)
 
     assert torch.autograd.gradcheck(fn, (Q, K, V), eps=1e-6, atol=1e-6, rtol=1e-5)
+
+
+def test_backward_saved_rows_match_band_recompute(dev):
+    """tension_global_bwd given the forward's out and mass rows (tau-mass
+    coefficients from one pass over those rows) and without them (band
+    recompute): both against the oracle and against each other (bf16, d64)."""
+    from bozo_amd import _lib as L
+    B, H, T, D = 2, 3, 200, 64
+    inp = make_inputs(B, T, H, D, seed=5, std=0.5, dtype=torch.bfloat16, rope=False)
+    Q, K, V, dO = (inp[n].to(dev).contiguous() for n in ("Q", "K", "V", "dO"))
+    dO = dO.to(torch.bfloat16)
+    out = torch.empty_like(Q)
+    mass = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    lib = L.lib()
+    L.check(lib.tension_global_fwd(L.buf(Q), L.buf(K), L.buf(V), L.buf(out), None, None, L.buf(mass),
+                                   B, T, H, D, 0, 8.0, 0, L.stream_handle()), "fwd")
+    ws = torch.empty(lib.tension_global_bwd_workspace(B, T, H, L.F32, 0), dtype=torch.uint8, device=dev)
+    grads = {}
+    for name, o, m in (("saved", out, mass), ("band", None, None)):
+        g = [torch.empty_like(Q) for _ in range(3)]
+        L.check(lib.tension_global_bwd(L.buf(Q), L.buf(K), L.buf(V), L.buf(dO), None, None, L.buf(o), L.buf(m),
+                                       L.buf(g[0]), L.buf(g[1]), L.buf(g[2]), ws.data_ptr(), B, T, H, D, 0,
+                                       8.0, 0, L.stream_handle()), name)
+        torch.cuda.synchronize()
+        grads[name] = g
+    ref = O.global_backward(f64(inp["Q"]), f64(inp["K"]), f64(inp["V"]), 8.0, f64(dO.cpu()), None, None)
+    for i, n in enumerate(("dQ", "dK", "dV")):
+        for route in ("saved", "band"):
+            err = rel_l2(f64(grads[route][i]), ref[i])
+            assert err <= 2e-2, f"{route} {n}: {err:.3e}"
+        assert rel_l2(f64(grads["saved"][i]), f64(grads["band"][i])) <= 1e-2, n
+    mo, _, _ = O.global_forward(f64(inp["Q"]), f64(inp["K"]), f64(inp["V"]), 8.0, None, None)
+    assert rel_l2(f64(out), mo) <= 2e-2
