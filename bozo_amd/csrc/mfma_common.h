@@ -138,6 +138,14 @@ __device__ __forceinline__ float sigmoid_scaled(float s, float k2, float bias2) 
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(s, k2, bias2)));
 }
 
+// B-operand fragments (features 8g..8g+7 and 32+8g..) of query row tq; rows
+// past T read row T-1.
+__device__ __forceinline__ void load_qfrag(const bf16* qb_, int64_t rs, int tq, int T, int g, bf16x8* qf) {
+  const int tr = tq < T ? tq : T - 1;
+  qf[0] = load8(qb_ + (int64_t)tr * rs + 8 * g);
+  qf[1] = load8(qb_ + (int64_t)tr * rs + 32 + 8 * g);
+}
+
 // Per-query normalisation factor of the forward output.
 template <int NORM>
 __device__ __forceinline__ float out_factor(float msum, int t, int W) {

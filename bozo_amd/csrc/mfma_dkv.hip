@@ -162,8 +162,18 @@ static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, b
   }
 }
 
+void launch_gl_dkv(const BandParams& p, hipStream_t st);
+
 void launch_mfma_dkv(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
   const bool bias = p.bias.p != nullptr, dtau = p.dtau.p != nullptr;
+#ifndef TENSION_NO_GL_BWD
+  // global block: the coefficients are in the workspace whichever way the dQ
+  // phase produced them
+  if (p.glob && !bias && !dtau && norm == NORM_MASS_) {
+    launch_gl_dkv(p, st);
+    return;
+  }
+#endif
   switch (norm) {
     case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, dtau); break;
     case NORM_COUNT_: go_n<NORM_COUNT_>(p, st, nwg, bias, dtau); break;

@@ -272,6 +272,8 @@ static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, b
   if (hold) go_h<NORM, true>(p, st, nwg, bias, dtau); else go_h<NORM, false>(p, st, nwg, bias, dtau);
 }
 
+void launch_gl_dq(const BandParams& p, hipStream_t st);
+
 void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
   const bool bias = p.bias.p != nullptr, dtau = p.dtau.p != nullptr;
   // every query tile's band spans <= 2 key blocks iff the window is <= 64
@@ -279,6 +281,12 @@ void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm)
   if (norm == NORM_MASS_ && !hold && p.coef_pre) {
     const int64_t threads = (int64_t)p.B * p.T * p.H * 8;
     hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, p);
+#ifndef TENSION_NO_GL_BWD
+    if (p.glob && !bias && !dtau) {
+      launch_gl_dq(p, st);
+      return;
+    }
+#endif
   }
   switch (norm) {
     case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, dtau, hold); break;

@@ -132,12 +132,6 @@ __device__ __forceinline__ void fwd_store(const BandParams& p, int b, int h, int
   if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)o.tq * p.mass.s1 + h * p.mass.s2, o.msum);
 }
 
-__device__ __forceinline__ void load_qfrag(const bf16* qb_, int64_t rs, int tq, int T, int g, bf16x8* qf) {
-  const int tr = tq < T ? tq : T - 1;
-  qf[0] = load8(qb_ + (int64_t)tr * rs + 8 * g);
-  qf[1] = load8(qb_ + (int64_t)tr * rs + 32 + 8 * g);
-}
-
 // ------------------------------------------------------------------ ring kernel (W <= 64)
 
 template <int NORM, bool BIAS, bool TAU>
@@ -292,8 +286,16 @@ static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, b
   }
 }
 
+void launch_gl_fwd(const BandParams& p, hipStream_t st);
+
 void launch_mfma_fwd(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
   const bool bias = p.bias.p != nullptr, tau = p.tau.p != nullptr;
+#ifndef TENSION_NO_GL_FWD
+  if (p.glob && !bias && !tau && norm == NORM_MASS_) {
+    launch_gl_fwd(p, st);
+    return;
+  }
+#endif
   const bool ring = !p.glob && p.win <= kTile && p.chunk > 0;
   switch (norm) {
     case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, tau, ring); break;

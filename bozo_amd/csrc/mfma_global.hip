@@ -1,0 +1,470 @@
+// bf16 MFMA forward of the global block (full causal, diagonal included,
+// tau-mass normalised; model.py:217-238), head dim 64, no bias / tau_local.
+//
+// The block is MFMA-shaped (T x T causal) and its per-score VALU work (the
+// sigmoid: one multiply, exp2, add, rcp, bf16 pack) outweighs the MFMA work,
+// so the kernel is laid out to keep both units fed:
+//   * a workgroup owns a 64-query tile and streams the key blocks 0 .. tile
+//     through a two-deep LDS ring (global_load_lds);
+//   * wave w takes query half qh = w & 1 (32 queries, two 16-row MFMA tiles)
+//     against key half kh = w >> 1 (32 keys) of every 64-key block, so every
+//     K and V^T fragment read from LDS feeds two MFMAs;
+//   * only the diagonal block is masked (key <= query); every earlier block
+//     lies wholly inside every query's band;
+//   * the tau mass comes from the P.V product (an all-ones A operand), i.e.
+//     it sums exactly the bf16 P the output is built from;
+//   * the two key halves of a query half meet once, through LDS, at the end.
+// Workgroups go out heaviest tile first; blockIdx -> (b, h) keeps every tile
+// of one (b, h) on one XCD (round-robin dispatch, B*H a multiple of 8), so its
+// 512 KB of K/V stays in that XCD's L2.
+#include "mfma_common.h"
+
+namespace tension {
+
+#ifndef TENSION_GL_FWD_WPE
+#define TENSION_GL_FWD_WPE 3
+#endif
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_FWD_WPE, 8)))
+void gl_fwd(BandParams p) {
+  // ring slots: K in lds[0..1], V in lds[2..3]; reused for the key-half merge
+  __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
+  bf16(*Kb)[kDTile] = lds;
+  bf16(*Vb)[kDTile] = lds + 2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int qh = wave & 1, kh = wave >> 1;
+  const int BH = p.B * p.H;
+  const int id = (int)blockIdx.x;
+  const int tile = p.ntiles - 1 - id / BH;  // heaviest first
+  const int bh = id % BH;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int t0 = tile * kTile;
+  const int nblk = tile + 1;
+
+  const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+
+  // Q^T fragments of this wave's two query tiles (rows past T read row T-1)
+  bf16x8 qf[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) load_qfrag(qb_, p.q.s1, t0 + 32 * qh + 16 * i + c, T, g, qf[i]);
+  tile_async(kb_, p.k.s1, 0, T, Kb[0], wave, lane);
+  tile_async(vb_, p.v.s1, 0, T, Vb[0], wave, lane);
+  if (nblk > 1) {
+    tile_async(kb_, p.k.s1, kTile, T, Kb[1], wave, lane);
+    tile_async(vb_, p.v.s1, kTile, T, Vb[1], wave, lane);
+  }
+  const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  const bf16x8 ones = ones_bf16x8();
+  f32x4 acc[2][4] = {};
+  f32x4 macc[2] = {};
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
+    __syncthreads();
+    const bf16* Ks = Kb[blk & 1];
+    const bf16* Vs = Vb[blk & 1];
+    // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
+    f32x4 s[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bf16x8 a0 = dt_row8(Ks, 32 * kh + 16 * j + c, g);
+      const bf16x8 a1 = dt_row8(Ks, 32 * kh + 16 * j + c, 4 + g);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f32x4 z = {};
+        z = mfma(a0, qf[i][0], z);
+        s[i][j] = mfma(a1, qf[i][1], z);
+      }
+    }
+    bf16x8 vt[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) vt[m] = dt_tr8(Vs, m, 32 * kh, g, c);
+    const bool diag = blk == tile;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float pr[2][4];
+      const int dq = 32 * qh + 16 * i + c;  // query - t0 (= query - kb0 on the diagonal block)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[i][j][r] * k2));
+          pr[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : pv;
+        }
+      const bf16x8 pb = pack_b(pr[0], pr[1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[i][m] = mfma(vt[m], pb, acc[i][m]);
+      macc[i] = mfma(ones, pb, macc[i]);
+    }
+    if (blk + 2 < nblk) {
+      __syncthreads();  // every wave is done with this ring slot
+      tile_async(kb_, p.k.s1, (blk + 2) * kTile, T, Kb[blk & 1], wave, lane);
+      tile_async(vb_, p.v.s1, (blk + 2) * kTile, T, Vb[blk & 1], wave, lane);
+    }
+  }
+
+  // Key halves meet: wave (qh, kh) keeps query tile i = kh and hands its
+  // partial of tile 1 - kh to its partner (qh, 1 - kh) through LDS:
+  // red[slot][e][lane], slot = 2 qh + kh, 17 floats (16 of O^T, 1 mass).
+  __syncthreads();  // the ring slots are free
+  float* red = (float*)&lds[0][0];  // 4 x 17 x 64 floats = 17 KB of the 32 KB
+  auto give = [&](const f32x4* a, const f32x4& mm) {
+    float* dst = red + (2 * qh + kh) * 17 * 64 + lane;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[(4 * m + r) * 64] = a[m][r];
+    dst[16 * 64] = mm[0];
+  };
+  if (kh == 0) give(acc[1], macc[1]); else give(acc[0], macc[0]);
+  __syncthreads();
+  f32x4 o[4];
+  float m;
+  if (kh == 0) {
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) o[mm] = acc[0][mm];
+    m = macc[0][0];
+  } else {
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) o[mm] = acc[1][mm];
+    m = macc[1][0];
+  }
+  {
+    const float* src = red + (2 * qh + (1 - kh)) * 17 * 64 + lane;
+    m += src[16 * 64];
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[mm][r] += src[(4 * mm + r) * 64];
+  }
+  const int tq = t0 + 32 * qh + 16 * kh + c;
+  if (tq >= T) return;
+  bf16* orow = (bf16*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
+  store_row4x4(orow, o, 1.f / (m > kMassEps ? m : kMassEps), g);
+  if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, m);
+}
+
+// ---------------------------------------------------------------- backward
+//
+// Both backward kernels take the per-query tau-mass coefficients a_t = 1/m_t
+// and c_t = dO_t.out_t / m_t from the workspace (coef_from_out), so
+//   dtau = a_t dP - c_t,   G = dtau * P (1 - P)   (P recomputed in fp32),
+// and use the forward's 2 x 2 wave split (32 queries x 32 keys per wave per
+// 64 x 64 block): every fragment read from LDS feeds two MFMAs, and the two
+// partial sums of an output row meet once, through LDS, at the end.
+
+#ifndef TENSION_GL_BWD_WPE
+#define TENSION_GL_BWD_WPE 2
+#endif
+
+// dQ: query-centric like the forward.  Wave (qh = w & 1, kh = w >> 1):
+//   S^T = K Q^T, dP^T = V dO^T      (A = K / V rows from LDS)
+//   dQ^T += K^T G^T                  (A = K^T read transposed)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_BWD_WPE, 8)))
+void gl_dq(BandParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
+  bf16(*Kb)[kDTile] = lds;
+  bf16(*Vb)[kDTile] = lds + 2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int qh = wave & 1, kh = wave >> 1;
+  const int BH = p.B * p.H;
+  const int id = (int)blockIdx.x;
+  const int tile = p.ntiles - 1 - id / BH;  // heaviest first
+  const int bh = id % BH;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int t0 = tile * kTile;
+  const int nblk = tile + 1;
+
+  const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const bf16* gb_ = (const bf16*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+
+  bf16x8 qf[2][2], gf[2][2];
+  float ca[2], cc[2];
+  const int64_t nws = (int64_t)p.B * p.T * p.H;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int tq = t0 + 32 * qh + 16 * i + c;
+    load_qfrag(qb_, p.q.s1, tq, T, g, qf[i]);
+    load_qfrag(gb_, p.dout.s1, tq, T, g, gf[i]);
+    const int64_t wi = ((int64_t)b * p.T + (tq < T ? tq : T - 1)) * p.H + h;
+    ca[i] = ((const float*)p.ws)[wi];
+    cc[i] = ((const float*)p.ws)[nws + wi];
+  }
+  tile_async(kb_, p.k.s1, 0, T, Kb[0], wave, lane);
+  tile_async(vb_, p.v.s1, 0, T, Vb[0], wave, lane);
+  if (nblk > 1) {
+    tile_async(kb_, p.k.s1, kTile, T, Kb[1], wave, lane);
+    tile_async(vb_, p.v.s1, kTile, T, Vb[1], wave, lane);
+  }
+  const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  f32x4 acc[2][4] = {};
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
+    __syncthreads();
+    const bf16* Ks = Kb[blk & 1];
+    const bf16* Vs = Vb[blk & 1];
+    f32x4 s[2][2], dp[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 32 * kh + 16 * j + c;
+      const bf16x8 k0 = dt_row8(Ks, row, g), k1 = dt_row8(Ks, row, 4 + g);
+      const bf16x8 v0 = dt_row8(Vs, row, g), v1 = dt_row8(Vs, row, 4 + g);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f32x4 z = {};
+        z = mfma(k0, qf[i][0], z);
+        s[i][j] = mfma(k1, qf[i][1], z);
+        f32x4 y = {};
+        y = mfma(v0, gf[i][0], y);
+        dp[i][j] = mfma(v1, gf[i][1], y);
+      }
+    }
+    bf16x8 kt[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) kt[m] = dt_tr8(Ks, m, 32 * kh, g, c);
+    const bool diag = blk == tile;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float gd[2][4];
+      const int dq = 32 * qh + 16 * i + c;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[i][j][r] * k2));
+          const float gv = (dp[i][j][r] * ca[i] - cc[i]) * (x - x * x);
+          gd[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : gv;
+        }
+      const bf16x8 pb = pack_b(gd[0], gd[1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[i][m] = mfma(kt[m], pb, acc[i][m]);
+    }
+    if (blk + 2 < nblk) {
+      __syncthreads();
+      tile_async(kb_, p.k.s1, (blk + 2) * kTile, T, Kb[blk & 1], wave, lane);
+      tile_async(vb_, p.v.s1, (blk + 2) * kTile, T, Vb[blk & 1], wave, lane);
+    }
+  }
+
+  // key halves meet (as in the forward): 16 floats per lane
+  __syncthreads();
+  float* red = (float*)&lds[0][0];
+  auto give = [&](const f32x4* a) {
+    float* dst = red + (2 * qh + kh) * 16 * 64 + lane;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[(4 * m + r) * 64] = a[m][r];
+  };
+  if (kh == 0) give(acc[1]); else give(acc[0]);
+  __syncthreads();
+  f32x4 o[4];
+  if (kh == 0) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) o[m] = acc[0][m];
+  } else {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) o[m] = acc[1][m];
+  }
+  const float* src = red + (2 * qh + (1 - kh)) * 16 * 64 + lane;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[m][r] += src[(4 * m + r) * 64];
+  const int tq = t0 + 32 * qh + 16 * kh + c;
+  if (tq >= T) return;
+  bf16* drow = (bf16*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2;
+  store_row4x4(drow, o, (float)(1.0 / p.scale), g);
+}
+
+// dK / dV: key-centric.  A workgroup owns a 64-key tile and streams the
+// query blocks tile .. ntiles-1 (Q and dO through a two-deep LDS ring, the
+// block's a_t / c_t through a small LDS ring).  Wave (kh = w & 1, qh = w >> 1):
+//   S = Q K^T, dP = dO V^T            (A = Q / dO rows from LDS, B = this
+//                                      wave's K / V fragments)
+//   dV^T += dO^T (a P),  dK^T += Q^T G  (A = dO^T / Q^T read transposed)
+// Query rows past T get a = c = 0, which zeroes their P and G.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_BWD_WPE, 8)))
+void gl_dkv(BandParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
+  __shared__ __attribute__((aligned(16))) float coef[2][2][kTile];  // [slot][a, c][query]
+  bf16(*Qb)[kDTile] = lds;
+  bf16(*Gb)[kDTile] = lds + 2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int kh = wave & 1, qh = wave >> 1;
+  const int BH = p.B * p.H;
+  const int id = (int)blockIdx.x;
+  const int tile = id / BH;  // key tile 0 sees every query block: heaviest first
+  const int bh = id % BH;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int k0 = tile * kTile;
+  const int nblk = p.ntiles - tile;
+
+  const bf16* qb_ = (const bf16*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const bf16* kb_ = (const bf16*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const bf16* gb_ = (const bf16*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  const int64_t nws = (int64_t)p.B * p.T * p.H;
+  const float* wsf = (const float*)p.ws;
+
+  // K / V fragments (B operands) of this wave's two key tiles
+  bf16x8 kf[2][2], vf[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int tk = k0 + 32 * kh + 16 * i + c;
+    load_qfrag(kb_, p.k.s1, tk, T, g, kf[i]);
+    load_qfrag(vb_, p.v.s1, tk, T, g, vf[i]);
+  }
+  // coefficient of query block qb for thread tid < 128 (a for tid < 64, c
+  // for 64..127); 0 past T
+  auto coef_load = [&](int qb) -> float {
+    const int t = qb * kTile + (tid & 63);
+    if (tid >= 128 || t >= T) return 0.f;
+    const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
+    return wsf[(tid >> 6) * nws + wi];
+  };
+  const int q_first = tile;  // query blocks tile .. ntiles-1
+  if (tid < 128) coef[0][tid >> 6][tid & 63] = coef_load(q_first);
+  float cnext = nblk > 1 ? coef_load(q_first + 1) : 0.f;
+  tile_async(qb_, p.q.s1, q_first * kTile, T, Qb[0], wave, lane);
+  tile_async(gb_, p.dout.s1, q_first * kTile, T, Gb[0], wave, lane);
+  if (nblk > 1) {
+    tile_async(qb_, p.q.s1, (q_first + 1) * kTile, T, Qb[1], wave, lane);
+    tile_async(gb_, p.dout.s1, (q_first + 1) * kTile, T, Gb[1], wave, lane);
+  }
+  const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  f32x4 dk[2][4] = {}, dv[2][4] = {};
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
+    __syncthreads();
+    // slot (blk + 1) & 1 was last read in block blk - 1: free past the barrier
+    if (blk + 1 < nblk && tid < 128) coef[(blk + 1) & 1][tid >> 6][tid & 63] = cnext;
+    if (blk + 2 < nblk) cnext = coef_load(q_first + blk + 2);
+    const bf16* Qs = Qb[blk & 1];
+    const bf16* Gs = Gb[blk & 1];
+    f32x4 s[2][2], dp[2][2];  // [query tile j][key tile i]
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 32 * qh + 16 * j + c;
+      const bf16x8 q0 = dt_row8(Qs, row, g), q1 = dt_row8(Qs, row, 4 + g);
+      const bf16x8 d0 = dt_row8(Gs, row, g), d1 = dt_row8(Gs, row, 4 + g);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f32x4 z = {};
+        z = mfma(q0, kf[i][0], z);
+        s[j][i] = mfma(q1, kf[i][1], z);
+        f32x4 y = {};
+        y = mfma(d0, vf[i][0], y);
+        dp[j][i] = mfma(d1, vf[i][1], y);
+      }
+    }
+    // a / c of queries 32 qh + 16 j + 4 g + r
+    f32x4 a4[2], c4[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      a4[j] = *(const f32x4*)&coef[blk & 1][0][32 * qh + 16 * j + 4 * g];
+      c4[j] = *(const f32x4*)&coef[blk & 1][1][32 * qh + 16 * j + 4 * g];
+    }
+    bf16x8 qt[4], gt[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      qt[m] = dt_tr8(Qs, m, 32 * qh, g, c);
+      gt[m] = dt_tr8(Gs, m, 32 * qh, g, c);
+    }
+    const bool diag = blk == 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float pa[2][4], gd[2][4];
+      const int dk_ = 32 * kh + 16 * i + c;  // key - k0 (= key - q0 on the diagonal block)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[j][i][r] * k2));
+          const bool off = diag && 32 * qh + 16 * j + 4 * g + r < dk_;  // query before key
+          pa[j][r] = off ? 0.f : x * a4[j][r];
+          gd[j][r] = off ? 0.f : (dp[j][i][r] * a4[j][r] - c4[j][r]) * (x - x * x);
+        }
+      const bf16x8 pb = pack_b(pa[0], pa[1]);
+      const bf16x8 gbv = pack_b(gd[0], gd[1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        dv[i][m] = mfma(gt[m], pb, dv[i][m]);
+        dk[i][m] = mfma(qt[m], gbv, dk[i][m]);
+      }
+    }
+    if (blk + 2 < nblk) {
+      __syncthreads();
+      tile_async(qb_, p.q.s1, (q_first + blk + 2) * kTile, T, Qb[blk & 1], wave, lane);
+      tile_async(gb_, p.dout.s1, (q_first + blk + 2) * kTile, T, Gb[blk & 1], wave, lane);
+    }
+  }
+
+  // query halves meet: wave (kh, qh) keeps key tile i = qh and hands tile
+  // 1 - qh to its partner (kh, 1 - qh): 32 floats per lane (dK, dV)
+  __syncthreads();
+  float* red = (float*)&lds[0][0];  // 4 x 32 x 64 floats = the whole 32 KB
+  auto give = [&](const f32x4* a, const f32x4* v) {
+    float* dst = red + (2 * kh + qh) * 32 * 64 + lane;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dst[(4 * m + r) * 64] = a[m][r];
+        dst[(16 + 4 * m + r) * 64] = v[m][r];
+      }
+  };
+  if (qh == 0) give(dk[1], dv[1]); else give(dk[0], dv[0]);
+  __syncthreads();
+  f32x4 ok_[4], ov[4];
+  if (qh == 0) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) { ok_[m] = dk[0][m]; ov[m] = dv[0][m]; }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) { ok_[m] = dk[1][m]; ov[m] = dv[1][m]; }
+  }
+  const float* src = red + (2 * kh + (1 - qh)) * 32 * 64 + lane;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ok_[m][r] += src[(4 * m + r) * 64];
+      ov[m][r] += src[(16 + 4 * m + r) * 64];
+    }
+  const int tk = k0 + 32 * kh + 16 * qh + c;
+  if (tk >= T) return;
+  bf16* dkrow = (bf16*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2;
+  bf16* dvrow = (bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2;
+  store_row4x4(dkrow, ok_, (float)(1.0 / p.scale), g);
+  store_row4x4(dvrow, ov, 1.f, g);
+}
+
+void launch_gl_dq(const BandParams& p, hipStream_t st) {
+  const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);
+  hipLaunchKernelGGL(gl_dq, dim3(n), dim3(kThreads), 0, st, p);
+}
+
+void launch_gl_dkv(const BandParams& p, hipStream_t st) {
+  const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);
+  hipLaunchKernelGGL(gl_dkv, dim3(n), dim3(kThreads), 0, st, p);
+}
+
+void launch_gl_fwd(const BandParams& p, hipStream_t st) {
+  const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);
+  hipLaunchKernelGGL(gl_fwd, dim3(n), dim3(kThreads), 0, st, p);
+}
+
+}  // namespace tension
