@@ -216,6 +216,43 @@ __device__ __forceinline__ void tile_async(const bf16* base, int64_t rs, int r0,
   }
 }
 
+// tile_async with the per-lane part of the source address computed once:
+// lane L of wave w copies chunks q_n = (4n + w) * 64 + L (n = 0, 1) of every
+// tile, i.e. row r_n = q_n / 8 and logical chunk c_n = (q_n & 7) ^ dsw(r_n),
+// so its source for the tile at row r0 is p_n + r0 * rs with
+// p_n = base + r_n * rs + 8 c_n.  Rows past T-1 are clamped as tile_async
+// does: row r0 + r_n > T-1 reads row T-1, i.e. p_n + lim_n * rs with
+// lim_n = T-1 - r_n, kept precomputed so the per-tile cost is one select
+// and one 64-bit add (r0 >= 0).
+struct TileSrc {
+  const bf16* p[2];
+  int lim[2];
+  int64_t lim_off[2];
+  int64_t rs;
+};
+
+__device__ __forceinline__ TileSrc tile_src(const bf16* base, int64_t rs, int T, int wave, int lane) {
+  TileSrc s;
+  s.rs = rs;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int q = (n * 4 + wave) * 64 + lane;
+    const int r = q >> 3;
+    s.p[n] = base + (int64_t)r * rs + 8 * ((q & 7) ^ dsw(r));
+    s.lim[n] = T - 1 - r;
+    s.lim_off[n] = (int64_t)s.lim[n] * rs;
+  }
+  return s;
+}
+
+__device__ __forceinline__ void tile_async_src(const TileSrc& s, int r0, bf16* tile, int wave) {
+  const int64_t off = (int64_t)r0 * s.rs;  // uniform
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+    __builtin_amdgcn_global_load_lds((const void*)(s.p[n] + (r0 <= s.lim[n] ? off : s.lim_off[n])),
+                                     (lds_void*)(tile + (n * 4 + wave) * 512), 16, 0, 0);
+}
+
 // Wait until at most n vector-memory operations of this wave are in flight
 // (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at
 // their maximum, i.e. not waited on).

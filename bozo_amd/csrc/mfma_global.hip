@@ -51,11 +51,12 @@ void gl_fwd(BandParams p) {
   bf16x8 qf[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) load_qfrag(qb_, p.q.s1, t0 + 32 * qh + 16 * i + c, T, g, qf[i]);
-  tile_async(kb_, p.k.s1, 0, T, Kb[0], wave, lane);
-  tile_async(vb_, p.v.s1, 0, T, Vb[0], wave, lane);
+  const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
+  tile_async_src(ksrc, 0, Kb[0], wave);
+  tile_async_src(vsrc, 0, Vb[0], wave);
   if (nblk > 1) {
-    tile_async(kb_, p.k.s1, kTile, T, Kb[1], wave, lane);
-    tile_async(vb_, p.v.s1, kTile, T, Vb[1], wave, lane);
+    tile_async_src(ksrc, kTile, Kb[1], wave);
+    tile_async_src(vsrc, kTile, Vb[1], wave);
   }
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   const bf16x8 ones = ones_bf16x8();
@@ -102,8 +103,8 @@ void gl_fwd(BandParams p) {
     }
     if (blk + 2 < nblk) {
       __syncthreads();  // every wave is done with this ring slot
-      tile_async(kb_, p.k.s1, (blk + 2) * kTile, T, Kb[blk & 1], wave, lane);
-      tile_async(vb_, p.v.s1, (blk + 2) * kTile, T, Vb[blk & 1], wave, lane);
+      tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
+      tile_async_src(vsrc, (blk + 2) * kTile, Vb[blk & 1], wave);
     }
   }
 
@@ -157,14 +158,17 @@ void gl_fwd(BandParams p) {
 // 64 x 64 block): every fragment read from LDS feeds two MFMAs, and the two
 // partial sums of an output row meet once, through LDS, at the end.
 
-#ifndef TENSION_GL_BWD_WPE
-#define TENSION_GL_BWD_WPE 2
+#ifndef TENSION_GL_DQ_WPE
+#define TENSION_GL_DQ_WPE 2
+#endif
+#ifndef TENSION_GL_DKV_WPE
+#define TENSION_GL_DKV_WPE 2
 #endif
 
 // dQ: query-centric like the forward.  Wave (qh = w & 1, kh = w >> 1):
 //   S^T = K Q^T, dP^T = V dO^T      (A = K / V rows from LDS)
 //   dQ^T += K^T G^T                  (A = K^T read transposed)
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_BWD_WPE, 8)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DQ_WPE, 8)))
 void gl_dq(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
   bf16(*Kb)[kDTile] = lds;
@@ -198,11 +202,12 @@ void gl_dq(BandParams p) {
     ca[i] = ((const float*)p.ws)[wi];
     cc[i] = ((const float*)p.ws)[nws + wi];
   }
-  tile_async(kb_, p.k.s1, 0, T, Kb[0], wave, lane);
-  tile_async(vb_, p.v.s1, 0, T, Vb[0], wave, lane);
+  const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
+  tile_async_src(ksrc, 0, Kb[0], wave);
+  tile_async_src(vsrc, 0, Vb[0], wave);
   if (nblk > 1) {
-    tile_async(kb_, p.k.s1, kTile, T, Kb[1], wave, lane);
-    tile_async(vb_, p.v.s1, kTile, T, Vb[1], wave, lane);
+    tile_async_src(ksrc, kTile, Kb[1], wave);
+    tile_async_src(vsrc, kTile, Vb[1], wave);
   }
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 acc[2][4] = {};
@@ -250,8 +255,8 @@ void gl_dq(BandParams p) {
     }
     if (blk + 2 < nblk) {
       __syncthreads();
-      tile_async(kb_, p.k.s1, (blk + 2) * kTile, T, Kb[blk & 1], wave, lane);
-      tile_async(vb_, p.v.s1, (blk + 2) * kTile, T, Vb[blk & 1], wave, lane);
+      tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
+      tile_async_src(vsrc, (blk + 2) * kTile, Vb[blk & 1], wave);
     }
   }
 
@@ -293,7 +298,7 @@ void gl_dq(BandParams p) {
 //                                      wave's K / V fragments)
 //   dV^T += dO^T (a P),  dK^T += Q^T G  (A = dO^T / Q^T read transposed)
 // Query rows past T get a = c = 0, which zeroes their P and G.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_BWD_WPE, 8)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DKV_WPE, 8)))
 void gl_dkv(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
   __shared__ __attribute__((aligned(16))) float coef[2][2][kTile];  // [slot][a, c][query]
@@ -337,11 +342,12 @@ void gl_dkv(BandParams p) {
   const int q_first = tile;  // query blocks tile .. ntiles-1
   if (tid < 128) coef[0][tid >> 6][tid & 63] = coef_load(q_first);
   float cnext = nblk > 1 ? coef_load(q_first + 1) : 0.f;
-  tile_async(qb_, p.q.s1, q_first * kTile, T, Qb[0], wave, lane);
-  tile_async(gb_, p.dout.s1, q_first * kTile, T, Gb[0], wave, lane);
+  const TileSrc qsrc = tile_src(qb_, p.q.s1, T, wave, lane), gsrc = tile_src(gb_, p.dout.s1, T, wave, lane);
+  tile_async_src(qsrc, q_first * kTile, Qb[0], wave);
+  tile_async_src(gsrc, q_first * kTile, Gb[0], wave);
   if (nblk > 1) {
-    tile_async(qb_, p.q.s1, (q_first + 1) * kTile, T, Qb[1], wave, lane);
-    tile_async(gb_, p.dout.s1, (q_first + 1) * kTile, T, Gb[1], wave, lane);
+    tile_async_src(qsrc, (q_first + 1) * kTile, Qb[1], wave);
+    tile_async_src(gsrc, (q_first + 1) * kTile, Gb[1], wave);
   }
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 dk[2][4] = {}, dv[2][4] = {};
@@ -407,8 +413,8 @@ void gl_dkv(BandParams p) {
     }
     if (blk + 2 < nblk) {
       __syncthreads();
-      tile_async(qb_, p.q.s1, (q_first + blk + 2) * kTile, T, Qb[blk & 1], wave, lane);
-      tile_async(gb_, p.dout.s1, (q_first + blk + 2) * kTile, T, Gb[blk & 1], wave, lane);
+      tile_async_src(qsrc, (q_first + blk + 2) * kTile, Qb[blk & 1], wave);
+      tile_async_src(gsrc, (q_first + blk + 2) * kTile, Gb[blk & 1], wave);
     }
   }
 

@@ -113,7 +113,7 @@ class _CausalTensionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        Q, K, V, Bias, out, mass = ctx.saved_tensors
+        Q, K, V, Bias = ctx.saved_tensors
         B, T, H, D = Q.shape
         dOut = _rows(grads[0])
         dTau = _rows(grads[1]) if ctx.return_tau else None
