@@ -331,8 +331,9 @@ def bench_window(args, dev):
 
 def profile_kernels(n, dev):
     """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
-    of each band kernel on rotated config-2 sets and n config-4 decode steps
-    over 4 rotated caches, then a plain device copy of
+    of each band kernel on rotated config-2 sets, n config-4 decode steps
+    over 4 rotated caches and n config-3 global forward + backward calls, then
+    a plain device copy of
     known size (256 MiB read + 256 MiB written) whose FETCH_SIZE/WRITE_SIZE
     readings calibrate the counters into bytes."""
     from bozo_amd import _lib as L
@@ -361,12 +362,29 @@ def profile_kernels(n, dev):
         caches[i % NC].step(qkv[0][i], qkv[1][i], qkv[2][i])
     torch.cuda.synchronize()
     del caches, qkv
+    # config-3 global block: n forward and n backward calls (the backward runs
+    # coef_from_out, gl_dq and gl_dkv)
+    Bg, Hg, Tg = 4, 12, 2048
+    q, k, v, do = ((torch.randn(Bg, Tg, Hg, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+                   for _ in range(4))
+    out, mass = torch.empty_like(q), torch.empty(Bg, Tg, Hg, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    lib = L.lib()
+    ws = torch.empty(lib.tension_global_bwd_workspace(Bg, Tg, Hg, L.F32, 0), dtype=torch.uint8, device=dev)
+    for _ in range(n):
+        L.check(lib.tension_global_fwd(L.buf(q), L.buf(k), L.buf(v), L.buf(out), None, None, L.buf(mass),
+                                       Bg, Tg, Hg, D, 0, 8.0, 0, L.stream_handle()), "global fwd")
+        L.check(lib.tension_global_bwd(L.buf(q), L.buf(k), L.buf(v), L.buf(do), None, None, L.buf(out),
+                                       L.buf(mass), L.buf(dq), L.buf(dk), L.buf(dv), ws.data_ptr(), Bg, Tg, Hg,
+                                       D, 0, 8.0, 0, L.stream_handle()), "global bwd")
+    torch.cuda.synchronize()
+    del q, k, v, do, out, mass, dq, dk, dv, ws
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"[bench] profile-kernels: {n} launches each of fwd/bwd/dq/dkv and decode, 4 copies of 256 MiB")
+    log(f"[bench] profile-kernels: {n} launches each of fwd/bwd/dq/dkv, decode, global fwd/bwd; 4 copies of 256 MiB")
 
 
 def _phase_regions(cur):
