@@ -163,7 +163,11 @@ __device__ __forceinline__ void store_row4x4(bf16* row, const f32x4* acc, float 
     u16x4 o;
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+#ifdef TENSION_NT_STORES
+    __builtin_nontemporal_store(o, (u16x4*)(row + 16 * m + 4 * g));
+#else
     *(u16x4*)(row + 16 * m + 4 * g) = o;
+#endif
   }
 }
 
@@ -306,6 +310,12 @@ __device__ __forceinline__ TileRegs seq_tile_load(const SeqBuf& s, uint32_t row0
 
 // Four fp32 C-layout rows (features 16m + 4g .. +3, m = 0..3) of one output
 // row, scaled by f, as bf16 at byte offset `row` (dropped past row T-1).
+#ifdef TENSION_NT_STORES
+constexpr int kStoreAux = 2;  // buffer cache policy nt
+#else
+constexpr int kStoreAux = 0;
+#endif
+
 __device__ __forceinline__ void seq_store_row4x4(const SeqBuf& s, uint32_t row, const f32x4* acc, float f,
                                                  int g) {
 #pragma unroll
@@ -313,7 +323,8 @@ __device__ __forceinline__ void seq_store_row4x4(const SeqBuf& s, uint32_t row, 
     u16x4 o;
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), s.r, (int)(row + 2 * (16 * m + 4 * g)), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), s.r, (int)(row + 2 * (16 * m + 4 * g)), 0,
+                                          kStoreAux);
   }
 }
 

@@ -108,9 +108,9 @@ struct OutRow {
 
 template <int NORM, bool TAU>
 __device__ __forceinline__ OutRow fwd_finish(const BandParams& p, int b, int h, int tq, int g, const f32x4* acc,
-                                             float msum) {
+                                             float msum, bool summed = false) {
   OutRow o;
-  o.msum = wave_sum_g(msum);
+  o.msum = summed ? msum : wave_sum_g(msum);
   o.tq = tq;
   const float f = out_factor<NORM>(o.msum, tq, p.W);
 #pragma unroll
@@ -132,9 +132,81 @@ __device__ __forceinline__ void fwd_store(const BandParams& p, int b, int h, int
   if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)o.tq * p.mass.s1 + h * p.mass.s2, o.msum);
 }
 
+// FAST-path output: the wave's 16 x 64 bf16 rows pass through its own 2 KB
+// of a free LDS slot (16-byte chunk k of row r at position k ^ (r & 7)) and
+// leave as whole 128-byte rows, 16 bytes per lane, instead of four 32-byte
+// pieces per row (partial-line writes), with non-temporal stores: the rows
+// are not read again by this kernel, and streaming them out (rather than
+// leaving dirty lines in L2 for the end-of-kernel write-back) measured
+// 16.2 -> 14.0 us at config 2.  LDS operations of one wave execute in order,
+// so the read-back needs no barrier.
+__device__ __forceinline__ void fwd_store_staged(const BandParams& p, int b, int h, int g, int c, int lane, int w,
+                                                 const OutRow& o, bf16* slot) {
+  bf16* sb = slot + w * (16 * kTile);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)  // d = 16m + 4g .. +3: chunk 2m + g/2, half g & 1
+    *(u16x4*)(sb + c * kTile + 8 * ((2 * m + (g >> 1)) ^ (c & 7)) + 4 * (g & 1)) = o.v[m];
+  const int row0 = o.tq - c;  // first query row of the wave
+  bf16* obase = (bf16*)p.out.p + b * p.out.s0 + h * p.out.s2;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int rr = (lane >> 3) + 8 * n, cc = lane & 7;
+    const u16x8 v = *(const u16x8*)(sb + rr * kTile + 8 * (cc ^ (rr & 7)));
+    __builtin_nontemporal_store(v, (u16x8*)(obase + (int64_t)(row0 + rr) * p.out.s1 + 8 * cc));
+  }
+  if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)o.tq * p.mass.s1 + h * p.mass.s2, o.msum);
+}
+
 // ------------------------------------------------------------------ ring kernel (W <= 64)
 
-template <int NORM, bool BIAS, bool TAU>
+// One query tile at W = 64 with T % 64 == 0 (no bias, no tau): the band of
+// wave w (queries t0 + 16w + c) is 16-key sub-blocks s = w .. w+4 of the
+// 128 keys of blocks t-1 (s < 4) and t (s >= 4).  Sub-block w keeps key
+// index kk = 4g + r >= c, sub-block w+4 keeps kk < c, the three between are
+// whole, so the masks are two lane constants (mlo, mhi).  The P.V products
+// run over the sub-block pairs (2 pr, 2 pr + 1), pr = w/2 .. w/2 + 2, with a
+// zero half where the pair sticks out of the band; the tau mass comes from
+// an all-ones A operand (the bf16 P the output is built from).  Sub-blocks
+// of block t-1 are absent on tile 0.  The wave index is a template argument
+// so that every band decision is static.
+template <int w>
+__device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb,
+                                              bool has_prev, int g, int c, const bf16x8* qf, float k2,
+                                              const bool* mlo, const bool* mhi, f32x4* acc, f32x4& macc) {
+  const bf16x8 ones = ones_bf16x8();
+#pragma unroll
+  for (int pi = 0; pi < 3; ++pi) {
+    const int pr = (w >> 1) + pi;  // 0..3
+    if (pr < 2 && !has_prev) continue;
+    const bf16* Kt = pr < 2 ? Ka : Kb;
+    const bf16* Vt = pr < 2 ? Va : Vb;
+    float pv[2][4];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int s5 = 2 * pr + h2 - w;  // position in the band, 0..4
+      if (s5 < 0 || s5 > 4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pv[h2][r] = 0.f;
+        continue;
+      }
+      const int row = 16 * ((2 * pr + h2) & 3) + c;
+      f32x4 z = {};
+      z = mfma(dt_row8(Kt, row, g), qf[0], z);
+      z = mfma(dt_row8(Kt, row, 4 + g), qf[1], z);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z[r] * k2));
+        pv[h2][r] = s5 == 0 ? (mlo[r] ? x : 0.f) : (s5 == 4 ? (mhi[r] ? x : 0.f) : x);
+      }
+    }
+    const bf16x8 pb = pack_b(pv[0], pv[1]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Vt, m, 32 * (pr & 1), g, c), pb, acc[m]);
+    macc = mfma(ones, pb, macc);
+  }
+}
+
+template <int NORM, bool BIAS, bool TAU, bool FAST>
 __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 K0[kDTile];
   __shared__ __attribute__((aligned(16))) bf16 K1[kDTile];
@@ -158,45 +230,82 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
 
   // key block gb (rows 64 gb ..) into a slot pair
+  const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
   auto fetch = [&](int gb, bf16* Kd, bf16* Vd) {
     if (gb >= 0 && gb < p.ntiles) {
-      tile_async(kb_, p.k.s1, gb * kTile, T, Kd, wave, lane);
-      tile_async(vb_, p.v.s1, gb * kTile, T, Vd, wave, lane);
+      tile_async_src(ksrc, gb * kTile, Kd, wave);
+      tile_async_src(vsrc, gb * kTile, Vd, wave);
     }
   };
+  bool mlo[4], mhi[4];  // FAST band masks of the first / last sub-block
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mlo[r] = 4 * g + r >= c;
+    mhi[r] = 4 * g + r < c;
+  }
 
+  // Everything the first two tiles need is requested up front (the third
+  // ring slot is free until tile t_first + 1): Q of both tiles and key
+  // blocks t_first - 1 .. t_first + 1, so a two-tile workgroup makes one
+  // round trip to HBM instead of two.
   bf16x8 qf[2], qn[2];
   load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
   fetch(t_first - 1, K0, V0);
   fetch(t_first, K1, V1);
+  const bool pre = t_first + 1 < t_end;
+  if (pre) {
+    fetch(t_first + 1, K2, V2);
+    load_qfrag(qb_, p.q.s1, (t_first + 1) * kTile + wave * 16 + c, T, g, qn);
+  }
   OutRow pend;             // the previous tile's output, stored after the next wait
   bool has_pend = false;
+  bf16* stage = K2;        // FAST: the slot no block uses in the latest step
 
   // tile t = t_first + lt uses key blocks t-1 (slot lt % 3) and t (slot
-  // (lt+1) % 3); block t+1 goes to slot (lt+2) % 3, freed by tile t-1.
+  // (lt+1) % 3); block t+1 goes to slot (lt+2) % 3, freed by tile t-1
+  // (for lt = 0 it was requested before the loop).
   auto tile_step = [&](int lt, const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb,
                        bf16* Kn, bf16* Vn) -> bool {
     const int t = t_first + lt;
     if (t >= t_end) return false;
-    wait_vm<0>();
+    // lt = 0 with the prefetch: the 4 DMA instructions of block t+1 and the
+    // 2 loads of its Q fragment were issued after block t's, so <= 6 may
+    // still be in flight
+    if (lt == 0 && pre) wait_vm<6>(); else wait_vm<0>();
     __syncthreads();
-    if (has_pend) fwd_store(p, b, h, g, pend);
     const bool more = t + 1 < t_end;
-    if (more) {
+    // FAST (at most two tiles per workgroup): slot Kn receives no block in
+    // this step, and the tile that last read it finished before the barrier
+    if (has_pend) {
+      if (FAST) fwd_store_staged(p, b, h, g, c, lane, wave, pend, Kn); else fwd_store(p, b, h, g, pend);
+    }
+    stage = Kn;
+    if (more && lt > 0) {
       load_qfrag(qb_, p.q.s1, (t + 1) * kTile + wave * 16 + c, T, g, qn);
       fetch(t + 1, Kn, Vn);
     }
     const int t0 = t * kTile;
     const int tq = t0 + wave * 16 + c;
-    const int lo = tq - p.win > 0 ? tq - p.win : 0;
-    const int hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
-    const WaveBand wb = wave_band(p, t0 + wave * 16);
-    // rows past T hold row T-1 (finite) and are masked out entirely
     f32x4 acc[4] = {};
-    float msum = 0.f;
-    if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
-    fwd_block<BIAS, TAU>(p, Kb, Vb, t0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
-    pend = fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, msum);
+    if (FAST) {
+      f32x4 macc = {};
+      switch (wave) {
+        case 0: fwd_tile_fast<0>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        case 1: fwd_tile_fast<1>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        case 2: fwd_tile_fast<2>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        default: fwd_tile_fast<3>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+      }
+      pend = fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, macc[0], true);
+    } else {
+      const int lo = tq - p.win > 0 ? tq - p.win : 0;
+      const int hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
+      const WaveBand wb = wave_band(p, t0 + wave * 16);
+      // rows past T hold row T-1 (finite) and are masked out entirely
+      float msum = 0.f;
+      if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
+      fwd_block<BIAS, TAU>(p, Kb, Vb, t0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
+      pend = fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, msum);
+    }
     has_pend = true;
     if (more) { qf[0] = qn[0]; qf[1] = qn[1]; }
     return true;
@@ -207,7 +316,9 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
     if (!tile_step(lt + 1, K1, V1, K2, V2, K0, V0)) break;
     if (!tile_step(lt + 2, K2, V2, K0, V0, K1, V1)) break;
   }
-  if (has_pend) fwd_store(p, b, h, g, pend);
+  if (has_pend) {
+    if (FAST) fwd_store_staged(p, b, h, g, c, lane, wave, pend, stage); else fwd_store(p, b, h, g, pend);
+  }
 }
 
 // ------------------------------------------------------------------ streaming kernel
@@ -271,7 +382,18 @@ template <int NORM, bool BIAS, bool TAU>
 static void go(const BandParams& p, hipStream_t st, unsigned nwg, bool ring) {
   if (ring) {
     const unsigned n = (unsigned)((int64_t)p.B * p.H * ((p.ntiles + p.chunk - 1) / p.chunk));
-    hipLaunchKernelGGL((mfma_fwd_ring<NORM, BIAS, TAU>), dim3(n), dim3(kThreads), 0, st, p);
+#ifndef TENSION_NO_FAST_FWD
+    // the staged output stores need a free ring slot: at most two tiles per
+    // workgroup
+    if (!BIAS && !TAU && p.win == kTile && p.T % kTile == 0) {
+      BandParams q = p;
+      if (q.chunk > 2) q.chunk = 2;
+      const unsigned nq = (unsigned)((int64_t)q.B * q.H * ((q.ntiles + q.chunk - 1) / q.chunk));
+      hipLaunchKernelGGL((mfma_fwd_ring<NORM, false, false, true>), dim3(nq), dim3(kThreads), 0, st, q);
+      return;
+    }
+#endif
+    hipLaunchKernelGGL((mfma_fwd_ring<NORM, BIAS, TAU, false>), dim3(n), dim3(kThreads), 0, st, p);
   } else {
     hipLaunchKernelGGL((mfma_fwd<NORM, BIAS, TAU>), dim3(nwg), dim3(kThreads), 0, st, p);
   }
