@@ -55,11 +55,21 @@ void mfma_bwd_fused(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Ot[kDTile];     // dO tile of the step
   __shared__ __attribute__((aligned(16))) bf16 XP[kXElems];    // P' = a P
   __shared__ __attribute__((aligned(16))) bf16 XG[kXElems];    // G
+#ifndef TENSION_BWD_DIRECT_STORES
+  __shared__ __attribute__((aligned(16))) bf16 Stg[4 * 16 * kTile];  // per-wave output staging
+#endif
   const int tid = threadIdx.x, lane = tid & 63;
   // the wave index is uniform across the wave; readfirstlane lets the
   // compiler see that, so every branch on it is a scalar branch
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
+  // output rows (dQ, dK, dV): row index `row` of lane c's row
+#ifndef TENSION_BWD_DIRECT_STORES
+  bf16* const stg = Stg + w * (16 * kTile);
+#define STORE_ROWS(view, row, acc_, f_) seq_store_rows_staged(view, row, acc_, f_, g, c, lane, stg)
+#else
+#define STORE_ROWS(view, row, acc_, f_) seq_store_row4x4(view, (row) * (view).rs2, acc_, f_, g)
+#endif
   const int nch = p.chunk;  // runs per (b, h)
   const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
   const int bh = id / nch, run = id % nch;
@@ -200,7 +210,7 @@ void mfma_bwd_fused(BandParams p) {
         dq_pair((w >> 1) + 1, gb[1], gb[2]);
         dq_pair((w >> 1) + 2, gb[3], gb[4]);
       }
-      seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
+      STORE_ROWS(sdq, (uint32_t)tq, acc, inv_scale);
     }
   };
 
@@ -345,7 +355,7 @@ void mfma_bwd_fused(BandParams p) {
           if (kind[1] | kind[2]) dq_pair((w >> 1) + 1, gb[1], gb[2]);
           if (kind[3] | kind[4]) dq_pair((w >> 1) + 2, gb[3], gb[4]);
         }
-        seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
+        STORE_ROWS(sdq, (uint32_t)tq, acc, inv_scale);
       }
     } else {
     // G overwrites dP in place (dpv), P' = a P overwrites P (pv)
@@ -389,7 +399,7 @@ void mfma_bwd_fused(BandParams p) {
         if (kind[1] | kind[2]) dq_pair((w >> 1) + 1, dpv[1], dpv[2]);
         if (kind[3] | kind[4]) dq_pair((w >> 1) + 2, dpv[3], dpv[4]);
       }
-      seq_store_row4x4(sdq, (uint32_t)tq * sdq.rs2, acc, inv_scale, g);
+      STORE_ROWS(sdq, (uint32_t)tq, acc, inv_scale);
     }
     }  // !FAST
     }  // not all live
@@ -438,8 +448,8 @@ void mfma_bwd_fused(BandParams p) {
     }
     if (own_old) {
       const uint32_t tk = (uint32_t)((t - 1) * kTile + 16 * w + c);
-      seq_store_row4x4(sdk, tk * sdk.rs2, dk_old, inv_scale, g);
-      seq_store_row4x4(sdv, tk * sdv.rs2, dv_old, 1.f, g);
+      STORE_ROWS(sdk, tk, dk_old, inv_scale);
+      STORE_ROWS(sdv, tk, dv_old, 1.f);
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -464,9 +474,10 @@ void mfma_bwd_fused(BandParams p) {
   // its own step (no query tile follows it)
   if (tE == tB - 1) {
     const uint32_t tk = (uint32_t)((tB - 1) * kTile + 16 * w + c);
-    seq_store_row4x4(sdk, tk * sdk.rs2, dk_old, inv_scale, g);
-    seq_store_row4x4(sdv, tk * sdv.rs2, dv_old, 1.f, g);
+    STORE_ROWS(sdk, tk, dk_old, inv_scale);
+    STORE_ROWS(sdv, tk, dv_old, 1.f);
   }
+#undef STORE_ROWS
 }
 
 template <int NORM, bool BIAS, bool DTAU, bool FAST>

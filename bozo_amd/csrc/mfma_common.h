@@ -328,6 +328,32 @@ __device__ __forceinline__ void seq_store_row4x4(const SeqBuf& s, uint32_t row, 
   }
 }
 
+// Rows of a wave's 16 x 64 C-layout tile (lane (g, c): row c, features
+// 16m + 4g .. +3) written through the wave's own 2 KB of LDS `sb` (16-byte
+// chunk k of row r at position k ^ (r & 7)) and stored as whole 128-byte
+// rows, 16 bytes per lane, with non-temporal buffer stores (one full line
+// per 8 lanes instead of four 32-byte pieces).  row_c: row index of lane c's
+// row; rows past the view's end are dropped by the range check.  LDS
+// operations of one wave execute in order, so no barrier is needed.
+__device__ __forceinline__ void seq_store_rows_staged(const SeqBuf& s, uint32_t row_c, const f32x4* acc, float f,
+                                                      int g, int c, int lane, bf16* sb) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    u16x4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+    *(u16x4*)(sb + c * kTile + 8 * ((2 * m + (g >> 1)) ^ (c & 7)) + 4 * (g & 1)) = o;
+  }
+  const uint32_t row0 = row_c - (uint32_t)c;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int rr = (lane >> 3) + 8 * n, cc = lane & 7;
+    const u16x8 v = *(const u16x8*)(sb + rr * kTile + 8 * (cc ^ (rr & 7)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), s.r,
+                                           (int)((row0 + rr) * s.rs2 + 16 * cc), 0, 2);
+  }
+}
+
 // Register-staged rows into a direct tile.  Thread tid owns the 16-byte
 // chunk ch = tid % 8 of rows ra = 16 (tid / 64) + (tid / 8) % 8 and ra + 8:
 // wave w stores exactly rows 16w .. 16w+15, and each 16-lane group writes
