@@ -354,6 +354,26 @@ __device__ __forceinline__ void seq_store_rows_staged(const SeqBuf& s, uint32_t 
   }
 }
 
+// As seq_store_rows_staged for a plain pointer: row0 points at the wave's
+// first row (lane c = 0), rs is the row stride in elements, and only rows
+// below nvalid are stored.
+__device__ __forceinline__ void store_rows_staged(bf16* row0, int64_t rs, int nvalid, const f32x4* acc, float f,
+                                                  int g, int c, int lane, bf16* sb) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    u16x4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+    *(u16x4*)(sb + c * kTile + 8 * ((2 * m + (g >> 1)) ^ (c & 7)) + 4 * (g & 1)) = o;
+  }
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int rr = (lane >> 3) + 8 * n, cc = lane & 7;
+    const u16x8 v = *(const u16x8*)(sb + rr * kTile + 8 * (cc ^ (rr & 7)));
+    if (rr < nvalid) __builtin_nontemporal_store(v, (u16x8*)(row0 + rr * rs + 8 * cc));
+  }
+}
+
 // Register-staged rows into a direct tile.  Thread tid owns the 16-byte
 // chunk ch = tid % 8 of rows ra = 16 (tid / 64) + (tid / 8) % 8 and ra + 8:
 // wave w stores exactly rows 16w .. 16w+15, and each 16-lane group writes

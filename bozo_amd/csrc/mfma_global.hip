@@ -142,11 +142,14 @@ void gl_fwd(BandParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[mm][r] += src[(4 * mm + r) * 64];
   }
-  const int tq = t0 + 32 * qh + 16 * kh + c;
-  if (tq >= T) return;
-  bf16* orow = (bf16*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
-  store_row4x4(orow, o, 1.f / (m > kMassEps ? m : kMassEps), g);
-  if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, m);
+  // rows out through the wave's 2 KB of LDS as whole lines (the merge reads
+  // are done past the barrier)
+  const int r0 = t0 + 32 * qh + 16 * kh;  // the wave's first row
+  __syncthreads();
+  store_rows_staged((bf16*)p.out.p + b * p.out.s0 + (int64_t)r0 * p.out.s1 + h * p.out.s2, p.out.s1, T - r0, o,
+                    1.f / (m > kMassEps ? m : kMassEps), g, c, lane, &lds[0][0] + wave * (16 * kTile));
+  const int tq = r0 + c;
+  if (tq < T && p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, m);
 }
 
 // ---------------------------------------------------------------- backward
@@ -285,10 +288,10 @@ void gl_dq(BandParams p) {
   for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[m][r] += src[(4 * m + r) * 64];
-  const int tq = t0 + 32 * qh + 16 * kh + c;
-  if (tq >= T) return;
-  bf16* drow = (bf16*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2;
-  store_row4x4(drow, o, (float)(1.0 / p.scale), g);
+  const int r0 = t0 + 32 * qh + 16 * kh;  // the wave's first row
+  __syncthreads();
+  store_rows_staged((bf16*)p.dq.p + b * p.dq.s0 + (int64_t)r0 * p.dq.s1 + h * p.dq.s2, p.dq.s1, T - r0, o,
+                    (float)(1.0 / p.scale), g, c, lane, &lds[0][0] + wave * (16 * kTile));
 }
 
 // dK / dV: key-centric.  A workgroup owns a 64-key tile and streams the
@@ -450,12 +453,13 @@ void gl_dkv(BandParams p) {
       ok_[m][r] += src[(4 * m + r) * 64];
       ov[m][r] += src[(16 + 4 * m + r) * 64];
     }
-  const int tk = k0 + 32 * kh + 16 * qh + c;
-  if (tk >= T) return;
-  bf16* dkrow = (bf16*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2;
-  bf16* dvrow = (bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2;
-  store_row4x4(dkrow, ok_, (float)(1.0 / p.scale), g);
-  store_row4x4(dvrow, ov, 1.f, g);
+  const int r0 = k0 + 32 * kh + 16 * qh;  // the wave's first row
+  __syncthreads();
+  bf16* sb = &lds[0][0] + wave * (16 * kTile);
+  store_rows_staged((bf16*)p.dk.p + b * p.dk.s0 + (int64_t)r0 * p.dk.s1 + h * p.dk.s2, p.dk.s1, T - r0, ok_,
+                    (float)(1.0 / p.scale), g, c, lane, sb);
+  store_rows_staged((bf16*)p.dv.p + b * p.dv.s0 + (int64_t)r0 * p.dv.s1 + h * p.dv.s2, p.dv.s1, T - r0, ov, 1.f,
+                    g, c, lane, sb);
 }
 
 void launch_gl_dq(const BandParams& p, hipStream_t st) {
