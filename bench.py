@@ -276,7 +276,7 @@ def bench_window(args, dev):
     # for comparison only
     dom = max(("fwd", "bwd"), key=lambda k: per_kernel[k]["us"])
     d = per_kernel[dom]
-    kname = {"fwd": "mfma_fwd", "bwd": "mfma_bwd_fused", "dq": "mfma_bwd_dq", "dkv": "mfma_bwd_dkv"}
+    kname = {"fwd": "mfma_fwd_ring", "bwd": "mfma_bwd_fused", "dq": "mfma_bwd_dq", "dkv": "mfma_bwd_dkv"}
 
     # compulsory HBM bytes of one fwd+bwd: read Q,K,V, write out; read Q,K,V,dO,
     # write dQ,dK,dV
