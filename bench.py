@@ -533,6 +533,64 @@ def bench_decode(dev, reps):
             "traffic": traffic}
 
 
+def bench_model(dev, steps, warmup, aux):
+    """Config 5: one TensionLM-117M training step (random init, bf16
+    autocast, AdamW as train.py:894-902, clip 1.0) on B8 x T1024 token ids
+    ~ U[0, 32768).  ``aux``: the reference default, return_all with tau
+    emitted by every layer and the four aux losses computed (weights 0.01,
+    0.02, 0, 0 as train.py:135-140 -- all four are evaluated there too);
+    otherwise CE only (local layers on the valid-count path, no tau)."""
+    import torch.nn.functional as F
+    from bozo_amd import model as M
+    cfg = M.config_117m(use_triton=True)
+    torch.manual_seed(4)
+    m = M.TensionLM(cfg).to(dev).train()
+    opt = M.configure_adamw(m, lr=3e-4, weight_decay=0.1, fused=True)
+    B, T = 8, 1024
+    g = torch.Generator(device=dev).manual_seed(4)
+    ids = torch.randint(0, cfg.vocab_size, (B, T + 1), device=dev, generator=g)
+    inputs, targets = ids[:, :-1], ids[:, 1:]
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            if aux:
+                logits, hidden, taus = m(inputs, return_all=True)
+            else:
+                logits = m(inputs)
+            loss = F.cross_entropy(logits.reshape(-1, cfg.vocab_size), targets.reshape(-1))
+            if aux:
+                loss = (loss + 0.01 * M.manifold_closure_loss(hidden)
+                        + 0.02 * M.tension_diversity_loss(taus, m.window_groups)
+                        + 0.0 * M.constraint_consistency_loss(taus)
+                        + 0.0 * M.tension_entropy_loss(taus))
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(warmup):
+        loss = step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        loss = step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ms = e0.elapsed_time(e1) / steps
+    res = {"config": "TensionLM-117M training step B8 T1024 bf16 autocast AdamW (config 5), "
+                     + ("aux losses + tau (reference default)" if aux else "CE only"),
+           "ms_per_step": round(ms, 3), "wall_ms_per_step": round(wall, 3),
+           "tokens_per_s": round(B * T / (ms * 1e-3), 1), "params": m.num_params,
+           "final_loss": round(float(loss.item()), 4)}
+    del m, opt
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -568,6 +626,10 @@ def main():
     log("[bench] decode (config 4) ...")
     others.append(bench_decode(dev, 4))
     log(f"[bench] {others[-1]}")
+    for aux in (False, True):
+        log(f"[bench] TensionLM-117M training step (config 5, aux={aux}) ...")
+        others.append(bench_model(dev, 10, 3, aux))
+        log(f"[bench] {others[-1]}")
     result["other_configs"] = others
     if not args.no_cpu:
         log("[bench] CPU baseline ...")

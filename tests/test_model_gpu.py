@@ -1,0 +1,199 @@
+"""TensionLM on the HIP kernels (bozo_amd/model.py) against the reference
+model's semantics.
+
+* float32: the model on the GPU (exact kernels) against the functional
+  float64 restatement of the reference forward (oracle/model_ref.py) on the
+  CPU, same weights: logits, every aux loss and every parameter gradient.
+* bf16 autocast at head_dim 64 (the MFMA kernels): the same GPU model with
+  its tension ops swapped for the reference's torch path computed in float32
+  (oracle/torch_ref.py, autocast off inside, output cast back to the input
+  dtype like the reference op).  Everything else (bf16 linear layers, norms)
+  is the same code on the same weights, so the difference is the op's own.
+* a few AdamW steps on a fixed batch lower the loss (the op trains).
+"""
+import contextlib
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from bozo_amd import model as M
+from oracle import model_ref, torch_ref
+from tests._util import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+AUX_W = dict(closure=0.01, diversity=0.02, consistency=0.1, entropy=0.05)
+
+
+def total_loss(logits, hidden, taus, targets, window_groups):
+    ce = F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), targets.reshape(-1))
+    if taus is None:
+        return ce, {}
+    parts = dict(closure=M.manifold_closure_loss(hidden),
+                 diversity=M.tension_diversity_loss(taus, window_groups),
+                 consistency=M.constraint_consistency_loss(taus),
+                 entropy=M.tension_entropy_loss(taus))
+    return ce + sum(AUX_W[k] * v for k, v in parts.items()), parts
+
+
+def make_model(cfg, seed, dev):
+    torch.manual_seed(seed)
+    m = M.TensionLM(cfg)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.add_(0.05 * torch.randn_like(p))
+    return m.to(dev)
+
+
+@pytest.mark.parametrize("use_rope,use_triton,return_all,use_bias", [
+    (True, True, False, False), (True, True, True, False), (False, False, True, True),
+    (True, False, False, True)])
+def test_float32_model_vs_functional_reference(dev, use_rope, use_triton, return_all, use_bias):
+    cfg = M.TensionConfig(vocab_size=96, dim=64, num_layers=4, num_heads=4, window=8,
+                          max_seq_len=64, dropout=0.0, global_every=2, use_rope=use_rope,
+                          use_triton=use_triton)
+    m = make_model(cfg, 0, dev).eval()
+    g = torch.Generator().manual_seed(5)
+    B, T = 2, 45
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=g)
+    tgt = torch.randint(0, cfg.vocab_size, (B, T), generator=g)
+    bias = torch.randn(B, T, cfg.window, generator=g) * 0.5 if use_bias else None
+    bias_g = torch.randn(B, T, T, generator=g) * 0.5 if use_bias else None
+    print(f"[model fp32] rope={use_rope} triton={use_triton} all={return_all} bias={use_bias}", flush=True)
+
+    to = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    res = m(ids.to(dev), return_all=return_all, tau_bias=to(bias), tau_bias_global=to(bias_g))
+    lg, hid, taus = res if return_all else (res, None, None)
+    loss, parts = total_loss(lg, hid, taus, tgt.to(dev), m.window_groups)
+    loss.backward()
+    torch.cuda.synchronize()
+
+    sd = {k: v.detach().double().cpu().requires_grad_(True) for k, v in m.state_dict().items()}
+    dbl = lambda t: None if t is None else t.double()  # noqa: E731
+    ref = model_ref.forward(sd, cfg, ids, return_all, dbl(bias), dbl(bias_g))
+    lr, hr, tr = ref if return_all else (ref, None, None)
+    loss_r, parts_r = total_loss(lr, hr, tr, tgt, m.window_groups)
+    loss_r.backward()
+
+    assert rel_l2(lg.detach().cpu().numpy(), lr.detach().numpy()) < 1e-5
+    assert abs(loss.item() - loss_r.item()) < 1e-5 * abs(loss_r.item())
+    for k in parts:
+        assert abs(parts[k].item() - parts_r[k].item()) <= 1e-5 * abs(parts_r[k].item()) + 1e-9, k
+    if return_all:
+        for a, b in zip(taus, tr):
+            assert np.max(np.abs(a.detach().cpu().numpy() - b.detach().numpy())) < 1e-5
+    for name, p in m.named_parameters():
+        ref_g = sd[name].grad.numpy()
+        err = rel_l2(p.grad.cpu().numpy(), ref_g)
+        assert err < 1e-4, (name, err)
+
+
+def _ref_ct(Q, K, V, window, scale, return_tau=False, bias=None, *, normalize=None):
+    """The reference op's math in float32 on the CPU (differentiable through
+    the device moves), result cast to Q.dtype on Q's device."""
+    with torch.autocast("cuda", enabled=False):
+        f = lambda t: None if t is None else t.float().cpu()  # noqa: E731
+        raw, tau = torch_ref.unfold_tension(f(Q), f(K), f(V), window, scale, return_tau=True,
+                                            bias=f(bias))
+        if normalize == "mass":
+            raw = torch_ref.normalize_mass(raw, tau)
+        elif normalize == "count":
+            raw = torch_ref.normalize_count(raw, window)
+        back = lambda t: t.to(Q.device).to(Q.dtype)  # noqa: E731
+        return (back(raw), back(tau)) if return_tau else back(raw)
+
+
+def _ref_gt(Q, K, V, scale, bias=None, W_local=None):
+    with torch.autocast("cuda", enabled=False):
+        f = lambda t: None if t is None else t.float()  # noqa: E731
+        T = Q.shape[1]
+        x = torch.matmul(f(Q).permute(0, 2, 1, 3), f(K).permute(0, 2, 3, 1).contiguous()) / scale
+        if bias is not None:
+            x = x + f(bias)[:, None]
+        tau = torch.sigmoid(x) * torch.tril(torch.ones(T, T, device=Q.device))
+        mass = tau.sum(-1).clamp(min=torch_ref.MASS_EPS)
+        out = (torch.matmul(tau, f(V).permute(0, 2, 1, 3)) / mass[..., None]).permute(0, 2, 1, 3)
+        out = out.to(Q.dtype)
+        if W_local is None:
+            return out
+        tl = tau.permute(0, 2, 1, 3).flip(-1)[..., :min(W_local, T)]
+        return out, tl.to(Q.dtype)
+
+
+def _ref_rope(x, cos, sin, pos_offset=0, out_dtype=None):
+    with torch.autocast("cuda", enabled=False):
+        return torch_ref.rope(x.float(), cos, sin, pos_offset).to(out_dtype or x.dtype)
+
+
+@contextlib.contextmanager
+def reference_ops():
+    saved = (M.causal_tension, M.global_tension, M.rope)
+    M.causal_tension, M.global_tension, M.rope = _ref_ct, _ref_gt, _ref_rope
+    try:
+        yield
+    finally:
+        M.causal_tension, M.global_tension, M.rope = saved
+
+
+def _run_bf16(m, ids, tgt, return_all):
+    m.zero_grad(set_to_none=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        res = m(ids, return_all=return_all)
+        lg, hid, taus = res if return_all else (res, None, None)
+        loss, parts = total_loss(lg, hid, taus, tgt, m.window_groups)
+    loss.backward()
+    torch.cuda.synchronize()
+    grads = {n: p.grad.detach().float().cpu().numpy().copy() for n, p in m.named_parameters()}
+    return lg.detach().float().cpu().numpy(), loss.item(), grads
+
+
+@pytest.mark.parametrize("use_triton,return_all", [(True, False), (True, True), (False, False)])
+def test_bf16_autocast_model_vs_reference_ops(dev, use_triton, return_all):
+    cfg = M.TensionConfig(vocab_size=512, dim=128, num_layers=4, num_heads=2, window=64,
+                          max_seq_len=320, dropout=0.0, global_every=2, use_rope=True,
+                          use_triton=use_triton)
+    m = make_model(cfg, 1, dev).train()
+    g = torch.Generator().manual_seed(6)
+    B, T = 2, 320
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
+    tgt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
+    print(f"[model bf16] triton={use_triton} all={return_all}", flush=True)
+    lg, loss, grads = _run_bf16(m, ids, tgt, return_all)
+    with reference_ops():
+        lr, loss_r, grads_r = _run_bf16(m, ids, tgt, return_all)
+    e_logits = rel_l2(lg, lr)
+    e_grads = {n: rel_l2(grads[n], grads_r[n]) for n in grads}
+    worst = max(e_grads, key=e_grads.get)
+    print(f"  logits rel {e_logits:.2e} loss {loss:.5f} vs {loss_r:.5f} worst grad {worst} "
+          f"{e_grads[worst]:.2e}", flush=True)
+    # bf16 tolerance of the op (2e-2 relative) on the outputs; the parameter
+    # gradients collect it through the whole network, so 2x that
+    assert e_logits < 2e-2
+    assert abs(loss - loss_r) < 2e-2 * abs(loss_r)
+    assert e_grads[worst] < 4e-2, (worst, e_grads[worst])
+
+
+def test_adamw_steps_lower_the_loss(dev):
+    cfg = M.TensionConfig(vocab_size=256, dim=128, num_layers=4, num_heads=2, window=64,
+                          max_seq_len=256, dropout=0.1, global_every=2, use_rope=True,
+                          use_triton=True)
+    torch.manual_seed(2)
+    m = M.TensionLM(cfg).to(dev).train()
+    opt = M.configure_adamw(m, lr=3e-3)
+    g = torch.Generator().manual_seed(7)
+    ids = torch.randint(0, cfg.vocab_size, (4, 257), generator=g).to(dev)
+    losses = []
+    for _ in range(30):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            lg, hid, taus = m(ids[:, :-1], return_all=True)
+            loss, _ = total_loss(lg, hid, taus, ids[:, 1:], m.window_groups)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        losses.append(loss.item())
+    print(f"[model train] loss {losses[0]:.3f} -> {losses[-1]:.3f}", flush=True)
+    assert all(np.isfinite(losses))
+    assert losses[-1] < 0.7 * losses[0]
