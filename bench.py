@@ -603,6 +603,8 @@ def main():
     ap.add_argument("--summarize", metavar="PATH", nargs="+",
                     help="print per-phase kernel stats / calibrated traffic of rocprofv3 output "
                          "dirs or .db files and exit")
+    ap.add_argument("--model-only", action="store_true",
+                    help="only the TensionLM-117M training step (config 5), one JSON line per variant")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize)
@@ -618,6 +620,10 @@ def main():
     torch.cuda.set_device(dev)
     if args.profile_kernels:
         profile_kernels(args.profile_kernels, dev)
+        return
+    if args.model_only:
+        for aux in (False, True):
+            print(json.dumps(bench_model(dev, args.steps, args.warmup, aux)), flush=True)
         return
     result = bench_window(args, dev)
     log("[bench] global block (config 3) ...")

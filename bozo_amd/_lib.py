@@ -24,6 +24,7 @@ NORM_MASS = 1 << 0
 NORM_COUNT = 1 << 1
 GLOBAL = 1 << 2
 FORCE_EXACT = 1 << 3
+DECODE_SELF = 1 << 4
 
 # status codes
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3

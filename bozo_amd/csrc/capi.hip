@@ -365,6 +365,10 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   if (pos_out && pos_out == pos_in) return fail(TENSION_ERR_ARG, "pos_out must not alias pos_in");
   if (k_cache->dtype != k_new->dtype || v_cache->dtype != v_new->dtype)
     return fail(TENSION_ERR_ARG, "cache and new-token dtypes must match");
+  if ((flags & TENSION_NORM_MASS) && (flags & TENSION_NORM_COUNT))
+    return fail(TENSION_ERR_ARG, "decode: TENSION_NORM_MASS and TENSION_NORM_COUNT are exclusive");
+  if ((flags & TENSION_DECODE_SELF) && tau && tau->ptr)
+    return fail(TENSION_ERR_ARG, "decode: tau output is not supported with TENSION_DECODE_SELF");
   DecodeParams p;
   memset(&p, 0, sizeof p);
   p.q = make_buf(q); p.kn = make_buf(k_new); p.vn = make_buf(v_new);
@@ -379,7 +383,7 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   // the fast kernel reads each (n, h) cache slab through a buffer descriptor
   // of W * row_stride * 2 bytes (31-bit range, rows of at least 64 elements)
   auto slab_fits = [&](const tension_buf* b) { return b->s[2] >= 64 && W * b->s[2] * 2 < ((int64_t)1 << 31); };
-  const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 512 && a16(q, false) &&
+  const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 1024 && a16(q, false) &&
                     a16(k_new, false) && a16(v_new, false) && a16(out, false) && a16(k_cache, true) &&
                     a16(v_cache, true) && slab_fits(k_cache) && slab_fits(v_cache);
   hipError_t e = hipSuccess;

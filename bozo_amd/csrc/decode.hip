@@ -16,6 +16,13 @@ __device__ __forceinline__ int ring_w(int slot, int pos, int W) {
   return w < 0 ? w + W : w;
 }
 
+// Normaliser of one decode output row: tau mass, number of keys, or 1.
+__device__ __forceinline__ float decode_norm(int flags, float mass, int keys) {
+  if (flags & TENSION_NORM_MASS) return 1.f / (mass > kMassEps ? mass : kMassEps);
+  if (flags & TENSION_NORM_COUNT) return 1.f / (float)(keys > 1 ? keys : 1);
+  return 1.f;
+}
+
 // Fast path: bf16 q / cache / out, D = 64, W <= 8 * NW * NP.
 //
 // NW waves per workgroup; pass i covers cache rows 8 * NW * i .. + 8 * NW - 1,
@@ -111,6 +118,27 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vv[e];
   }
+  // TENSION_DECODE_SELF: the new token is a key too (global layers attend to
+  // s <= t).  Wave 1 holds its k row in lanes 0-7 and its v row in lanes
+  // 8-15 (chunk = lane & 7, the same chunk of q each lane holds): lanes 0-7
+  // form the dot, lanes 8-15 take its sigmoid through the row rotate and
+  // scale their v chunk; the results meet the cache sums in LDS.
+  __shared__ float sred[65];
+  const bool self_key = (p.flags & TENSION_DECODE_SELF) != 0;
+  if (self_key && wave == 1) {
+    const bf16x8 kv = __builtin_bit_cast(bf16x8, knew);
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += q[e] * (float)kv[e];
+    const float ts = sigmoid_fast(row_sum8(part));
+    const float tv = dpp_move<0x128>(ts);  // lanes 8-15 <- lanes 0-7
+    if (lane >= 8 && lane < 16) {
+      const bf16x8 vv = __builtin_bit_cast(bf16x8, vnew);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sred[8 * (lane - 8) + e] = tv * (float)vv[e];
+    }
+    if (lane == 0) sred[64] = ts;
+  }
   // Fold row pairs (lanes 8 apart) with a DPP rotate; then lane ch of every
   // 16-lane row holds the sums over rows rw = 2r, 2r + 1 of its wave, and the
   // NW * 4 row partials meet in LDS.  tau, hence msum, is equal on the 8 lanes
@@ -133,8 +161,11 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
       o += red[r][tid];
       m += mred[r];
     }
-    float inv = 1.f;
-    if (p.flags & TENSION_NORM_MASS) inv = 1.f / (m > kMassEps ? m : kMassEps);
+    if (self_key) {
+      o += sred[tid];
+      m += sred[64];
+    }
+    const float inv = decode_norm(p.flags, m, live + (self_key ? 1 : 0));
     bf16* orow = (bf16*)p.out.p + n * p.out.s0 + h * p.out.s1;
     orow[tid] = (bf16)(o * inv);
   } else if (ai < 16) {
@@ -181,15 +212,28 @@ __global__ __launch_bounds__(64) void decode_exact(DecodeParams p) {
     msum += tau;
     if (p.tau.p) st<A>(p.tau, n * p.tau.s0 + h * p.tau.s1 + ring_w(slot, pos, W), tau);
   }
+  const int64_t no = n * p.kn.s0 + h * p.kn.s1;
+  const int64_t nvo = n * p.vn.s0 + h * p.vn.s1;
+  const bool self_key = (p.flags & TENSION_DECODE_SELF) != 0;
+  if (self_key) {  // the new token as a key (s <= t)
+    A dot = A(0);
+    for (int d = 0; d < D; ++d) dot += ld<A>(p.q, qo + d) * ld<A>(p.kn, no + d);
+    const A tau = sigmoid_exact(dot / scale);
+    for (int d = 0; d < D; ++d) acc[d] += tau * ld<A>(p.vn, nvo + d);
+    msum += tau;
+  }
   A inv = A(1);
-  if (p.flags & TENSION_NORM_MASS) inv = A(1) / (msum > A(kMassEps) ? msum : A(kMassEps));
+  if (p.flags & TENSION_NORM_MASS) {
+    inv = A(1) / (msum > A(kMassEps) ? msum : A(kMassEps));
+  } else if (p.flags & TENSION_NORM_COUNT) {
+    const int keys = (pos < W ? pos : W) + (self_key ? 1 : 0);
+    inv = A(1) / A(keys > 1 ? keys : 1);
+  }
   const int64_t oo = n * p.out.s0 + h * p.out.s1;
   for (int d = 0; d < D; ++d) st<A>(p.out, oo + d, acc[d] * inv);
   const int slot = pos % W;
   const int64_t ko = n * p.kc.s0 + h * p.kc.s1 + (int64_t)slot * p.kc.s2;
   const int64_t vo = n * p.vc.s0 + h * p.vc.s1 + (int64_t)slot * p.vc.s2;
-  const int64_t no = n * p.kn.s0 + h * p.kn.s1;
-  const int64_t nvo = n * p.vn.s0 + h * p.vn.s1;
   for (int d = 0; d < D; ++d) {
     st<A>(p.kc, ko + d, ld<A>(p.kn, no + d));
     st<A>(p.vc, vo + d, ld<A>(p.vn, nvo + d));
@@ -199,7 +243,7 @@ __global__ __launch_bounds__(64) void decode_exact(DecodeParams p) {
 
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err) {
   if (fast) {
-    // fast requires D == 64, W <= 512
+    // fast requires D == 64, W <= 1024
     const dim3 grid((unsigned)(p.N * p.H));
     if (p.W <= 32)
       hipLaunchKernelGGL((decode_bf16_d64<4, 1>), grid, dim3(256), 0, st, p);
@@ -209,8 +253,10 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
       hipLaunchKernelGGL((decode_bf16_d64<8, 2>), grid, dim3(512), 0, st, p);
     else if (p.W <= 256)
       hipLaunchKernelGGL((decode_bf16_d64<8, 4>), grid, dim3(512), 0, st, p);
-    else
+    else if (p.W <= 512)
       hipLaunchKernelGGL((decode_bf16_d64<8, 8>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((decode_bf16_d64<8, 16>), grid, dim3(512), 0, st, p);
   } else {
     const unsigned grid = (unsigned)((p.N * p.H + 63) / 64);
     if (f64)

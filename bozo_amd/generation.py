@@ -1,0 +1,186 @@
+"""KV-cached generation for TensionLM on the streaming decode kernel.
+
+The reference generates by re-running the whole forward over the last
+``max_seq_len`` tokens for every new token (``model.py:617-652`` and
+``generate_cached`` ``model.py:719-768``, whose TODO at 736-739 asks for a
+per-layer cache).  A tension layer only reads keys/values of earlier
+positions, so one token can be advanced through all layers from caches:
+
+* local layers keep a ring of the last W post-RoPE K/V rows per (sequence,
+  head) and run ``tension_decode_step`` with the same normalisation as the
+  full forward (valid count on the reference's Triton path without tau,
+  tau mass otherwise);
+* global layers keep every earlier row (a ring of ``max_seq_len`` slots that
+  never wraps) and run the step with the new token as a key too (keys s <= t,
+  tau-mass normalised);
+* RoPE and the oscillatory modulation take the token's absolute position.
+
+Each step therefore reads O(W) cached rows per local layer instead of
+re-running O(T W) work.  The result equals the full forward's last row as
+long as the sequence fits ``max_seq_len``; beyond that the reference slides
+its context window (every position shifts, so no cache can serve it) and
+``generate_cached`` re-runs the forward over the window, as the reference
+does.
+
+Sampling (``sample_next``) restates the reference's: repetition penalty over
+the last 32 tokens, temperature, top-p nucleus, one multinomial draw
+(``model.py:634-650``).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from .ops import TensionDecodeCache
+
+
+class TensionKVCache:
+    """Per-layer K/V caches of N sequences advancing in lock step.
+
+    ``prefill(ids)`` runs the model's forward over the prompt [N, T] and
+    keeps each layer's last W (local) / all (global) post-RoPE K/V rows;
+    ``step(next_ids)`` advances one token per sequence and returns its
+    logits [N, vocab].  The model must be in eval mode (dropout off)."""
+
+    def __init__(self, model, N: int):
+        self.model = model
+        self.N = N
+        self.t = 0  # tokens cached per sequence
+        cfg = model.cfg
+        self.windows = [cfg.max_seq_len if b.global_layer else cfg.window for b in model.blocks]
+        self.layers: list[Optional[TensionDecodeCache]] = [None] * len(model.blocks)
+
+    def _fill(self, i: int, k: Tensor, v: Tensor):
+        N, T, H, HD = k.shape
+        layer = self.model.blocks[i].tension
+        c = self.layers[i]
+        if c is None or c.k.dtype != k.dtype:
+            c = TensionDecodeCache(N, H, HD, self.windows[i], dtype=k.dtype, device=k.device,
+                                   scale=layer.scale)
+            self.layers[i] = c
+        W = c.W
+        s = max(0, T - W)
+        slots = torch.arange(s, T, device=k.device) % W
+        c.k[:, :, slots] = k[:, s:].transpose(1, 2)
+        c.v[:, :, slots] = v[:, s:].transpose(1, 2)
+        c.pos[c.cur].fill_(T)
+
+    @torch.no_grad()
+    def prefill(self, ids: Tensor) -> Tensor:
+        """Forward over the prompt ids [N, T] (T <= max_seq_len) filling the
+        caches; returns the logits [N, T, vocab]."""
+        model = self.model
+        N, T = ids.shape
+        if N != self.N:
+            raise ValueError(f"prefill: {N} sequences, cache built for {self.N}")
+        if not 1 <= T <= model.cfg.max_seq_len:
+            raise ValueError(f"prefill: prompt length {T} outside [1, {model.cfg.max_seq_len}]")
+        if model.training:
+            raise RuntimeError("generation needs model.eval() (dropout off)")
+        layers = [b.tension for b in model.blocks]
+        for i, layer in enumerate(layers):
+            layer.kv_sink = (lambda k, v, i=i: self._fill(i, k, v))
+        try:
+            logits = model(ids)
+        finally:
+            for layer in layers:
+                layer.kv_sink = None
+        self.t = T
+        return logits
+
+    @torch.no_grad()
+    def step(self, next_ids: Tensor, return_tau: bool = False):
+        """Advance every sequence by one token (ids [N]) at position ``t``;
+        returns logits [N, vocab] and, with ``return_tau``, the new token's
+        tau row [N, H, W] of every local layer (None for global layers) --
+        the last row of the full forward's tau."""
+        model = self.model
+        cfg = model.cfg
+        t = self.t
+        if t == 0:
+            raise RuntimeError("step before prefill")
+        if t >= cfg.max_seq_len:
+            raise ValueError(f"position {t} is past max_seq_len {cfg.max_seq_len}")
+        if model.training:
+            raise RuntimeError("generation needs model.eval() (dropout off)")
+        N = next_ids.shape[0]
+        x = model.embedding(next_ids.view(N, 1))
+        if model.pos_embedding is not None:
+            x = x + model.pos_embedding(model.pos_buf[:, t:t + 1])
+        taus = []
+        for blk, c in zip(model.blocks, self.layers):
+            h = blk.pre_norm(x)
+            h, tau = _layer_step(blk.tension, h, c, t, return_tau)
+            taus.append(tau)
+            if blk.oscillate is not None:
+                osc = blk.oscillate
+                h = h * (1.0 + osc.amp * torch.sin(osc.pos_buf[t:t + 1] * osc.freqs + osc.phases)[None])
+            x = blk.ffn(h)
+        logits = model.lm_head(model.final_norm(x))[:, 0]
+        self.t = t + 1
+        return (logits, taus) if return_tau else logits
+
+
+def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, t: int, return_tau: bool):
+    """One token through a tension layer: x [N, 1, D] at position t."""
+    N, _, D = x.shape
+    q, k, v = layer._qkv(x, pos_offset=t)
+    q, k, v = q[:, 0], k[:, 0], v[:, 0]
+    tau = None
+    if layer.global_layer:
+        out = cache.step(q, k, v, normalize="mass", include_self=True)
+    else:
+        norm = "count" if layer.count_norm else "mass"
+        if return_tau:
+            out, tau = cache.step(q, k, v, normalize=norm, return_tau=True)
+        else:
+            out = cache.step(q, k, v, normalize=norm)
+    return layer.norm(x + layer.wo(out.reshape(N, 1, D))), tau
+
+
+def sample_next(logits: Tensor, history: list, temp: float = 0.8, top_p: float = 0.92,
+                rep_penalty: float = 1.3, generator: Optional[torch.Generator] = None) -> int:
+    """Next token from one logits row [vocab] (model.py:634-650)."""
+    logits = logits.float().clone()
+    recent = sorted(set(history[-32:]))
+    if recent:
+        idx = torch.tensor(recent, device=logits.device)
+        sel = logits[idx]
+        logits[idx] = torch.where(sel > 0, sel / rep_penalty, sel * rep_penalty)
+    logits = logits / max(temp, 1e-5)
+    probs = torch.softmax(logits, dim=-1)
+    sorted_p, sorted_i = torch.sort(probs, descending=True)
+    cum_p = torch.cumsum(sorted_p, dim=-1)
+    keep = (cum_p - sorted_p) < top_p
+    sorted_p[~keep] = 0.0
+    sorted_p /= sorted_p.sum()
+    return int(sorted_i[torch.multinomial(sorted_p, 1, generator=generator).item()].item())
+
+
+@torch.no_grad()
+def generate_cached(model, input_ids: list, max_new: int = 200, temp: float = 0.8,
+                    top_p: float = 0.92, rep_penalty: float = 1.3,
+                    generator: Optional[torch.Generator] = None) -> list:
+    """Autoregressive generation with per-layer K/V caches (same arguments
+    and result as the reference's ``generate_cached``, model.py:719-768)."""
+    model.eval()
+    device = next(model.parameters()).device
+    max_ctx = model.cfg.max_seq_len
+    ids = list(input_ids)
+    if not ids or max_new <= 0:
+        return ids
+    cache = TensionKVCache(model, 1)
+    logits = cache.prefill(torch.tensor([ids[-max_ctx:]], dtype=torch.long, device=device))[0, -1]
+    for i in range(max_new):
+        nxt = sample_next(logits, ids, temp, top_p, rep_penalty, generator)
+        ids.append(nxt)
+        if i == max_new - 1:
+            break
+        if len(ids) <= max_ctx:
+            logits = cache.step(torch.tensor([nxt], dtype=torch.long, device=device))[0]
+        else:  # the reference's context slides past max_seq_len: re-run the window
+            ctx = torch.tensor([ids[-max_ctx:]], dtype=torch.long, device=device)
+            logits = model(ctx)[0, -1]
+    return ids

@@ -86,8 +86,8 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("cos", ang.cos(), persistent=False)
         self.register_buffer("sin", ang.sin(), persistent=False)
 
-    def forward(self, x: Tensor, T: int) -> Tensor:
-        return rope(x, self.cos, self.sin)
+    def forward(self, x: Tensor, T: int, pos_offset: int = 0) -> Tensor:
+        return rope(x, self.cos, self.sin, pos_offset)
 
 
 class RMSNorm(nn.Module):
@@ -136,15 +136,18 @@ class MultiHeadCausalTensionLayer(nn.Module):
         self.wo = nn.Linear(D, D, bias=False)
         self.norm = RMSNorm(D)
         self.dropout = nn.Dropout(cfg.dropout)
+        # called with the layer's (k, v) [B,T,H,HD] after RoPE when set (the
+        # generation cache's prefill reads them here)
+        self.kv_sink = None
 
-    def _qkv(self, x: Tensor):
+    def _qkv(self, x: Tensor, pos_offset: int = 0):
         B, T, D = x.shape
         H, HD = self.num_heads, self.head_dim
         q = self.wq(x).view(B, T, H, HD)
         if self.rope_enabled:
             k = self.wk(x).view(B, T, H, HD)
             v = self.wv(x).view(B, T, H, HD)
-            q, k = self.rope(q, T), self.rope(k, T)
+            q, k = self.rope(q, T, pos_offset), self.rope(k, T, pos_offset)
         else:
             k, v = self.wkv(x).view(B, T, H, 2 * HD).split(HD, dim=-1)
         return q, k, v
@@ -152,6 +155,8 @@ class MultiHeadCausalTensionLayer(nn.Module):
     def forward(self, x: Tensor, return_tensions: bool = False, tau_bias: Optional[Tensor] = None):
         B, T, D = x.shape
         q, k, v = self._qkv(x)
+        if self.kv_sink is not None:
+            self.kv_sink(k, v)
         if self.global_layer:
             res = global_tension(q, k, v, self.scale, bias=tau_bias,
                                  W_local=self.local_window if return_tensions else None)
@@ -367,3 +372,6 @@ def tension_entropy_loss(all_tensions: list) -> Tensor:
         m = tau.mean(-1)
         total = total + F.relu(0.05 - m).mean() + F.relu(m - 0.80).mean()
     return total / len(all_tensions)
+
+
+from .generation import TensionKVCache, generate_cached, sample_next  # noqa: E402,F401

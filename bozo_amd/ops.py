@@ -226,24 +226,34 @@ def global_tension(Q: Tensor, K: Tensor, V: Tensor, scale: float,
 
 # ----------------------------------------------------------------- decode
 
+_DECODE_NORMS = {True: L.NORM_MASS, "mass": L.NORM_MASS, "count": L.NORM_COUNT,
+                 False: 0, None: 0, "raw": 0}
+
+
 def decode_step(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cache: Tensor,
                 pos_in: Tensor, pos_out: Optional[Tensor], scale: float,
-                normalize: bool = True, tau: Optional[Tensor] = None) -> Tensor:
+                normalize=True, tau: Optional[Tensor] = None, include_self: bool = False) -> Tensor:
     """One streaming step (no autograd): attends q [N,H,D] to the cached
     window, then appends k_new/v_new at slot pos % W of the ring caches
     [N,H,W,D] (in place).  pos_in: int32 [N] on the GPU; pos_out receives
-    pos_in + 1 when given.  Returns out [N,H,D] in q.dtype."""
+    pos_in + 1 when given.  ``normalize``: True / "mass" (tau mass), "count"
+    (number of keys) or False / None (raw sum).  ``include_self``: the new
+    token is a key too (a global layer's step; no tau then).  Returns out
+    [N,H,D] in q.dtype."""
     _on_gpu(q, k_new, v_new, k_cache, v_cache, pos_in)
     N, H, D = q.shape
     W = k_cache.shape[2]
     if pos_in.dtype != torch.int32 or (pos_out is not None and pos_out.dtype != torch.int32):
         raise TypeError("pos tensors must be int32")
+    if normalize not in _DECODE_NORMS:
+        raise ValueError(f"normalize must be one of {list(_DECODE_NORMS)}")
+    flags = _DECODE_NORMS[normalize] | (L.DECODE_SELF if include_self else 0)
     out = torch.empty_like(q)
     with torch.cuda.device(q.device):
         L.check(L.lib().tension_decode_step(
             L.buf(_rows(q)), L.buf(_rows(k_new)), L.buf(_rows(v_new)), L.buf(k_cache), L.buf(v_cache),
             L.buf(out), L.buf(tau), pos_in.data_ptr(), _ptr(pos_out), N, H, D, W, float(scale),
-            L.NORM_MASS if normalize else 0, _stream(q)), "tension_decode_step")
+            flags, _stream(q)), "tension_decode_step")
     return out
 
 
@@ -262,12 +272,13 @@ class TensionDecodeCache:
         self.W = W
         self.scale = float(scale) if scale is not None else math.sqrt(D)
 
-    def step(self, q: Tensor, k_new: Tensor, v_new: Tensor, normalize: bool = True,
-             return_tau: bool = False):
+    def step(self, q: Tensor, k_new: Tensor, v_new: Tensor, normalize=True,
+             return_tau: bool = False, include_self: bool = False):
         tau = (torch.empty(q.shape[0], q.shape[1], self.W, dtype=q.dtype, device=q.device)
                if return_tau else None)
         pin, pout = self.pos[self.cur], self.pos[1 - self.cur]
-        out = decode_step(q, k_new, v_new, self.k, self.v, pin, pout, self.scale, normalize, tau)
+        out = decode_step(q, k_new, v_new, self.k, self.v, pin, pout, self.scale, normalize, tau,
+                          include_self)
         self.cur = 1 - self.cur
         return (out, tau) if return_tau else out
 

@@ -60,7 +60,10 @@ enum {
   /* bias is [B,T,T] indexed by key position (global block, model.py:224-225) */
   TENSION_GLOBAL = 1 << 2,
   /* force the exact (non-MFMA) kernels even when the MFMA path applies */
-  TENSION_FORCE_EXACT = 1 << 3
+  TENSION_FORCE_EXACT = 1 << 3,
+  /* decode: the new token is also a key (keys s <= t, the global block's
+   * diagonal, model.py:221) */
+  TENSION_DECODE_SELF = 1 << 4
 };
 
 typedef struct tension_buf {
@@ -181,8 +184,14 @@ int tension_global_bwd(const tension_buf* q, const tension_buf* k,
  *   pos_in: device int32 [N], tokens already cached per sequence.
  *   pos_out (nullable): device int32 [N], receives pos_in + 1 (must not
  *   alias pos_in).  tau (nullable, out): [N,H,W], w=0 oldest.
- *   Attends to the min(pos, W) most recent cached tokens (strictly past).
- *   flags: TENSION_NORM_MASS (tau-mass normalised) or 0 (raw).
+ *   Attends to the min(pos, W) most recent cached tokens (strictly past),
+ *   plus the new token itself with TENSION_DECODE_SELF (a global layer's
+ *   step: the cache then holds every earlier token, W >= positions; tau
+ *   must be null).
+ *   flags: TENSION_NORM_MASS (tau-mass normalised), TENSION_NORM_COUNT
+ *   (divided by the number of keys, max(min(pos, W), 1) for a local layer,
+ *   the valid count of model.py:159-163,264) or neither (raw); optionally
+ *   TENSION_DECODE_SELF.
  * ------------------------------------------------------------------------- */
 int tension_decode_step(const tension_buf* q, const tension_buf* k_new,
                         const tension_buf* v_new, const tension_buf* k_cache,

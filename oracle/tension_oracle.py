@@ -268,14 +268,18 @@ def global_backward(Q, K, V, scale: float, dout, bias=None, dtau_local=None):
 # --------------------------------------------------------------------------
 
 def decode_step(q, k_cache, v_cache, pos, W: int, scale: float,
-                normalize: bool = True):
+                normalize=True, self_kv=None):
     """One decode step over a ring cache.
 
     q [N,H,D]; k_cache/v_cache [N,H,W,D]; pos [N] = number of tokens already
     appended for each sequence.  Slot i holds the most recent position p with
     p % W == i.  The query attends to positions max(0,pos-W)..pos-1 (strictly
-    past, like the local window).  Returns (out [N,H,D], tau [N,H,W]) with tau
-    in window order (w=0 oldest: key position pos-W+w), zero on empty slots.
+    past, like the local window) and, with ``self_kv`` = (k_new, v_new)
+    [N,H,D], to the new token itself (the global block's diagonal).
+    ``normalize``: True / "mass" (tau mass), "count" (number of keys,
+    max(min(pos, W) + self, 1)) or False (raw).  Returns (out [N,H,D], tau
+    [N,H,W]) with tau in window order (w=0 oldest: key position pos-W+w),
+    zero on empty slots (the self key's tau is not part of it).
     """
     q, kc, vc = _f64(q), _f64(k_cache), _f64(v_cache)
     N, H, D = q.shape
@@ -283,6 +287,7 @@ def decode_step(q, k_cache, v_cache, pos, W: int, scale: float,
     tau = np.zeros((N, H, W))
     for n in range(N):
         P = int(pos[n])
+        mass = np.zeros(H)
         for w in range(W):
             p = P - W + w
             if p < 0:
@@ -291,8 +296,18 @@ def decode_step(q, k_cache, v_cache, pos, W: int, scale: float,
             x = (q[n] * kc[n, :, slot]).sum(-1) / scale
             tau[n, :, w] = sigmoid(x)
             out[n] += tau[n, :, w][:, None] * vc[n, :, slot]
-        if normalize:
-            out[n] /= np.maximum(tau[n].sum(-1), MASS_EPS)[:, None]
+        mass += tau[n].sum(-1)
+        keys = min(P, W)
+        if self_kv is not None:
+            kn, vn = _f64(self_kv[0])[n], _f64(self_kv[1])[n]
+            ts = sigmoid((q[n] * kn).sum(-1) / scale)
+            out[n] += ts[:, None] * vn
+            mass += ts
+            keys += 1
+        if normalize is True or normalize == "mass":
+            out[n] /= np.maximum(mass, MASS_EPS)[:, None]
+        elif normalize == "count":
+            out[n] /= max(keys, 1)
     return out, tau
 
 
@@ -372,6 +387,7 @@ PINS = {
     "normalize_mass/normalize_count": "K=0 closed form (window mean of V); valid_count formula",
     "global_forward": "brute-force loops; diag-masked global == window W=T; torch einsum restatement",
     "global_backward": "torch autograd through the einsum restatement; finite differences",
-    "decode_step": "equals last rows of window_forward + tau-mass normalisation over a sequence",
+    "decode_step": "equals last rows of window_forward + tau-mass / valid-count normalisation over "
+                   "a sequence; with self_kv, the rows of global_forward",
     "rope_apply": "norm preservation; relative-position identity; adjoint = inverse rotation",
 }

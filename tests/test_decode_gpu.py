@@ -57,6 +57,63 @@ def test_decode_matches_window_rows(dev, dtype, D, W, prefill):
     assert int(cache.pos[cache.cur][0]) == L
 
 
+@pytest.mark.parametrize("dtype,W,prefill", [
+    (torch.bfloat16, 64, 10),    # fast path, filling
+    (torch.bfloat16, 64, 70),    # fast path, wrapped
+    (torch.float32, 16, 20),     # exact path
+])
+def test_decode_count_matches_window_rows(dev, dtype, W, prefill):
+    from bozo_amd import TensionDecodeCache
+    N, H, D, S = 2, 3, 64, 8
+    L = prefill + S
+    q, k, v = (t.to(dtype) for t in seq_inputs(N, L, H, D, seed=7 + W))
+    cache = TensionDecodeCache(N, H, D, W, dtype=dtype, device=dev)
+    for t in range(prefill):
+        cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev), normalize="count")
+    msg, _ = O.window_forward(f64(q), f64(k), f64(v), W, math.sqrt(D))
+    ref = O.normalize_count(msg, W)
+    for t in range(prefill, L):
+        out = cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev), normalize="count")
+        torch.cuda.synchronize()
+        if dtype == torch.float32:
+            assert max_abs(f64(out), ref[:, t]) <= 1e-5
+        else:
+            assert rel_l2(f64(out), ref[:, t]) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,W,prefill", [
+    (torch.bfloat16, 1024, 1000),  # fast path, 16 passes, nearly full
+    (torch.bfloat16, 1024, 0),     # fast path, empty cache: the first rows are self only
+    (torch.bfloat16, 300, 150),    # fast path, 8 passes
+    (torch.bfloat16, 64, 3),       # fast path, one pass
+    (torch.float32, 40, 20),       # exact path
+])
+def test_decode_self_matches_global_rows(dev, dtype, W, prefill):
+    """include_self over a cache that holds every earlier token is the global
+    block (keys s <= t), row by row."""
+    from bozo_amd import TensionDecodeCache
+    N, H, D, S = 2, 2, 64, 8
+    L = prefill + S
+    assert L <= W
+    q, k, v = (t.to(dtype) for t in seq_inputs(N, L, H, D, seed=11 + W))
+    cache = TensionDecodeCache(N, H, D, W, dtype=dtype, device=dev)
+    cache.k[:, :, :prefill] = k[:, :prefill].permute(0, 2, 1, 3).to(dev)
+    cache.v[:, :, :prefill] = v[:, :prefill].permute(0, 2, 1, 3).to(dev)
+    cache.pos[cache.cur].fill_(prefill)
+    ref, _, _ = O.global_forward(f64(q), f64(k), f64(v), math.sqrt(D))
+    for t in range(prefill, L):
+        out = cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev), include_self=True)
+        torch.cuda.synchronize()
+        if dtype == torch.float32:
+            assert max_abs(f64(out), ref[:, t]) <= 1e-5
+        else:
+            assert rel_l2(f64(out), ref[:, t]) <= 2e-2
+    assert torch.equal(cache.k[:, :, prefill:L].cpu(), k[:, prefill:L].permute(0, 2, 1, 3))
+    with pytest.raises(Exception, match="not supported"):
+        cache.step(q[:, 0].to(dev), k[:, 0].to(dev), v[:, 0].to(dev), include_self=True,
+                   return_tau=True)
+
+
 def test_decode_config4_shape_steps(dev):
     """BASELINE config 4 shape (64 seqs, H16, d64, W256 bf16): cache
     pre-filled with W tokens, then steps checked against the oracle's

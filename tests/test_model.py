@@ -279,3 +279,37 @@ def test_configure_adamw_groups():
     assert opt.defaults["betas"] == (0.9, 0.95) and opt.defaults["eps"] == 1e-8
     n = sum(p.numel() for g in opt.param_groups for p in g["params"])
     assert n == m.num_params
+
+
+# ------------------------------------------------------------------ sampling
+
+def reference_sample(logits, ids, temp, top_p, rep_penalty, generator):
+    """The reference's sampling steps (model.py:634-650) written as its loop."""
+    logits = logits.float().clone()
+    for tok in set(ids[-32:]):
+        if logits[tok] > 0:
+            logits[tok] /= rep_penalty
+        else:
+            logits[tok] *= rep_penalty
+    logits = logits / max(temp, 1e-5)
+    probs = F.softmax(logits, dim=-1)
+    sorted_p, sorted_i = torch.sort(probs, descending=True)
+    cum_p = torch.cumsum(sorted_p, dim=-1)
+    mask = (cum_p - sorted_p) < top_p
+    sorted_p[~mask] = 0.0
+    sorted_p /= sorted_p.sum()
+    return sorted_i[torch.multinomial(sorted_p, 1, generator=generator).item()].item()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_sample_next_matches_reference_loop(seed):
+    from bozo_amd.generation import sample_next
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(300, generator=g) * 3
+    hist = torch.randint(0, 300, (50,), generator=g).tolist()
+    temp, top_p = [(0.8, 0.92), (1.5, 0.5), (1e-7, 0.92), (0.7, 1.0), (1.0, 0.1), (0.5, 0.99)][seed]
+    a = sample_next(logits, hist, temp, top_p, 1.3, torch.Generator().manual_seed(100 + seed))
+    b = reference_sample(logits, hist, temp, top_p, 1.3, torch.Generator().manual_seed(100 + seed))
+    assert a == b
+    # the penalty only touches the last 32 tokens, by sign
+    assert sample_next(logits, [], 1e-7, 0.9) == int(torch.argmax(logits))

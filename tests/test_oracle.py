@@ -271,6 +271,41 @@ def test_decode_equals_last_row_of_window(prefill):
         kc, vc, pos = O.decode_append(kc, vc, pos, k[:, t], v[:, t], W)
 
 
+@pytest.mark.parametrize("prefill", [0, 5])
+def test_decode_count_equals_window_count_rows(prefill):
+    N, H, D, W, S = 2, 2, 4, 6, 9
+    L = prefill + S
+    q, k, v = rnd(93, N, L, H, D), rnd(94, N, L, H, D), rnd(95, N, L, H, D)
+    kc, vc = np.zeros((N, H, W, D)), np.zeros((N, H, W, D))
+    pos = np.zeros(N, dtype=np.int64)
+    for t in range(prefill):
+        kc, vc, pos = O.decode_append(kc, vc, pos, k[:, t], v[:, t], W)
+    msg, _ = O.window_forward(q, k, v, W, 2.0)
+    ref = O.normalize_count(msg, W)
+    raw_o = None
+    for t in range(prefill, L):
+        o, _ = O.decode_step(q[:, t], kc, vc, pos, W, 2.0, normalize="count")
+        close(o, ref[:, t], 1e-12)
+        raw_o, _ = O.decode_step(q[:, t], kc, vc, pos, W, 2.0, normalize=False)
+        close(raw_o, msg[:, t], 1e-12)
+        kc, vc, pos = O.decode_append(kc, vc, pos, k[:, t], v[:, t], W)
+
+
+def test_decode_self_equals_global_rows():
+    """A cache that holds every earlier token plus the new token as a key is
+    the global block (keys s <= t), row by row."""
+    N, H, D, L = 2, 3, 4, 11
+    W = L  # never wraps
+    q, k, v = rnd(96, N, L, H, D), rnd(97, N, L, H, D), rnd(98, N, L, H, D)
+    ref, _, _ = O.global_forward(q, k, v, 2.0)
+    kc, vc = np.zeros((N, H, W, D)), np.zeros((N, H, W, D))
+    pos = np.zeros(N, dtype=np.int64)
+    for t in range(L):
+        o, _ = O.decode_step(q[:, t], kc, vc, pos, W, 2.0, normalize=True, self_kv=(k[:, t], v[:, t]))
+        close(o, ref[:, t], 1e-12)
+        kc, vc, pos = O.decode_append(kc, vc, pos, k[:, t], v[:, t], W)
+
+
 # ---------------------------------------------------------------- rope
 
 def test_rope_properties():
