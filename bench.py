@@ -591,6 +591,51 @@ def bench_model(dev, steps, warmup, aux):
     return res
 
 
+def bench_generation(dev, prompt=512, new=128):
+    """TensionLM-117M generation, logits of one new token per sequence
+    (sampling excluded), bf16 autocast, random init: the reference's method
+    (re-running the forward over the context for every token, model.py:
+    719-768) against the cached step on the decode kernel, eager and
+    replayed from a HIP graph, for 1 and 64 sequences."""
+    from bozo_amd import model as M
+    from bozo_amd.generation import TensionKVCache
+    cfg = M.config_117m(use_triton=True)
+    torch.manual_seed(4)
+    m = M.TensionLM(cfg).to(dev).eval()
+    g = torch.Generator(device=dev).manual_seed(5)
+    res = {"config": f"TensionLM-117M generation, prompt {prompt}, {new} new tokens, bf16 autocast, "
+                     "logits only"}
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ids = torch.randint(0, cfg.vocab_size, (64, prompt + new), device=dev, generator=g)
+        m(ids[:1, :prompt])
+        ms = timed(lambda i: m(ids[:1, :prompt + i + 1])[:, -1], 16)
+        res["reforward_ms_per_token_n1"] = round(ms, 3)
+        for N in (1, 64):
+            for mode in ("eager", "graph"):
+                cache = TensionKVCache(m, N)
+                cache.prefill(ids[:N, :prompt])
+                step = cache.step if mode == "eager" else cache.graph_step
+                step(ids[:N, prompt])  # warm-up (and capture)
+                ms = timed(lambda i: step(ids[:N, prompt + 1 + i]), new - 1)
+                res[f"cached_{mode}_ms_per_step_n{N}"] = round(ms, 4)
+                res[f"cached_{mode}_tokens_per_s_n{N}"] = round(N / (ms * 1e-3), 1)
+                del cache
+    del m
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -605,6 +650,8 @@ def main():
                          "dirs or .db files and exit")
     ap.add_argument("--model-only", action="store_true",
                     help="only the TensionLM-117M training step (config 5), one JSON line per variant")
+    ap.add_argument("--generation-only", action="store_true",
+                    help="only the TensionLM-117M cached-generation timing, one JSON line")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize)
@@ -621,6 +668,9 @@ def main():
     if args.profile_kernels:
         profile_kernels(args.profile_kernels, dev)
         return
+    if args.generation_only:
+        print(json.dumps(bench_generation(dev)), flush=True)
+        return
     if args.model_only:
         for aux in (False, True):
             print(json.dumps(bench_model(dev, args.steps, args.warmup, aux)), flush=True)
@@ -636,6 +686,9 @@ def main():
         log(f"[bench] TensionLM-117M training step (config 5, aux={aux}) ...")
         others.append(bench_model(dev, 10, 3, aux))
         log(f"[bench] {others[-1]}")
+    log("[bench] TensionLM-117M cached generation ...")
+    others.append(bench_generation(dev))
+    log(f"[bench] {others[-1]}")
     result["other_configs"] = others
     if not args.no_cpu:
         log("[bench] CPU baseline ...")

@@ -73,13 +73,23 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   const u16x8 vnew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
       vnr, (ai >= 8 && ai < 16) ? 16 * (ai - 8) : 128, 0, 0));
 
-  // one descriptor per cache slab; loads of rows >= W return zeros
+  // One descriptor per cache slab; loads of rows past its range return
+  // zeros.  The range is W rows, or, for a self-key step (a global layer's
+  // cache, filled from slot 0 and never wrapped), the live rows only: that
+  // cache is long and partly empty, and the position read it needs first
+  // costs little there.  Window caches keep the loads ahead of that read.
+  const bool self_key = (p.flags & TENSION_DECODE_SELF) != 0;
+  int rows = W;
+  if (self_key) {
+    const int pe = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
+    rows = pe < W ? pe : W;
+  }
   const bf16* kbase = (const bf16*)p.kc.p + n * p.kc.s0 + h * p.kc.s1;
   const bf16* vbase = (const bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1;
   const __amdgpu_buffer_rsrc_t kr_ = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)kbase, (short)0, (int)((int64_t)W * p.kc.s2 * 2), kRawBufWord3);
+      (void*)kbase, (short)0, (int)((int64_t)rows * p.kc.s2 * 2), kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vr_ = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)vbase, (short)0, (int)((int64_t)W * p.vc.s2 * 2), kRawBufWord3);
+      (void*)vbase, (short)0, (int)((int64_t)rows * p.vc.s2 * 2), kRawBufWord3);
   const uint32_t row0 = (uint32_t)(wave * 8 + rw);
   const uint32_t kstep = (uint32_t)(kRows * p.kc.s2 * 2), vstep = (uint32_t)(kRows * p.vc.s2 * 2);
   const uint32_t koff = row0 * (uint32_t)(p.kc.s2 * 2) + 16 * ch;
@@ -124,7 +134,6 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   // form the dot, lanes 8-15 take its sigmoid through the row rotate and
   // scale their v chunk; the results meet the cache sums in LDS.
   __shared__ float sred[65];
-  const bool self_key = (p.flags & TENSION_DECODE_SELF) != 0;
   if (self_key && wave == 1) {
     const bf16x8 kv = __builtin_bit_cast(bf16x8, knew);
     float part = 0.f;

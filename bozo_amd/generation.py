@@ -33,7 +33,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from .ops import TensionDecodeCache
+from .ops import TensionDecodeCache, decode_step, rope
 
 
 class TensionKVCache:
@@ -90,54 +90,135 @@ class TensionKVCache:
         self.t = T
         return logits
 
+    def _check_step(self):
+        cfg = self.model.cfg
+        if self.t == 0:
+            raise RuntimeError("step before prefill")
+        if self.t >= cfg.max_seq_len:
+            raise ValueError(f"position {self.t} is past max_seq_len {cfg.max_seq_len}")
+        if self.model.training:
+            raise RuntimeError("generation needs model.eval() (dropout off)")
+
+    def _advance(self):
+        for c in self.layers:
+            c.cur = 1 - c.cur
+        self.t += 1
+
     @torch.no_grad()
     def step(self, next_ids: Tensor, return_tau: bool = False):
         """Advance every sequence by one token (ids [N]) at position ``t``;
         returns logits [N, vocab] and, with ``return_tau``, the new token's
         tau row [N, H, W] of every local layer (None for global layers) --
         the last row of the full forward's tau."""
-        model = self.model
-        cfg = model.cfg
-        t = self.t
-        if t == 0:
-            raise RuntimeError("step before prefill")
-        if t >= cfg.max_seq_len:
-            raise ValueError(f"position {t} is past max_seq_len {cfg.max_seq_len}")
-        if model.training:
-            raise RuntimeError("generation needs model.eval() (dropout off)")
-        N = next_ids.shape[0]
-        x = model.embedding(next_ids.view(N, 1))
-        if model.pos_embedding is not None:
-            x = x + model.pos_embedding(model.pos_buf[:, t:t + 1])
-        taus = []
-        for blk, c in zip(model.blocks, self.layers):
-            h = blk.pre_norm(x)
-            h, tau = _layer_step(blk.tension, h, c, t, return_tau)
-            taus.append(tau)
-            if blk.oscillate is not None:
-                osc = blk.oscillate
-                h = h * (1.0 + osc.amp * torch.sin(osc.pos_buf[t:t + 1] * osc.freqs + osc.phases)[None])
-            x = blk.ffn(h)
-        logits = model.lm_head(model.final_norm(x))[:, 0]
-        self.t = t + 1
+        self._check_step()
+        taus = [] if return_tau else None
+        logits = self._step_device(next_ids, [c.cur for c in self.layers], taus)
+        self._advance()
         return (logits, taus) if return_tau else logits
 
+    @torch.no_grad()
+    def graph_step(self, next_ids: Tensor) -> Tensor:
+        """``step`` replayed from a HIP graph (captured on the first call, one
+        graph per parity of the position counters).  Returns a view of the
+        graph's static logits buffer [N, vocab], overwritten by the next
+        call.  The result is the eager step's."""
+        self._check_step()
+        if self._graphs is None:
+            self._capture()
+        par = self.layers[0].cur
+        self._ids.copy_(next_ids)
+        self._graphs[par].replay()
+        self._advance()
+        return self._logits[par]
 
-def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, t: int, return_tau: bool):
-    """One token through a tension layer: x [N, 1, D] at position t."""
+    _graphs = None
+
+    def _capture(self):
+        dev = self.layers[0].k.device
+        self._ids = torch.zeros(self.N, dtype=torch.long, device=dev)
+        saved = [(c.k.clone(), c.v.clone(), c.pos[0].clone(), c.pos[1].clone()) for c in self.layers]
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):  # warm-up launches (library set-up) outside the capture
+            for par in (0, 1):
+                self._step_device(self._ids, [par] * len(self.layers), None)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        for c, (k, v, p0, p1) in zip(self.layers, saved):
+            c.k.copy_(k)
+            c.v.copy_(v)
+            c.pos[0].copy_(p0)
+            c.pos[1].copy_(p1)
+        graphs, logits = [], []
+        pool = None
+        for par in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                logits.append(self._step_device(self._ids, [par] * len(self.layers), None))
+            pool = g.pool()
+            graphs.append(g)
+        torch.cuda.synchronize(dev)
+        self._graphs, self._logits = graphs, logits
+
+    def _step_device(self, next_ids: Tensor, parities, taus):
+        """One token through the model with its position read from the layer
+        caches' device counters (no host value of t), so the same launches
+        can be captured once and replayed at every position."""
+        model = self.model
+        N = next_ids.shape[0]
+        c0 = self.layers[0]
+        pos = c0.pos[parities[0]][:1].long()  # [1]: position of the new token
+        x = model.embedding(next_ids.view(N, 1))
+        if model.pos_embedding is not None:
+            x = x + model.pos_embedding(pos.view(1, 1))
+        # per-position tables, gathered once for every layer
+        rot = None
+        first = model.blocks[0].tension
+        if first.rope_enabled:
+            rot = (first.rope.cos.index_select(0, pos), first.rope.sin.index_select(0, pos))
+        fpos = None
+        for blk, c, par in zip(model.blocks, self.layers, parities):
+            h = blk.pre_norm(x)
+            h = _layer_step(blk.tension, h, c, par, rot, taus)
+            if blk.oscillate is not None:
+                osc = blk.oscillate
+                if fpos is None:
+                    fpos = osc.pos_buf.index_select(0, pos)
+                h = h * (1.0 + osc.amp * torch.sin(fpos * osc.freqs + osc.phases)[None])
+            ffn = blk.ffn
+            y = ffn.proj(torch.nn.functional.silu(ffn.gate(h)) * ffn.val(h))
+            # the residual in the stream's dtype (same values as x + y)
+            x = ffn.norm(h + y.to(h.dtype))
+        return model.lm_head(model.final_norm(x))[:, 0]
+
+
+def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, par: int, rot, taus):
+    """One token through a tension layer: x [N, 1, D]; ``rot`` the RoPE
+    (cos, sin) rows [1, HD/2] of its position; cache counters pos[par] ->
+    pos[1 - par]."""
     N, _, D = x.shape
-    q, k, v = layer._qkv(x, pos_offset=t)
-    q, k, v = q[:, 0], k[:, 0], v[:, 0]
-    tau = None
-    if layer.global_layer:
-        out = cache.step(q, k, v, normalize="mass", include_self=True)
+    H, HD = layer.num_heads, layer.head_dim
+    q = layer.wq(x).view(N, 1, H, HD)
+    if layer.rope_enabled:
+        k = layer.wk(x).view(N, 1, H, HD)
+        v = layer.wv(x).view(N, 1, H, HD)
+        q, k = rope(q, *rot), rope(k, *rot)
     else:
-        norm = "count" if layer.count_norm else "mass"
-        if return_tau:
-            out, tau = cache.step(q, k, v, normalize=norm, return_tau=True)
-        else:
-            out = cache.step(q, k, v, normalize=norm)
-    return layer.norm(x + layer.wo(out.reshape(N, 1, D))), tau
+        k, v = layer.wkv(x).view(N, 1, H, 2 * HD).split(HD, dim=-1)
+    q, k, v = q[:, 0], k[:, 0], v[:, 0]
+    pin, pout = cache.pos[par], cache.pos[1 - par]
+    if layer.global_layer:
+        out = decode_step(q, k, v, cache.k, cache.v, pin, pout, cache.scale, "mass", None, True)
+        if taus is not None:
+            taus.append(None)
+    else:
+        tau = None
+        if taus is not None:
+            tau = torch.empty(N, H, cache.W, dtype=q.dtype, device=q.device)
+            taus.append(tau)
+        out = decode_step(q, k, v, cache.k, cache.v, pin, pout, cache.scale,
+                          "count" if layer.count_norm else "mass", tau)
+    return layer.norm(x + layer.wo(out.reshape(N, 1, D)).to(x.dtype))
 
 
 def sample_next(logits: Tensor, history: list, temp: float = 0.8, top_p: float = 0.92,
@@ -162,9 +243,10 @@ def sample_next(logits: Tensor, history: list, temp: float = 0.8, top_p: float =
 @torch.no_grad()
 def generate_cached(model, input_ids: list, max_new: int = 200, temp: float = 0.8,
                     top_p: float = 0.92, rep_penalty: float = 1.3,
-                    generator: Optional[torch.Generator] = None) -> list:
+                    generator: Optional[torch.Generator] = None, use_graph: bool = True) -> list:
     """Autoregressive generation with per-layer K/V caches (same arguments
-    and result as the reference's ``generate_cached``, model.py:719-768)."""
+    and result as the reference's ``generate_cached``, model.py:719-768).
+    ``use_graph``: replay each cached step from a HIP graph."""
     model.eval()
     device = next(model.parameters()).device
     max_ctx = model.cfg.max_seq_len
@@ -179,7 +261,8 @@ def generate_cached(model, input_ids: list, max_new: int = 200, temp: float = 0.
         if i == max_new - 1:
             break
         if len(ids) <= max_ctx:
-            logits = cache.step(torch.tensor([nxt], dtype=torch.long, device=device))[0]
+            nid = torch.tensor([nxt], dtype=torch.long, device=device)
+            logits = (cache.graph_step(nid) if use_graph else cache.step(nid))[0]
         else:  # the reference's context slides past max_seq_len: re-run the window
             ctx = torch.tensor([ids[-max_ctx:]], dtype=torch.long, device=device)
             logits = model(ctx)[0, -1]

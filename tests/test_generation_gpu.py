@@ -83,6 +83,32 @@ def test_cached_steps_match_full_forward_bf16(dev, use_triton):
             assert err < 2e-2, (t, err)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_graph_step_matches_eager(dev, bf16):
+    """Every replay of the captured step equals the eager step (two caches
+    from the same prefill, eager work between the replays)."""
+    cfg = M.TensionConfig(vocab_size=256, dim=128, num_layers=4, num_heads=2, window=16,
+                          max_seq_len=96, dropout=0.0, global_every=2, use_rope=True,
+                          use_triton=True)
+    m = make_model(cfg, 6, dev)
+    N, P, S = 2, 30, 20
+    ids = torch.randint(0, cfg.vocab_size, (N, P + S), generator=torch.Generator().manual_seed(12)).to(dev)
+    print(f"[gen graph] bf16={bf16}", flush=True)
+    ctx = torch.autocast("cuda", dtype=torch.bfloat16) if bf16 else torch.autocast("cuda", enabled=False)
+    with torch.no_grad(), ctx:
+        ea, gr = TensionKVCache(m, N), TensionKVCache(m, N)
+        ea.prefill(ids[:, :P])
+        gr.prefill(ids[:, :P])
+        for t in range(P, P + S):
+            a = ea.step(ids[:, t]).float()
+            b = gr.graph_step(ids[:, t]).float().clone()
+            torch.cuda.synchronize()
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-5), (t, (a - b).abs().max().item())
+    for ca, cb in zip(ea.layers, gr.layers):
+        assert torch.equal(ca.k, cb.k) and torch.equal(ca.v, cb.v)
+        assert torch.equal(ca.pos[ca.cur], cb.pos[cb.cur])
+
+
 def reforward_generate(model, input_ids, max_new, temp, top_p, rep_penalty, generator):
     """The reference's generation loop (model.py:625-652) with the same sampler."""
     dev = next(model.parameters()).device
@@ -101,9 +127,10 @@ def test_generate_cached_matches_reforward(dev):
                           use_triton=True)
     m = make_model(cfg, 5, dev)
     prompt = torch.randint(0, cfg.vocab_size, (20,), generator=torch.Generator().manual_seed(10)).tolist()
-    a = generate_cached(m, prompt, max_new=40, temp=0.9, top_p=0.95, rep_penalty=1.3,
-                        generator=torch.Generator(device=dev).manual_seed(11))
     b = reforward_generate(m, prompt, 40, 0.9, 0.95, 1.3, torch.Generator(device=dev).manual_seed(11))
-    print(f"[gen sample] {a[20:30]}", flush=True)
-    assert len(a) == 60 and a[:20] == prompt
-    assert a == b
+    for use_graph in (False, True):
+        a = generate_cached(m, prompt, max_new=40, temp=0.9, top_p=0.95, rep_penalty=1.3,
+                            generator=torch.Generator(device=dev).manual_seed(11), use_graph=use_graph)
+        print(f"[gen sample] graph={use_graph} {a[20:30]}", flush=True)
+        assert len(a) == 60 and a[:20] == prompt
+        assert a == b
