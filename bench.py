@@ -636,6 +636,68 @@ def bench_generation(dev, prompt=512, new=128):
     return res
 
 
+def bench_export(dev, reps=20):
+    """Tau export reductions at the 117M shape: 9 local layers of tau
+    [1, 1024, 12, 64] bf16 (sigmoid of 2 N(0,1), a spread like a trained
+    model's), per-head profile + head-masked aggregate + Gini + edge
+    selection on the device, against the reference's host path (copy to the
+    host, numpy reductions: oracle/export_ref.py) timed on this host."""
+    from bozo_amd import export as E
+    from oracle import export_ref as X
+    Ln, B, T, H, W = 9, 1, 1024, 12, 64
+    g = torch.Generator(device=dev).manual_seed(6)
+    taus = [torch.sigmoid(torch.randn(B, T, H, W, device=dev, generator=g) * 2).to(torch.bfloat16)
+            for _ in range(Ln)]
+    mask = torch.zeros(Ln, H, dtype=torch.bool)
+    mask[:, ::3] = True
+
+    def device_path():
+        st = E.head_stats(taus)
+        agg = E.aggregate_tau(taus, mask)
+        gini, mean = E.concentration(agg)
+        emit = E._valid(T, W, dev) & (agg >= 0.6)
+        return st, torch.nonzero(emit).cpu(), agg[emit].cpu()
+
+    device_path()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        device_path()
+    torch.cuda.synchronize()
+    dev_ms = (time.perf_counter() - t0) * 1e3 / reps
+    # the two kernels alone
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        E.head_stats(taus)
+    e1.record()
+    torch.cuda.synchronize()
+    stats_us = e0.elapsed_time(e1) * 1e3 / reps
+    e0.record()
+    for _ in range(reps):
+        E.aggregate_tau(taus, mask)
+    e1.record()
+    torch.cuda.synchronize()
+    agg_us = e0.elapsed_time(e1) * 1e3 / reps
+
+    t0 = time.perf_counter()
+    n_cpu = 0
+    while time.perf_counter() - t0 < 5.0 or n_cpu == 0:
+        np_taus = [t.float().cpu().numpy() for t in taus]
+        X.head_stats(np_taus)
+        agg = X.aggregate(np_taus, mask.numpy())
+        X.concentration(agg)
+        X.edges(agg, 0.6)
+        n_cpu += 1
+    cpu_ms = (time.perf_counter() - t0) * 1e3 / n_cpu
+    tau_bytes = Ln * B * T * H * W * 2
+    return {"config": "tau export reductions, 9 layers x [1,1024,12,64] bf16 (117M shape)",
+            "device_ms": round(dev_ms, 3), "head_stats_us": round(stats_us, 1),
+            "aggregate_us": round(agg_us, 1),
+            "aggregate_GBps": round(tau_bytes / (agg_us * 1e-6) / 1e9, 1),
+            "cpu_reference_path_ms": round(cpu_ms, 1), "cpu_cores": 1}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -651,7 +713,7 @@ def main():
     ap.add_argument("--model-only", action="store_true",
                     help="only the TensionLM-117M training step (config 5), one JSON line per variant")
     ap.add_argument("--generation-only", action="store_true",
-                    help="only the TensionLM-117M cached-generation timing, one JSON line")
+                    help="only the TensionLM-117M cached-generation and tau-export timings")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize)
@@ -670,6 +732,7 @@ def main():
         return
     if args.generation_only:
         print(json.dumps(bench_generation(dev)), flush=True)
+        print(json.dumps(bench_export(dev)), flush=True)
         return
     if args.model_only:
         for aux in (False, True):
@@ -686,6 +749,9 @@ def main():
         log(f"[bench] TensionLM-117M training step (config 5, aux={aux}) ...")
         others.append(bench_model(dev, 10, 3, aux))
         log(f"[bench] {others[-1]}")
+    log("[bench] tau export reductions ...")
+    others.append(bench_export(dev))
+    log(f"[bench] {others[-1]}")
     log("[bench] TensionLM-117M cached generation ...")
     others.append(bench_generation(dev))
     log(f"[bench] {others[-1]}")

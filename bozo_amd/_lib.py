@@ -25,6 +25,7 @@ NORM_COUNT = 1 << 1
 GLOBAL = 1 << 2
 FORCE_EXACT = 1 << 3
 DECODE_SELF = 1 << 4
+TAU_VALID_ONLY = 1 << 5
 
 # status codes
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
@@ -54,6 +55,8 @@ SIGNATURES = {
     "tension_global_bwd": (_i32, [BufP] * 11 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_decode_step": (_i32, [BufP] * 7 + [_vp, _vp] + [_i64] * 4 + [_f64, _i32, _vp]),
     "tension_rope": (_i32, [BufP, BufP, _vp, _vp] + [_i64] * 6 + [_i32, _vp]),
+    "tension_tau_head_stats": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _i32, _vp]),
+    "tension_tau_aggregate": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _vp, _vp]),
     "tension_last_error": (ctypes.c_char_p, []),
     "tension_version": (ctypes.c_char_p, []),
 }

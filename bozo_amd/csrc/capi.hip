@@ -415,4 +415,49 @@ int tension_rope(const tension_buf* x, const tension_buf* y, const float* cos, c
   return launched(e, "tension_rope");
 }
 
+namespace {
+
+int check_taus(const tension_buf* taus, int32_t L, int64_t B, int64_t T, int64_t H, int64_t W, Buf* out) {
+  if (!taus) return fail(TENSION_ERR_ARG, "taus is required");
+  if (L < 1 || L > kMaxLayers) return fail(TENSION_ERR_ARG, "tau export: L=%d outside [1, %d]", L, kMaxLayers);
+  if (B < 1 || T < 1 || H < 1 || W < 1 || T * W > 0x3fffffff || B * T * H * W > ((int64_t)1 << 40))
+    return fail(TENSION_ERR_ARG, "tau export: bad sizes B=%lld T=%lld H=%lld W=%lld", (long long)B,
+                (long long)T, (long long)H, (long long)W);
+  for (int l = 0; l < L; ++l) {
+    TRY(check_buf(&taus[l], "tau", true, 3));
+    out[l] = make_buf(&taus[l]);
+  }
+  return 0;
+}
+
+}  // namespace
+
+int tension_tau_head_stats(const tension_buf* taus, int32_t L, int64_t B, int64_t T, int64_t H, int64_t W,
+                           float* stats, int32_t flags, tension_stream_t stream) {
+  TauStatParams p;
+  memset(&p, 0, sizeof p);
+  TRY(check_taus(taus, L, B, T, H, W, p.tau));
+  if (!stats) return fail(TENSION_ERR_ARG, "stats is required");
+  p.stats = stats;
+  p.L = L; p.B = (int)B; p.T = (int)T; p.H = (int)H; p.W = (int)W;
+  p.valid_only = (flags & TENSION_TAU_VALID_ONLY) ? 1 : 0;
+  hipError_t e = hipSuccess;
+  launch_tau_stats(p, hs(stream), &e);
+  return launched(e, "tension_tau_head_stats");
+}
+
+int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B, int64_t T, int64_t H, int64_t W,
+                          const int32_t* head_mask, float* agg, tension_stream_t stream) {
+  TauAggParams p;
+  memset(&p, 0, sizeof p);
+  TRY(check_taus(taus, L, B, T, H, W, p.tau));
+  if (H > 64) return fail(TENSION_ERR_UNSUPPORTED, "tau aggregate: H=%lld > 64", (long long)H);
+  if (!head_mask || !agg) return fail(TENSION_ERR_ARG, "head_mask and agg are required");
+  p.mask = head_mask; p.agg = agg;
+  p.L = L; p.B = (int)B; p.T = (int)T; p.H = (int)H; p.W = (int)W;
+  hipError_t e = hipSuccess;
+  launch_tau_aggregate(p, hs(stream), &e);
+  return launched(e, "tension_tau_aggregate");
+}
+
 }  // extern "C"

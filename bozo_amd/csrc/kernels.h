@@ -25,11 +25,30 @@ struct RopeParams {
   int inverse;
 };
 
+// tau export reductions: up to kMaxLayers layers of tau [B, T, H, W] per call
+constexpr int kMaxLayers = 32;
+
+struct TauStatParams {
+  Buf tau[kMaxLayers];
+  float* stats;  // [L, H, 4]: mean, p99, peak_pos, concentration
+  int L, B, T, H, W;
+  int valid_only;
+};
+
+struct TauAggParams {
+  Buf tau[kMaxLayers];
+  const int32_t* mask;  // [L, H], nonzero = selected
+  float* agg;           // [T, W]
+  int L, B, T, H, W;
+};
+
 // phase: 0 forward, 1 dQ, 2 dK/dV.  Return 0 when launched (HIP status in
 // *err), -1 when no kernel exists for the request.
 int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err);
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
+int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);
+int launch_tau_aggregate(const TauAggParams& p, hipStream_t st, hipError_t* err);
 
 }  // namespace tension

@@ -214,6 +214,34 @@ int tension_rope(const tension_buf* x, const tension_buf* y, const float* cos,
                  int64_t H, int64_t D, int64_t pos_offset, int32_t inverse,
                  tension_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * tau export reductions (replace the host numpy passes of the reference's
+ * graph exporter over .cpu() copies of tau).  taus: L <= 32 buffers of
+ * tau [B,T,H,W] (s[3] == 1, any float dtype), one per local layer; every
+ * statistic reads the batch mean of tau.
+ *
+ * tension_tau_head_stats -- ts_bridge/head_filter.py:98-130 (profile_heads)
+ *   and, with TENSION_TAU_VALID_ONLY (cells with t + w < W read as 0),
+ *   ts_bridge/corpus_profile.py:58-98 (_per_head_stats).  stats: device
+ *   float [L,H,4] = mean over (t, w); 0.99 quantile over (t, w) (linear
+ *   interpolation, numpy's default); mean over t of the first arg-max over
+ *   w; mean over t of the max over w.
+ * ------------------------------------------------------------------------- */
+enum { TENSION_TAU_VALID_ONLY = 1 << 5 };
+
+int tension_tau_head_stats(const tension_buf* taus, int32_t L, int64_t B,
+                           int64_t T, int64_t H, int64_t W, float* stats,
+                           int32_t flags, tension_stream_t stream);
+
+/* tension_tau_aggregate -- ts_bridge/export.py:185-200 (and the per-step
+ *   form of streaming.py:127-146): agg[t,w] (device float [T,W]) = mean over
+ *   the selected (layer, head) pairs of tau; head_mask: device int32 [L,H],
+ *   nonzero = selected; all pairs when none is.  H <= 64. */
+int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B,
+                          int64_t T, int64_t H, int64_t W,
+                          const int32_t* head_mask, float* agg,
+                          tension_stream_t stream);
+
 /* Message for the last non-OK return on the calling thread ("" if none). */
 const char* tension_last_error(void);
 
