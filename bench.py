@@ -698,6 +698,48 @@ def bench_export(dev, reps=20):
             "cpu_reference_path_ms": round(cpu_ms, 1), "cpu_cores": 1}
 
 
+def bench_bias(dev, n_edges=50000, T=1024, W=64):
+    """Graph-bias builder: a 50k-edge content map, a 1024-token context,
+    the [1, T, W] window bias and the [1, T, T] global bias built on the
+    device (content ids on the host, one lookup kernel each), against the
+    reference's Python loops (oracle/bias_ref.py) on this host."""
+    import numpy as np
+    from bozo_amd.bias import GraphBias
+    from oracle import bias_ref as R
+
+    class Tok:
+        def id_to_token(self, i):
+            return f"w{i}"
+
+    r = np.random.default_rng(7)
+    V = 4000
+    src, dst = r.integers(0, V, n_edges), r.integers(0, V, n_edges)
+    edge_map = {(f"w{a}", f"w{b}"): float(r.random()) for a, b in zip(src, dst)}
+    ids = r.integers(0, V, T).tolist()
+    gb = GraphBias(edge_map, alpha=0.5)
+    tok = Tok()
+    gb.local_bias(ids, tok, window=W, device=dev)  # table build + warm-up
+    res = {"config": f"graph bias, {len(edge_map)} edges, T={T} W={W}"}
+    for name, fn in (("local", lambda: gb.local_bias(ids, tok, window=W, device=dev)),
+                     ("global", lambda: gb.global_bias(ids, tok, device=dev))):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        res[f"{name}_device_ms"] = round((time.perf_counter() - t0) * 1e2, 3)
+    contents = [tok.id_to_token(i) for i in ids]
+    t0 = time.perf_counter()
+    R.local_bias(edge_map, 0.5, contents, W)
+    res["local_cpu_reference_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    t0 = time.perf_counter()
+    R.global_bias(edge_map, 0.5, contents[:256])
+    res["global_cpu_reference_ms_T256"] = round((time.perf_counter() - t0) * 1e3, 1)
+    res["cpu_cores"] = 1
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -713,7 +755,7 @@ def main():
     ap.add_argument("--model-only", action="store_true",
                     help="only the TensionLM-117M training step (config 5), one JSON line per variant")
     ap.add_argument("--generation-only", action="store_true",
-                    help="only the TensionLM-117M cached-generation and tau-export timings")
+                    help="only the cached-generation, tau-export and graph-bias timings")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize)
@@ -733,6 +775,7 @@ def main():
     if args.generation_only:
         print(json.dumps(bench_generation(dev)), flush=True)
         print(json.dumps(bench_export(dev)), flush=True)
+        print(json.dumps(bench_bias(dev)), flush=True)
         return
     if args.model_only:
         for aux in (False, True):
@@ -751,6 +794,9 @@ def main():
         log(f"[bench] {others[-1]}")
     log("[bench] tau export reductions ...")
     others.append(bench_export(dev))
+    log(f"[bench] {others[-1]}")
+    log("[bench] graph bias builder ...")
+    others.append(bench_bias(dev))
     log(f"[bench] {others[-1]}")
     log("[bench] TensionLM-117M cached generation ...")
     others.append(bench_generation(dev))

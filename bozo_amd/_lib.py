@@ -57,6 +57,8 @@ SIGNATURES = {
     "tension_rope": (_i32, [BufP, BufP, _vp, _vp] + [_i64] * 6 + [_i32, _vp]),
     "tension_tau_head_stats": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _i32, _vp]),
     "tension_tau_aggregate": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _vp, _vp]),
+    "tension_bias_table_insert": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _vp]),
+    "tension_bias_build": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _f64, BufP, _vp, _vp]),
     "tension_last_error": (ctypes.c_char_p, []),
     "tension_version": (ctypes.c_char_p, []),
 }

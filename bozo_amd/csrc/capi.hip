@@ -460,4 +460,41 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B, int64_t
   return launched(e, "tension_tau_aggregate");
 }
 
+int tension_bias_table_insert(const uint64_t* keys_in, const double* vals_in, int64_t n, uint64_t* table_keys,
+                              double* table_vals, int32_t log2cap, tension_stream_t stream) {
+  if (log2cap < 1 || log2cap > 40) return fail(TENSION_ERR_ARG, "bias table: log2cap=%d outside [1, 40]", log2cap);
+  if (n < 0 || 2 * n > ((int64_t)1 << log2cap))
+    return fail(TENSION_ERR_ARG, "bias table: %lld keys need a capacity of at least %lld", (long long)n,
+                (long long)(2 * n));
+  if (n == 0) return ok();
+  if (!keys_in || !vals_in || !table_keys || !table_vals) return fail(TENSION_ERR_ARG, "bias table: null pointer");
+  BiasTableParams p;
+  p.in_keys = (const unsigned long long*)keys_in; p.in_vals = vals_in; p.n = n;
+  p.keys = (unsigned long long*)table_keys; p.vals = table_vals; p.log2cap = log2cap;
+  hipError_t e = hipSuccess;
+  launch_bias_insert(p, hs(stream), &e);
+  return launched(e, "tension_bias_table_insert");
+}
+
+int tension_bias_build(const int32_t* content_ids, int64_t B, int64_t T, int64_t W, const uint64_t* table_keys,
+                       const double* table_vals, int32_t log2cap, double alpha, const tension_buf* bias,
+                       double* stats, tension_stream_t stream) {
+  if (B < 1 || T < 0 || W < 0 || T > 0x7fffffff / 2 || (W == 0 && T * T > 0x3fffffffffll))
+    return fail(TENSION_ERR_ARG, "bias build: bad sizes B=%lld T=%lld W=%lld", (long long)B, (long long)T,
+                (long long)W);
+  if (log2cap < 1 || log2cap > 40) return fail(TENSION_ERR_ARG, "bias build: log2cap=%d outside [1, 40]", log2cap);
+  if (!std::isfinite(alpha)) return fail(TENSION_ERR_ARG, "bias build: alpha must be finite");
+  if (T == 0) return ok();
+  TRY(check_buf(bias, "bias", true, 2));
+  if (!content_ids || !table_keys || !table_vals) return fail(TENSION_ERR_ARG, "bias build: null pointer");
+  BiasBuildParams p;
+  memset(&p, 0, sizeof p);
+  p.ids = content_ids; p.keys = (const unsigned long long*)table_keys; p.vals = table_vals;
+  p.log2cap = log2cap; p.alpha = alpha; p.out = bias->ptr; p.os0 = bias->s[0]; p.os1 = bias->s[1];
+  p.B = (int)B; p.T = (int)T; p.K = (int)(W > 0 ? W : T); p.global = W == 0; p.stats = stats;
+  hipError_t e = hipSuccess;
+  launch_bias_build(bias->dtype, p, hs(stream), &e);
+  return launched(e, "tension_bias_build");
+}
+
 }  // extern "C"

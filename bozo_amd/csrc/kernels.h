@@ -42,6 +42,29 @@ struct TauAggParams {
   int L, B, T, H, W;
 };
 
+// graph-bias builder: content-pair hash table and bias fill
+struct BiasTableParams {
+  const unsigned long long* in_keys;
+  const double* in_vals;
+  int64_t n;
+  unsigned long long* keys;  // [2^log2cap], empty = ~0
+  double* vals;
+  int log2cap;
+};
+
+struct BiasBuildParams {
+  const int32_t* ids;  // [T] content ids, -1 = no edges
+  const unsigned long long* keys;
+  const double* vals;
+  int log2cap;
+  double alpha;
+  void* out;            // [B, T, K], element strides os0, os1, 1
+  int64_t os0, os1;
+  int B, T, K;          // K = W (window) or T (global)
+  int global;
+  double* stats;        // [3] hits, weight sum, weight max (nullable)
+};
+
 // phase: 0 forward, 1 dQ, 2 dK/dV.  Return 0 when launched (HIP status in
 // *err), -1 when no kernel exists for the request.
 int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
@@ -50,5 +73,7 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_aggregate(const TauAggParams& p, hipStream_t st, hipError_t* err);
+int launch_bias_insert(const BiasTableParams& p, hipStream_t st, hipError_t* err);
+int launch_bias_build(int out_dtype, const BiasBuildParams& p, hipStream_t st, hipError_t* err);
 
 }  // namespace tension

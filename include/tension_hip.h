@@ -242,6 +242,34 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B,
                           const int32_t* head_mask, float* agg,
                           tension_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Graph-bias builder (ts_bridge/bias.py:125-233 GraphBias.local_bias /
+ * global_bias, whose O(T W) / O(T^2) host loops look up a content-pair ->
+ * weight map per (query, key)).  The map lives on the device as an
+ * open-addressing table: keys uint64 (src_id << 32 | dst_id), values double,
+ * capacity 2^log2cap, empty slots hold ~0 (fill table_keys with 0xff bytes
+ * first).  Hash: slot = (key * 0x9E3779B97F4A7C15) >> (64 - log2cap) (mod
+ * 2^64), linear probing.
+ *
+ * tension_bias_table_insert: insert n distinct keys (2 n <= capacity).
+ * tension_bias_build: content_ids device int32 [T] (-1 = no entry); bias
+ *   [B,T,W] (W > 0, key s = t - (W - w), zero where s < 0) or [B,T,T]
+ *   (W == 0, keys s < t), s[2] == 1, any float dtype; every element written:
+ *   alpha * weight(ids[s] -> ids[t]) where the weight is > 0, else 0.
+ *   stats (nullable, device double [3], caller-zeroed): += hits, += sum of
+ *   the hit weights, max of the hit weights.
+ * ------------------------------------------------------------------------- */
+int tension_bias_table_insert(const uint64_t* keys_in, const double* vals_in,
+                              int64_t n, uint64_t* table_keys,
+                              double* table_vals, int32_t log2cap,
+                              tension_stream_t stream);
+
+int tension_bias_build(const int32_t* content_ids, int64_t B, int64_t T,
+                       int64_t W, const uint64_t* table_keys,
+                       const double* table_vals, int32_t log2cap,
+                       double alpha, const tension_buf* bias, double* stats,
+                       tension_stream_t stream);
+
 /* Message for the last non-OK return on the calling thread ("" if none). */
 const char* tension_last_error(void);
 
