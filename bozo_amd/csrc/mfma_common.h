@@ -459,4 +459,56 @@ __device__ __forceinline__ int sub_kind(const WaveBand& w, int k0) {
   return 1;
 }
 
+// ---------------------------------------------------------------------------
+// LDS rings filled by DMA (global_load_lds) without full waits.
+//
+// __syncthreads() carries a workgroup release fence, and the compiler meets
+// it with "s_waitcnt vmcnt(0)": every copy still in flight, including the
+// prefetch of the next ring slot, has to land before the barrier, so a
+// two-deep ring degenerates to one deep.  The same happens at the first LDS
+// read the compiler cannot tell apart from a pending copy (the transposed
+// reads carry no alias information).  Ring loops therefore synchronise with
+// lds_barrier() after an explicit wait_vm<N>() for their own slot, and read
+// the ring transposed through dt_tr8_issue / tr_wait4 / tr_join.  The "memory" clobber keeps every other memory access on its
+// side of the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// dt_tr8 issued as inline asm: the compiler does not count these reads, so
+// their two halves stay in the TrRead until tr_wait4() -- lgkmcnt(0) as a
+// volatile asm that rewrites them, so no copy or use of a half can be placed
+// before it -- and only then are joined (tr_join).
+struct TrRead {
+  u16x4 lo, hi;
+};
+
+__device__ __forceinline__ TrRead dt_tr8_issue(const bf16* tile, int m, int k0, int g, int j) {
+  const int col = 16 * m + 4 * (j & 3);
+  const int r1 = k0 + 4 * g + (j >> 2), r2 = r1 + 16;
+  const bf16* a1 = tile + r1 * kTile + 8 * ((col >> 3) ^ dsw(r1)) + (col & 4);
+  const bf16* a2 = tile + r2 * kTile + 8 * ((col >> 3) ^ dsw(r2)) + (col & 4);
+  TrRead t;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(t.lo) : "v"(lds_addr(a1)));
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(t.hi) : "v"(lds_addr(a2)));
+  return t;
+}
+
+__device__ __forceinline__ void tr_wait4(TrRead* t) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(t[0].lo), "+v"(t[0].hi), "+v"(t[1].lo), "+v"(t[1].hi), "+v"(t[2].lo), "+v"(t[2].hi),
+                 "+v"(t[3].lo), "+v"(t[3].hi));
+}
+
+__device__ __forceinline__ bf16x8 tr_join(const TrRead& t) {
+  u16x8 r;
+  r[0] = t.lo[0]; r[1] = t.lo[1]; r[2] = t.lo[2]; r[3] = t.lo[3];
+  r[4] = t.hi[0]; r[5] = t.hi[1]; r[6] = t.hi[2]; r[7] = t.hi[3];
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 }  // namespace tension

@@ -17,6 +17,8 @@
 // Workgroups go out heaviest tile first; blockIdx -> (b, h) keeps every tile
 // of one (b, h) on one XCD (round-robin dispatch, B*H a multiple of 8), so its
 // 512 KB of K/V stays in that XCD's L2.
+#include <type_traits>
+
 #include "mfma_common.h"
 
 namespace tension {
@@ -63,9 +65,10 @@ void gl_fwd(BandParams p) {
   f32x4 acc[2][4] = {};
   f32x4 macc[2] = {};
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
-    __syncthreads();
+  // one 64-key block: S, P, O += P V, mass += P 1 (diag: the last block,
+  // masked key <= query)
+  auto block = [&](int blk, auto diag_tag) {
+    constexpr bool diag = decltype(diag_tag)::value;
     const bf16* Ks = Kb[blk & 1];
     const bf16* Vs = Vb[blk & 1];
     // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
@@ -81,10 +84,10 @@ void gl_fwd(BandParams p) {
         s[i][j] = mfma(a1, qf[i][1], z);
       }
     }
-    bf16x8 vt[4];
+    TrRead vr[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) vt[m] = dt_tr8(Vs, m, 32 * kh, g, c);
-    const bool diag = blk == tile;
+    for (int m = 0; m < 4; ++m) vr[m] = dt_tr8_issue(Vs, m, 32 * kh, g, c);
+    bf16x8 vt[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       float pr[2][4];
@@ -97,16 +100,31 @@ void gl_fwd(BandParams p) {
           pr[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : pv;
         }
       const bf16x8 pb = pack_b(pr[0], pr[1]);
+      if (i == 0) {
+        tr_wait4(vr);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) vt[m] = tr_join(vr[m]);
+      }
 #pragma unroll
       for (int m = 0; m < 4; ++m) acc[i][m] = mfma(vt[m], pb, acc[i][m]);
       macc[i] = mfma(ones, pb, macc[i]);
     }
+  };
+  // Off-diagonal blocks: the next block's copy (4 instructions) is always in
+  // flight here, so the wait leaves exactly it outstanding.
+  for (int blk = 0; blk + 1 < nblk; ++blk) {
+    wait_vm<4>();
+    lds_barrier();
+    block(blk, std::false_type{});
     if (blk + 2 < nblk) {
-      __syncthreads();  // every wave is done with this ring slot
+      lds_barrier();  // every wave is done with this ring slot
       tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
       tile_async_src(vsrc, (blk + 2) * kTile, Vb[blk & 1], wave);
     }
   }
+  wait_vm<0>();
+  lds_barrier();
+  block(nblk - 1, std::true_type{});
 
   // Key halves meet: wave (qh, kh) keeps query tile i = kh and hands its
   // partial of tile 1 - kh to its partner (qh, 1 - kh) through LDS:
@@ -215,9 +233,8 @@ void gl_dq(BandParams p) {
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 acc[2][4] = {};
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
-    __syncthreads();
+  auto block = [&](int blk, auto diag_tag) {
+    constexpr bool diag = decltype(diag_tag)::value;
     const bf16* Ks = Kb[blk & 1];
     const bf16* Vs = Vb[blk & 1];
     f32x4 s[2][2], dp[2][2];
@@ -236,10 +253,10 @@ void gl_dq(BandParams p) {
         dp[i][j] = mfma(v1, gf[i][1], y);
       }
     }
-    bf16x8 kt[4];
+    TrRead kr[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) kt[m] = dt_tr8(Ks, m, 32 * kh, g, c);
-    const bool diag = blk == tile;
+    for (int m = 0; m < 4; ++m) kr[m] = dt_tr8_issue(Ks, m, 32 * kh, g, c);
+    bf16x8 kt[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       float gd[2][4];
@@ -253,15 +270,28 @@ void gl_dq(BandParams p) {
           gd[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : gv;
         }
       const bf16x8 pb = pack_b(gd[0], gd[1]);
+      if (i == 0) {
+        tr_wait4(kr);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) kt[m] = tr_join(kr[m]);
+      }
 #pragma unroll
       for (int m = 0; m < 4; ++m) acc[i][m] = mfma(kt[m], pb, acc[i][m]);
     }
+  };
+  for (int blk = 0; blk + 1 < nblk; ++blk) {  // as in the forward
+    wait_vm<4>();
+    lds_barrier();
+    block(blk, std::false_type{});
     if (blk + 2 < nblk) {
-      __syncthreads();
+      lds_barrier();
       tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
       tile_async_src(vsrc, (blk + 2) * kTile, Vb[blk & 1], wave);
     }
   }
+  wait_vm<0>();
+  lds_barrier();
+  block(nblk - 1, std::true_type{});
 
   // key halves meet (as in the forward): 16 floats per lane
   __syncthreads();
@@ -303,10 +333,14 @@ void gl_dq(BandParams p) {
 // Query rows past T get a = c = 0, which zeroes their P and G.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DKV_WPE, 8)))
 void gl_dkv(BandParams p) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
-  __shared__ __attribute__((aligned(16))) float coef[2][2][kTile];  // [slot][a, c][query]
-  bf16(*Qb)[kDTile] = lds;
-  bf16(*Gb)[kDTile] = lds + 2;
+  // one LDS object: the Q / dO ring (4 tiles) and, behind it, the
+  // coefficient ring coef[slot][a, c][query] (with a second object the
+  // compiler waits for every copy in flight before each ring read)
+  __shared__ __attribute__((aligned(16))) bf16 lds[4 * kDTile + 8 * kTile];  // + 2 x 2 x 64 floats
+  float(*coef)[2][kTile] = (float(*)[2][kTile])(lds + 4 * kDTile);
+  static_assert(sizeof(lds) == 4 * kDTile * sizeof(bf16) + 2 * 2 * kTile * sizeof(float), "LDS layout");
+  bf16(*Qb)[kDTile] = (bf16(*)[kDTile])lds;
+  bf16(*Gb)[kDTile] = Qb + 2;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
@@ -335,12 +369,14 @@ void gl_dkv(BandParams p) {
     load_qfrag(vb_, p.v.s1, tk, T, g, vf[i]);
   }
   // coefficient of query block qb for thread tid < 128 (a for tid < 64, c
-  // for 64..127); 0 past T
+  // for 64..127).  Every lane loads (rows past T clamped to T - 1; such
+  // queries are zeroed where the coefficients are read) and nothing tests
+  // the value until the next block: a load under a lane branch, or a select
+  // right behind it, makes the compiler wait for every copy in flight.
   auto coef_load = [&](int qb) -> float {
     const int t = qb * kTile + (tid & 63);
-    if (tid >= 128 || t >= T) return 0.f;
-    const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
-    return wsf[(tid >> 6) * nws + wi];
+    const int64_t wi = ((int64_t)b * p.T + (t < T ? t : T - 1)) * p.H + h;
+    return wsf[((tid >> 6) & 1) * nws + wi];
   };
   const int q_first = tile;  // query blocks tile .. ntiles-1
   if (tid < 128) coef[0][tid >> 6][tid & 63] = coef_load(q_first);
@@ -355,12 +391,13 @@ void gl_dkv(BandParams p) {
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 dk[2][4] = {}, dv[2][4] = {};
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
-    __syncthreads();
+  // one 64-query block (diag: the first, masked query >= key)
+  auto block = [&](int blk, auto diag_tag) {
+    constexpr bool diag = decltype(diag_tag)::value;
     // slot (blk + 1) & 1 was last read in block blk - 1: free past the barrier
     if (blk + 1 < nblk && tid < 128) coef[(blk + 1) & 1][tid >> 6][tid & 63] = cnext;
-    if (blk + 2 < nblk) cnext = coef_load(q_first + blk + 2);
+    // unconditional (clamped to the last block) for the same reason
+    cnext = coef_load(q_first + (blk + 2 < nblk ? blk + 2 : nblk - 1));
     const bf16* Qs = Qb[blk & 1];
     const bf16* Gs = Gb[blk & 1];
     f32x4 s[2][2], dp[2][2];  // [query tile j][key tile i]
@@ -379,20 +416,29 @@ void gl_dkv(BandParams p) {
         dp[j][i] = mfma(d1, vf[i][1], y);
       }
     }
-    // a / c of queries 32 qh + 16 j + 4 g + r
+    // a / c of queries 32 qh + 16 j + 4 g + r (0 past T)
     f32x4 a4[2], c4[2];
+    const int qrow = (q_first + blk) * kTile + 32 * qh + 4 * g;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       a4[j] = *(const f32x4*)&coef[blk & 1][0][32 * qh + 16 * j + 4 * g];
       c4[j] = *(const f32x4*)&coef[blk & 1][1][32 * qh + 16 * j + 4 * g];
+      if ((q_first + blk + 1) * kTile > T) {  // the last block of a ragged sequence
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool out = qrow + 16 * j + r >= T;
+          a4[j][r] = out ? 0.f : a4[j][r];
+          c4[j][r] = out ? 0.f : c4[j][r];
+        }
+      }
     }
-    bf16x8 qt[4], gt[4];
+    TrRead qr[4], gr[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      qt[m] = dt_tr8(Qs, m, 32 * qh, g, c);
-      gt[m] = dt_tr8(Gs, m, 32 * qh, g, c);
+      qr[m] = dt_tr8_issue(Qs, m, 32 * qh, g, c);
+      gr[m] = dt_tr8_issue(Gs, m, 32 * qh, g, c);
     }
-    const bool diag = blk == 0;
+    bf16x8 qt[4], gt[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       float pa[2][4], gd[2][4];
@@ -408,23 +454,59 @@ void gl_dkv(BandParams p) {
         }
       const bf16x8 pb = pack_b(pa[0], pa[1]);
       const bf16x8 gbv = pack_b(gd[0], gd[1]);
+      if (i == 0) {
+        tr_wait4(qr);
+        tr_wait4(gr);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          qt[m] = tr_join(qr[m]);
+          gt[m] = tr_join(gr[m]);
+        }
+      }
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         dv[i][m] = mfma(gt[m], pb, dv[i][m]);
         dk[i][m] = mfma(qt[m], gbv, dk[i][m]);
       }
     }
-    if (blk + 2 < nblk) {
-      __syncthreads();
-      tile_async_src(qsrc, (q_first + blk + 2) * kTile, Qb[blk & 1], wave);
-      tile_async_src(gsrc, (q_first + blk + 2) * kTile, Gb[blk & 1], wave);
+  };
+  // Block blk's ring slot takes block blk + 2, or past the end a copy of the
+  // last block that nothing reads: with every copy and coefficient load
+  // unconditional, the compiler can tell which loads are in flight and does
+  // not add a full wait of its own before the ring reads.
+  auto refill = [&](int blk) {
+    const int nb = blk + 2 < nblk ? blk + 2 : nblk - 1;
+    lds_barrier();
+    tile_async_src(qsrc, (q_first + nb) * kTile, Qb[blk & 1], wave);
+    tile_async_src(gsrc, (q_first + nb) * kTile, Gb[blk & 1], wave);
+  };
+  // The diagonal block comes first; every block but the last has the next
+  // block's copy (4 instructions) in flight.  The barriers also publish the
+  // coefficient ring writes (lgkmcnt(0) before each).
+  if (nblk == 1) {
+    wait_vm<0>();
+    lds_barrier();
+    block(0, std::true_type{});
+  } else {
+    wait_vm<4>();
+    lds_barrier();
+    block(0, std::true_type{});
+    refill(0);
+    for (int blk = 1; blk + 1 < nblk; ++blk) {
+      wait_vm<4>();
+      lds_barrier();
+      block(blk, std::false_type{});
+      refill(blk);
     }
+    wait_vm<0>();
+    lds_barrier();
+    block(nblk - 1, std::false_type{});
   }
 
   // query halves meet: wave (kh, qh) keeps key tile i = qh and hands tile
   // 1 - qh to its partner (kh, 1 - qh): 32 floats per lane (dK, dV)
   __syncthreads();
-  float* red = (float*)&lds[0][0];  // 4 x 32 x 64 floats = the whole 32 KB
+  float* red = (float*)lds;  // 4 x 32 x 64 floats = the 32 KB of the ring
   auto give = [&](const f32x4* a, const f32x4* v) {
     float* dst = red + (2 * kh + qh) * 32 * 64 + lane;
 #pragma unroll
@@ -455,7 +537,7 @@ void gl_dkv(BandParams p) {
     }
   const int r0 = k0 + 32 * kh + 16 * qh;  // the wave's first row
   __syncthreads();
-  bf16* sb = &lds[0][0] + wave * (16 * kTile);
+  bf16* sb = lds + wave * (16 * kTile);
   store_rows_staged((bf16*)p.dk.p + b * p.dk.s0 + (int64_t)r0 * p.dk.s1 + h * p.dk.s2, p.dk.s1, T - r0, ok_,
                     (float)(1.0 / p.scale), g, c, lane, sb);
   store_rows_staged((bf16*)p.dv.p + b * p.dv.s0 + (int64_t)r0 * p.dv.s1 + h * p.dv.s2, p.dv.s1, T - r0, ov, 1.f,
