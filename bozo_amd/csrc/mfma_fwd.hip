@@ -17,9 +17,9 @@
 //     and t; a three-slot ring of LDS tiles holds them while block t+1
 //     streams in (global_load_lds), so each K/V block is fetched once per
 //     chunk and its HBM latency overlaps the previous tile's arithmetic.
-//     The slots are distinct LDS arrays selected at compile time, which lets
-//     the compiler see that reads of one slot do not wait on the DMA into
-//     another.
+//     The slots are tiles of one LDS array selected at compile time; the
+//     ring is synchronised with fence-free barriers after explicit copy
+//     waits, so reads of one slot do not wait on the DMA into another.
 //   mfma_fwd (any band, including the global block): one tile per workgroup,
 //     key blocks streamed through a two-deep ring.
 #include "mfma_common.h"
@@ -180,6 +180,10 @@ __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, co
     if (pr < 2 && !has_prev) continue;
     const bf16* Kt = pr < 2 ? Ka : Kb;
     const bf16* Vt = pr < 2 ? Va : Vb;
+    // V^T of the pair, read as counted asm (see dt_tr8_issue)
+    TrRead vr[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) vr[m] = dt_tr8_issue(Vt, m, 32 * (pr & 1), g, c);
     float pv[2][4];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
@@ -200,20 +204,25 @@ __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, co
       }
     }
     const bf16x8 pb = pack_b(pv[0], pv[1]);
+    tr_wait4(vr);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[m] = mfma(dt_tr8(Vt, m, 32 * (pr & 1), g, c), pb, acc[m]);
+    for (int m = 0; m < 4; ++m) acc[m] = mfma(tr_join(vr[m]), pb, acc[m]);
     macc = mfma(ones, pb, macc);
   }
 }
 
 template <int NORM, bool BIAS, bool TAU, bool FAST>
 __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
-  __shared__ __attribute__((aligned(16))) bf16 K0[kDTile];
-  __shared__ __attribute__((aligned(16))) bf16 K1[kDTile];
-  __shared__ __attribute__((aligned(16))) bf16 K2[kDTile];
-  __shared__ __attribute__((aligned(16))) bf16 V0[kDTile];
-  __shared__ __attribute__((aligned(16))) bf16 V1[kDTile];
-  __shared__ __attribute__((aligned(16))) bf16 V2[kDTile];
+  // the six ring tiles form one LDS object (separate objects make the
+  // compiler wait for every copy in flight before each ring read); the
+  // slots are still chosen at compile time
+  __shared__ __attribute__((aligned(16))) bf16 ring[6 * kDTile];
+  bf16* const K0 = ring;
+  bf16* const K1 = ring + kDTile;
+  bf16* const K2 = ring + 2 * kDTile;
+  bf16* const V0 = ring + 3 * kDTile;
+  bf16* const V1 = ring + 4 * kDTile;
+  bf16* const V2 = ring + 5 * kDTile;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar branches on it
   const int g = lane >> 4, c = lane & 15;
@@ -249,10 +258,58 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
   // blocks t_first - 1 .. t_first + 1, so a two-tile workgroup makes one
   // round trip to HBM instead of two.
   bf16x8 qf[2], qn[2];
+  const bool pre = t_first + 1 < t_end;
+  if constexpr (FAST) {
+    // At most two tiles, as straight-line code with every copy
+    // unconditional inside its branch (block -1 reads as block 0, which the
+    // first tile does not use), so that the compiler can count the copies in
+    // flight: tile t_first reads slots 0 and 1 while block t_first + 1 and
+    // the next Q fragment are still arriving.
+    auto fetch_any = [&](int gb, bf16* Kd, bf16* Vd) {
+      tile_async_src(ksrc, (gb > 0 ? gb : 0) * kTile, Kd, wave);
+      tile_async_src(vsrc, (gb > 0 ? gb : 0) * kTile, Vd, wave);
+    };
+    auto fast_tile = [&](int t, const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb) -> OutRow {
+      const int tq = t * kTile + wave * 16 + c;
+      f32x4 acc[4] = {}, macc = {};
+      switch (wave) {
+        case 0: fwd_tile_fast<0>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        case 1: fwd_tile_fast<1>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        case 2: fwd_tile_fast<2>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        default: fwd_tile_fast<3>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+      }
+      return fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, macc[0], true);
+    };
+    if (pre) {
+      load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
+      fetch_any(t_first - 1, K0, V0);
+      fetch_any(t_first, K1, V1);
+      fetch_any(t_first + 1, K2, V2);
+      load_qfrag(qb_, p.q.s1, (t_first + 1) * kTile + wave * 16 + c, T, g, qn);
+      wait_vm<6>();  // block t_first + 1 (4 copies) and qn (2 loads) may be in flight
+      lds_barrier();
+      const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1);
+      wait_vm<0>();
+      lds_barrier();  // slot 0 (block t_first - 1) is free: it stages the rows
+      fwd_store_staged(p, b, h, g, c, lane, wave, o0, K0);
+      qf[0] = qn[0];
+      qf[1] = qn[1];
+      const OutRow o1 = fast_tile(t_first + 1, K1, V1, K2, V2);
+      fwd_store_staged(p, b, h, g, c, lane, wave, o1, K0);
+    } else {
+      load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
+      fetch_any(t_first - 1, K0, V0);
+      fetch_any(t_first, K1, V1);
+      wait_vm<0>();
+      lds_barrier();
+      const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1);
+      fwd_store_staged(p, b, h, g, c, lane, wave, o0, K2);  // slot 2 holds no block
+    }
+    return;
+  }
   load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
   fetch(t_first - 1, K0, V0);
   fetch(t_first, K1, V1);
-  const bool pre = t_first + 1 < t_end;
   if (pre) {
     fetch(t_first + 1, K2, V2);
     load_qfrag(qb_, p.q.s1, (t_first + 1) * kTile + wave * 16 + c, T, g, qn);
@@ -272,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
     // 2 loads of its Q fragment were issued after block t's, so <= 6 may
     // still be in flight
     if (lt == 0 && pre) wait_vm<6>(); else wait_vm<0>();
-    __syncthreads();
+    lds_barrier();  // no fence: it would wait for the prefetch too
     const bool more = t + 1 < t_end;
     // FAST (at most two tiles per workgroup): slot Kn receives no block in
     // this step, and the tile that last read it finished before the barrier
