@@ -304,6 +304,49 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
   st<A>(p.y, yo + i + half, x1 * s + x2 * c);
 }
 
+// bf16 in and out, D a multiple of 16, 16-byte aligned rows and tables: one
+// thread rotates 8 pairs (16 bytes of each half and 32 bytes of each table
+// row), so a row of D = 64 is 4 consecutive threads reading whole 16-byte
+// pieces.  Both halves are read before either is written (y may alias x).
+__global__ __launch_bounds__(256) void rope_bf16_vec(RopeParams p) {
+  const int half = p.D >> 1, nq = half >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.T * p.H * nq;
+  if (idx >= total) return;
+  const int q = (int)(idx % nq);
+  int64_t r = idx / nq;
+  const int h = (int)(r % p.H);
+  r /= p.H;
+  const int t = (int)(r % p.T);
+  const int b = (int)(r / p.T);
+  const bf16* xr = (const bf16*)p.x.p + b * p.x.s0 + (int64_t)t * p.x.s1 + h * p.x.s2 + 8 * q;
+  bf16* yr = (bf16*)p.y.p + b * p.y.s0 + (int64_t)t * p.y.s1 + h * p.y.s2 + 8 * q;
+  const bf16x8 x1 = __builtin_bit_cast(bf16x8, *(const u16x8*)xr);
+  const bf16x8 x2 = __builtin_bit_cast(bf16x8, *(const u16x8*)(xr + half));
+  const int64_t to = (p.pos_offset + t) * half + 8 * q;
+  const f32x4 c0 = *(const f32x4*)(p.cos + to), c1 = *(const f32x4*)(p.cos + to + 4);
+  const f32x4 s0 = *(const f32x4*)(p.sin + to), s1 = *(const f32x4*)(p.sin + to + 4);
+  const float sg = p.inverse ? -1.f : 1.f;
+  bf16x8 y1, y2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = e < 4 ? c0[e & 3] : c1[e & 3];
+    const float sn = sg * (e < 4 ? s0[e & 3] : s1[e & 3]);
+    const float a = (float)x1[e], bb = (float)x2[e];
+    y1[e] = (bf16)(a * c - bb * sn);
+    y2[e] = (bf16)(a * sn + bb * c);
+  }
+  *(u16x8*)yr = __builtin_bit_cast(u16x8, y1);
+  *(u16x8*)(yr + half) = __builtin_bit_cast(u16x8, y2);
+}
+
+int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err) {
+  const int64_t total = (int64_t)p.B * p.T * p.H * (p.D / 16);
+  hipLaunchKernelGGL(rope_bf16_vec, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p);
+  *err = hipGetLastError();
+  return 0;
+}
+
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err) {
   const int64_t total = (int64_t)p.B * p.T * p.H * (p.D / 2);
   const unsigned grid = (unsigned)((total + 255) / 256);

@@ -71,6 +71,7 @@ int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipEr
 int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err);
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
+int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_aggregate(const TauAggParams& p, hipStream_t st, hipError_t* err);
 int launch_bias_insert(const BiasTableParams& p, hipStream_t st, hipError_t* err);

@@ -143,7 +143,7 @@ def test_decode_config4_shape_steps(dev):
 
 
 @pytest.mark.parametrize("dtype,out_dtype", [(torch.float32, None), (torch.bfloat16, torch.float32),
-                                             (torch.float64, None)])
+                                             (torch.float64, None), (torch.bfloat16, None)])
 def test_rope(dev, dtype, out_dtype):
     from bozo_amd import rope
     B, T, H, D = 2, 50, 3, 64
@@ -158,7 +158,10 @@ def test_rope(dev, dtype, out_dtype):
     want = O.rope_apply(f64(x), cos, sin, pos_offset=7)
     dwant = O.rope_apply_adjoint(dy.double().numpy(), cos, sin, pos_offset=7)
     assert y.dtype == (out_dtype or dtype)
-    assert max_abs(f64(y), want) <= 1e-5
+    if y.dtype == torch.bfloat16:  # the 16-byte kernel: one bf16 rounding of the fp32 result
+        assert np.max(np.abs(f64(y) - want) / np.maximum(np.abs(want), 1e-3)) <= 2 ** -8
+    else:
+        assert max_abs(f64(y), want) <= 1e-5
     tol = 1e-5 if dtype != torch.bfloat16 else 2e-2
     metric = max_abs if dtype != torch.bfloat16 else rel_l2
     assert metric(f64(xd.grad), dwant) <= tol
