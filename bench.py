@@ -239,6 +239,78 @@ def cpu_baseline(B, T, H, D, W, seconds=10.0):
                       f"unfold+tau-mass+autograd (oracle/torch_ref.py), {el:.1f} s on {cpu}"}
 
 
+class _ReferenceCpuOps:
+    """Swap the model's tension ops for the reference's CPU path (unfold +
+    normalisation, einsum global block, torch RoPE; oracle/torch_ref.py) for
+    the CPU baselines of the model rows."""
+
+    def __enter__(self):
+        from bozo_amd import model as M
+        from oracle import torch_ref as R
+
+        def ct(Q, K, V, window, scale, return_tau=False, bias=None, *, normalize=None):
+            raw, tau = R.unfold_tension(Q, K, V, window, scale, return_tau=True, bias=bias)
+            if normalize == "mass":
+                raw = R.normalize_mass(raw, tau)
+            elif normalize == "count":
+                raw = R.normalize_count(raw, window)
+            return (raw, tau) if return_tau else raw
+
+        def gt(Q, K, V, scale, bias=None, W_local=None):
+            out, tl = R.global_block(Q, K, V, scale, bias=bias, W_local=W_local)
+            return (out, tl) if W_local is not None else out
+
+        self.M, self.saved = M, (M.causal_tension, M.global_tension, M.rope)
+        M.causal_tension, M.global_tension = ct, gt
+        M.rope = lambda x, cos, sin, pos_offset=0, out_dtype=None: R.rope(x, cos, sin, pos_offset)
+        return self
+
+    def __exit__(self, *exc):
+        self.M.causal_tension, self.M.global_tension, self.M.rope = self.saved
+
+
+def cpu_model_baselines(seconds=10.0):
+    """The reference's CPU path for the model rows, fp32 on the host cores:
+    one 117M training step (CE + aux losses, AdamW) on one 1024-token
+    sequence, and the reference's generation step (forward over a 512-token
+    context for one new token)."""
+    import torch.nn.functional as F
+    from bozo_amd import model as M
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    cfg = M.config_117m(use_triton=False, dropout=0.0)
+    torch.manual_seed(4)
+    m = M.TensionLM(cfg)
+    opt = M.configure_adamw(m)
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, cfg.vocab_size, (1, 1025), generator=g)
+    res = {"cores": cores, "kind": "port"}
+    with _ReferenceCpuOps():
+        n, t0 = 0, time.perf_counter()
+        while n < 1 or (time.perf_counter() - t0 < seconds / 2 and n < 5):
+            lg, hid, taus = m(ids[:, :-1], return_all=True)
+            loss = (F.cross_entropy(lg.reshape(-1, cfg.vocab_size), ids[0, 1:])
+                    + 0.01 * M.manifold_closure_loss(hid) + 0.02 * M.tension_diversity_loss(taus, m.window_groups))
+            loss.backward()
+            torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            n += 1
+        el = time.perf_counter() - t0
+        res["train_tokens_per_s"] = round(1024 * n / el, 1)
+        res["train_sample"] = f"{n} steps of 1 x 1024 tokens, {el:.1f} s"
+        m.eval()
+        n, t0 = 0, time.perf_counter()
+        with torch.no_grad():
+            while n < 1 or (time.perf_counter() - t0 < seconds / 2 and n < 20):
+                m(ids[:, :512])[:, -1]
+                n += 1
+        el = time.perf_counter() - t0
+        res["generate_ms_per_token"] = round(el * 1e3 / n, 1)
+        res["generate_sample"] = f"{n} re-forwards of a 512-token context, {el:.1f} s"
+    return res
+
+
 def bench_window(args, dev):
     B, H, T, D, W = 8, 12, 1024, 64, 64
     scale = math.sqrt(D)
@@ -540,8 +612,11 @@ def bench_model(dev, steps, warmup, aux):
     emitted by every layer and the four aux losses computed (weights 0.01,
     0.02, 0, 0 as train.py:135-140 -- all four are evaluated there too);
     otherwise CE only (local layers on the valid-count path, no tau)."""
+    import gc
     import torch.nn.functional as F
     from bozo_amd import model as M
+    gc.collect()
+    torch.cuda.empty_cache()  # blocks cached by the earlier benches would be split for this one
     cfg = M.config_117m(use_triton=True)
     torch.manual_seed(4)
     m = M.TensionLM(cfg).to(dev).train()
@@ -780,6 +855,8 @@ def main():
     if args.model_only:
         for aux in (False, True):
             print(json.dumps(bench_model(dev, args.steps, args.warmup, aux)), flush=True)
+        if not args.no_cpu:
+            print(json.dumps({"cpu_model_baselines": cpu_model_baselines(args.cpu_seconds)}), flush=True)
         return
     result = bench_window(args, dev)
     log("[bench] global block (config 3) ...")
@@ -790,7 +867,7 @@ def main():
     log(f"[bench] {others[-1]}")
     for aux in (False, True):
         log(f"[bench] TensionLM-117M training step (config 5, aux={aux}) ...")
-        others.append(bench_model(dev, 10, 3, aux))
+        others.append(bench_model(dev, 10, 5, aux))
         log(f"[bench] {others[-1]}")
     log("[bench] tau export reductions ...")
     others.append(bench_export(dev))
@@ -805,6 +882,9 @@ def main():
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(1, 1024, 12, 64, 64, args.cpu_seconds)
+        log("[bench] CPU baselines of the model rows ...")
+        others.append({"config": "reference CPU path of the 117M model (fp32)",
+                       **cpu_model_baselines(args.cpu_seconds)})
     print(json.dumps(result), flush=True)
 
 
