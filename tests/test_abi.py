@@ -119,6 +119,49 @@ def test_decode_validation(lib):
     assert f(q, q, q, c, c, q, None, pos, None, 1, 1, 16, 0, 4.0, 0, None) == lib.ERR_ARG   # W = 0
 
 
+def test_decode_flag_validation(lib):
+    q = _buf(strides=(64, 16, 1, 0))
+    c = _buf()
+    pos = ctypes.c_void_p(0x2000)
+    f = lib.lib().tension_decode_step
+    assert f(q, q, q, c, c, q, None, pos, None, 1, 1, 16, 8, 4.0, lib.NORM_MASS | lib.NORM_COUNT,
+             None) == lib.ERR_ARG
+    assert b"exclusive" in lib.lib().tension_last_error()
+    tau = _buf(strides=(128, 8, 1, 0))
+    assert f(q, q, q, c, c, q, tau, pos, None, 1, 1, 16, 8, 4.0, lib.NORM_MASS | lib.DECODE_SELF,
+             None) == lib.ERR_ARG
+    assert b"not supported" in lib.lib().tension_last_error()
+
+
+def test_tau_export_validation(lib):
+    arr = (lib.TensionBuf * 1)(_buf().contents)
+    stats = ctypes.c_void_p(0x3000)
+    f = lib.lib().tension_tau_head_stats
+    assert f(arr, 0, 1, 16, 2, 8, stats, 0, None) == lib.ERR_ARG          # no layers
+    assert f(arr, 33, 1, 16, 2, 8, stats, 0, None) == lib.ERR_ARG         # more than 32
+    assert f(arr, 1, 1, 0, 2, 8, stats, 0, None) == lib.ERR_ARG           # T = 0
+    assert f(arr, 1, 1, 16, 2, 8, None, 0, None) == lib.ERR_ARG           # no output
+    bad = (lib.TensionBuf * 1)(_buf(strides=(4096, 64, 16, 2)).contents)
+    assert f(bad, 1, 1, 16, 2, 8, stats, 0, None) == lib.ERR_ARG          # innermost stride
+    g = lib.lib().tension_tau_aggregate
+    assert g(arr, 1, 1, 16, 65, 8, stats, stats, None) == lib.ERR_UNSUPPORTED  # H > 64
+    assert g(arr, 1, 1, 16, 2, 8, None, stats, None) == lib.ERR_ARG      # no mask
+
+
+def test_bias_builder_validation(lib):
+    p = ctypes.c_void_p(0x4000)
+    ins = lib.lib().tension_bias_table_insert
+    assert ins(p, p, 5, p, p, 3, None) == lib.ERR_ARG       # 5 keys need capacity >= 10 > 8
+    assert ins(p, p, 4, p, p, 0, None) == lib.ERR_ARG       # log2cap < 1
+    assert ins(None, None, 0, p, p, 3, None) == lib.OK       # nothing to insert, no launch
+    build = lib.lib().tension_bias_build
+    b = _buf(strides=(64, 8, 1, 0))
+    assert build(p, 0, 8, 8, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG              # B = 0
+    assert build(p, 1, 8, 8, p, p, 4, float("inf"), b, None, None) == lib.ERR_ARG     # alpha
+    assert build(p, 1, 8, 8, p, p, 4, 0.5, _buf(strides=(64, 8, 2, 0)), None, None) == lib.ERR_ARG
+    assert build(p, 1, 0, 8, p, p, 4, 0.5, b, None, None) == lib.OK                   # empty context
+
+
 def test_no_cpu_fallback():
     from bozo_amd import causal_tension, global_tension
     x = torch.zeros(1, 8, 1, 16)
