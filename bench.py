@@ -610,8 +610,9 @@ def bench_model(dev, steps, warmup, aux):
     autocast, AdamW as train.py:894-902, clip 1.0) on B8 x T1024 token ids
     ~ U[0, 32768).  ``aux``: the reference default, return_all with tau
     emitted by every layer and the four aux losses computed (weights 0.01,
-    0.02, 0, 0 as train.py:135-140 -- all four are evaluated there too);
-    otherwise CE only (local layers on the valid-count path, no tau)."""
+    0.02, 0, 0 as train.py:135-140 -- all four are evaluated there too; the
+    three tau losses in the fused kernels); otherwise CE only (local layers
+    on the valid-count path, no tau)."""
     import gc
     import torch.nn.functional as F
     from bozo_amd import model as M
@@ -633,11 +634,10 @@ def bench_model(dev, steps, warmup, aux):
             else:
                 logits = m(inputs)
             loss = F.cross_entropy(logits.reshape(-1, cfg.vocab_size), targets.reshape(-1))
-            if aux:
-                loss = (loss + 0.01 * M.manifold_closure_loss(hidden)
-                        + 0.02 * M.tension_diversity_loss(taus, m.window_groups)
-                        + 0.0 * M.constraint_consistency_loss(taus)
-                        + 0.0 * M.tension_entropy_loss(taus))
+            if aux:  # all four computed, as the reference does; the tau ones fused
+                div, cons, ent = M.tension_aux_losses(taus, m.window_groups)
+                loss = (loss + 0.01 * M.manifold_closure_loss(hidden) + 0.02 * div
+                        + 0.0 * cons + 0.0 * ent)
         loss.backward()
         torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
         opt.step()

@@ -58,6 +58,9 @@ SIGNATURES = {
     "tension_tau_head_stats": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _i32, _vp]),
     "tension_tau_aggregate": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _vp, _vp]),
     "tension_bias_table_insert": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _vp]),
+    "tension_aux_loss_partials": (_i64, [_i64, _i64, _i64]),
+    "tension_aux_loss_fwd": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _vp]),
+    "tension_aux_loss_bwd": (_i32, [BufP, BufP, _i32] + [_i64] * 4 + [_vp, _vp]),
     "tension_bias_build": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _f64, BufP, _vp, _vp]),
     "tension_last_error": (ctypes.c_char_p, []),
     "tension_version": (ctypes.c_char_p, []),

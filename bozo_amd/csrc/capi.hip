@@ -468,6 +468,42 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B, int64_t
   return launched(e, "tension_tau_aggregate");
 }
 
+int64_t tension_aux_loss_partials(int64_t B, int64_t T, int64_t H) {
+  const int64_t nrow = B * T * H;
+  return nrow > 0 ? (nrow * 8 + 255) / 256 : 0;
+}
+
+int tension_aux_loss_fwd(const tension_buf* taus, int32_t L, int64_t B, int64_t T, int64_t H, int64_t W,
+                         double* partials, tension_stream_t stream) {
+  AuxLossParams p;
+  memset(&p, 0, sizeof p);
+  TRY(check_taus(taus, L, B, T, H, W, p.tau));
+  if (W > 64) return fail(TENSION_ERR_UNSUPPORTED, "aux loss: W=%lld > 64", (long long)W);
+  if (!partials) return fail(TENSION_ERR_ARG, "partials is required");
+  if (B * T * H * 8 > 0x7fffffffll * 256) return fail(TENSION_ERR_ARG, "aux loss: too many rows");
+  p.acc = partials;
+  p.L = L; p.B = (int)B; p.T = (int)T; p.H = (int)H; p.W = (int)W;
+  hipError_t e = hipSuccess;
+  launch_aux_loss(false, p, hs(stream), &e);
+  return launched(e, "tension_aux_loss_fwd");
+}
+
+int tension_aux_loss_bwd(const tension_buf* taus, const tension_buf* dtaus, int32_t L, int64_t B, int64_t T,
+                         int64_t H, int64_t W, const float* coef, tension_stream_t stream) {
+  AuxLossParams p;
+  memset(&p, 0, sizeof p);
+  TRY(check_taus(taus, L, B, T, H, W, p.tau));
+  TRY(check_taus(dtaus, L, B, T, H, W, p.dtau));
+  if (W > 64) return fail(TENSION_ERR_UNSUPPORTED, "aux loss: W=%lld > 64", (long long)W);
+  if (!coef) return fail(TENSION_ERR_ARG, "coef is required");
+  if (B * T * H * 8 > 0x7fffffffll * 256) return fail(TENSION_ERR_ARG, "aux loss: too many rows");
+  p.coef = coef;
+  p.L = L; p.B = (int)B; p.T = (int)T; p.H = (int)H; p.W = (int)W;
+  hipError_t e = hipSuccess;
+  launch_aux_loss(true, p, hs(stream), &e);
+  return launched(e, "tension_aux_loss_bwd");
+}
+
 int tension_bias_table_insert(const uint64_t* keys_in, const double* vals_in, int64_t n, uint64_t* table_keys,
                               double* table_vals, int32_t log2cap, tension_stream_t stream) {
   if (log2cap < 1 || log2cap > 40) return fail(TENSION_ERR_ARG, "bias table: log2cap=%d outside [1, 40]", log2cap);

@@ -65,6 +65,15 @@ struct BiasBuildParams {
   double* stats;        // [3] hits, weight sum, weight max (nullable)
 };
 
+// fused tau regularisers: per-row passes over up to kMaxLayers layers
+struct AuxLossParams {
+  Buf tau[kMaxLayers];
+  Buf dtau[kMaxLayers];   // backward output
+  double* acc;            // forward: [L, blocks, 4] partial sums
+  const float* coef;      // backward: [L, 3] diversity, consistency, entropy
+  int L, B, T, H, W;
+};
+
 // phase: 0 forward, 1 dQ, 2 dK/dV.  Return 0 when launched (HIP status in
 // *err), -1 when no kernel exists for the request.
 int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
@@ -75,6 +84,7 @@ int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_aggregate(const TauAggParams& p, hipStream_t st, hipError_t* err);
 int launch_bias_insert(const BiasTableParams& p, hipStream_t st, hipError_t* err);
+int launch_aux_loss(bool bwd, const AuxLossParams& p, hipStream_t st, hipError_t* err);
 int launch_bias_build(int out_dtype, const BiasBuildParams& p, hipStream_t st, hipError_t* err);
 
 }  // namespace tension

@@ -374,4 +374,93 @@ def tension_entropy_loss(all_tensions: list) -> Tensor:
     return total / len(all_tensions)
 
 
+# ------------------------------------------------------------------ fused aux losses
+
+def _cons_n(W: int, T: int) -> int:
+    if W < 3 or T < 3:
+        return 0
+    n = min(W - 2, 4)
+    return n if T - (n + 1) > 0 else 0
+
+
+class _AuxLossFn(torch.autograd.Function):
+    """Diversity, consistency and entropy losses of every layer's tau in one
+    HIP pass forward and one backward (tension_aux_loss_fwd / _bwd)."""
+
+    @staticmethod
+    def forward(ctx, groups, *taus):
+        from . import _lib as Lb
+        L = len(taus)
+        B, T, H, W = taus[0].shape
+        dev = taus[0].device
+        rows = [t if t.stride(-1) == 1 else t.contiguous() for t in taus]
+        arr = (Lb.TensionBuf * L)(*[Lb.buf(t).contents for t in rows])
+        lib = Lb.lib()
+        P = lib.tension_aux_loss_partials(B, T, H)
+        part = torch.empty(L, P, 4, dtype=torch.float64, device=dev)
+        with torch.cuda.device(dev):
+            Lb.check(lib.tension_aux_loss_fwd(arr, L, B, T, H, W, part.data_ptr(),
+                                              torch.cuda.current_stream(dev).cuda_stream), "tension_aux_loss_fwd")
+        acc = part.sum(1)                                     # [L, 4]
+        nrow = B * T * H
+        div = torch.zeros((), dtype=torch.float64, device=dev)
+        active = torch.zeros(L, dtype=torch.float64, device=dev)
+        for logw, idx in groups:
+            mean_ent = acc[list(idx), 0].sum() / (len(idx) * nrow)
+            gap = logw - mean_ent
+            div = div + F.relu(gap)
+            active[list(idx)] = (gap > 0).double() / (len(idx) * nrow)
+        div = div / max(len(groups), 1)
+        n = _cons_n(W, T)
+        cons = torch.zeros((), dtype=torch.float64, device=dev)
+        if n:
+            cons = (acc[:, 1] / (n * B * (T - n - 1) * H)).sum() / L
+        ent = ((acc[:, 2] + acc[:, 3]) / nrow).sum() / L
+        ctx.save_for_backward(*rows)
+        ctx.active, ctx.meta = active, (len(groups), n, L, B, T, H, W)
+        return div.float(), cons.float(), ent.float()
+
+    @staticmethod
+    def backward(ctx, g_div, g_cons, g_ent):
+        from . import _lib as Lb
+        rows = ctx.saved_tensors
+        G, n, L, B, T, H, W = ctx.meta
+        dev = rows[0].device
+        coef = torch.zeros(L, 3, dtype=torch.float32, device=dev)
+        if g_div is not None:
+            coef[:, 0] = (-g_div.double() / max(G, 1) * ctx.active).float()
+        if g_cons is not None and n:
+            coef[:, 1] = (g_cons.double() / (L * n * B * (T - n - 1) * H)).float()
+        if g_ent is not None:
+            coef[:, 2] = (g_ent.double() / (L * B * T * H)).float()
+        dts = [torch.empty_like(t) for t in rows]
+        arr = (Lb.TensionBuf * L)(*[Lb.buf(t).contents for t in rows])
+        darr = (Lb.TensionBuf * L)(*[Lb.buf(t).contents for t in dts])
+        with torch.cuda.device(dev):
+            Lb.check(Lb.lib().tension_aux_loss_bwd(arr, darr, L, B, T, H, W, coef.data_ptr(),
+                                                   torch.cuda.current_stream(dev).cuda_stream),
+                     "tension_aux_loss_bwd")
+        return (None, *dts)
+
+
+def tension_aux_losses(all_tensions: list, window_groups: Optional[dict] = None):
+    """(tension_diversity_loss, constraint_consistency_loss,
+    tension_entropy_loss) of the same taus, in one fused pass on the GPU
+    when every tau has one [B, T, H, W] shape with W <= 64 (the model's
+    layers); otherwise the three functions above."""
+    if not all_tensions:
+        z = torch.tensor(0.0)
+        return z, z, z
+    shape = tuple(all_tensions[0].shape)
+    fused = (all_tensions[0].is_cuda and len(all_tensions) <= 32 and shape[-1] <= 64
+             and all(tuple(t.shape) == shape and t.dtype == all_tensions[0].dtype for t in all_tensions))
+    if not fused:
+        return (tension_diversity_loss(all_tensions, window_groups),
+                constraint_consistency_loss(all_tensions), tension_entropy_loss(all_tensions))
+    if window_groups is None:
+        window_groups = {shape[-1]: list(range(len(all_tensions)))}
+    groups = tuple((math.log(Wg), tuple(idx)) for Wg, idx in window_groups.items())
+    return _AuxLossFn.apply(groups, *all_tensions)
+
+
 from .generation import TensionKVCache, generate_cached, sample_next  # noqa: E402,F401

@@ -243,6 +243,34 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B,
                           tension_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * The model's tau regularisers (model.py:498-611: tension_diversity_loss,
+ * constraint_consistency_loss, tension_entropy_loss) over the tau of L <= 32
+ * layers, each [B,T,H,W] (W <= 64, s[3] == 1), computed in fp32.
+ *
+ * tension_aux_loss_fwd: partials (device double [L, P, 4], P =
+ *   tension_aux_loss_partials(B,T,H)) receives, per layer and workgroup, the
+ *   sums of: row entropy -sum p log(p + 1e-8) with p = tau / (sum tau +
+ *   1e-8); the consistency terms relu(tau[r,w1-1] tau[r-1,0] - tau[r,w1])
+ *   (w1 = 1..min(W-2,4), w1+1 <= r <= w1+T-min(W-2,4)-1); relu(0.05 - m);
+ *   relu(m - 0.8), m the row mean.  The caller sums over P and forms the
+ *   losses.
+ * tension_aux_loss_bwd: dtaus[l] = k_div[l] d(row entropy)/dtau
+ *   + k_cons[l] d(consistency terms)/dtau + k_ent[l] d(relu sums)/dtau,
+ *   coef = device float [L, 3] (k_div, k_cons, k_ent); every element of
+ *   every dtau is written.
+ * ------------------------------------------------------------------------- */
+int64_t tension_aux_loss_partials(int64_t B, int64_t T, int64_t H);
+
+int tension_aux_loss_fwd(const tension_buf* taus, int32_t L, int64_t B,
+                         int64_t T, int64_t H, int64_t W, double* partials,
+                         tension_stream_t stream);
+
+int tension_aux_loss_bwd(const tension_buf* taus, const tension_buf* dtaus,
+                         int32_t L, int64_t B, int64_t T, int64_t H,
+                         int64_t W, const float* coef,
+                         tension_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Graph-bias builder (ts_bridge/bias.py:125-233 GraphBias.local_bias /
  * global_bias, whose O(T W) / O(T^2) host loops look up a content-pair ->
  * weight map per (query, key)).  The map lives on the device as an

@@ -1,0 +1,92 @@
+"""The fused tau regularisers (tension_aux_loss_fwd / _bwd behind
+model.tension_aux_losses) against the model's PyTorch restatements of the
+reference losses (model.py:498-611), which the CPU suite pins with loops:
+loss values and dTau."""
+import math
+
+import pytest
+import torch
+
+from bozo_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+
+def taus_of(seed, L, B, T, H, W, dtype, dev):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for l in range(L):
+        x = torch.rand(B, T, H, W, generator=g)
+        x = x ** (1 + 3 * (l % 3))          # spread rows: some peaky, some flat
+        if l % 2:
+            x = 0.02 + 0.05 * x             # low-mean rows (the 0.05 floor)
+        if l == 0:
+            x = 0.75 + 0.25 * x             # high-mean rows (the 0.8 ceiling)
+        out.append(x.to(dtype).to(dev))
+    return out
+
+
+def reference(taus, groups):
+    return (M.tension_diversity_loss(taus, groups), M.constraint_consistency_loss(taus),
+            M.tension_entropy_loss(taus))
+
+
+@pytest.mark.parametrize("L,B,T,H,W,dtype,grouped", [
+    (4, 2, 37, 3, 64, torch.float32, True),
+    (3, 1, 20, 2, 5, torch.float32, False),
+    (2, 2, 9, 2, 3, torch.float32, False),     # n = 1
+    (2, 1, 12, 2, 2, torch.float32, False),    # no consistency terms (W < 3)
+    (2, 1, 5, 2, 8, torch.float32, False),     # T too short for the terms
+    (12, 2, 64, 4, 64, torch.bfloat16, True),  # the model's shape class
+])
+def test_fused_aux_losses_match_reference(dev, L, B, T, H, W, dtype, grouped):
+    taus = taus_of(L * 100 + W, L, B, T, H, W, dtype, dev)
+    groups = {W: list(range(0, L, 2)), 1024: list(range(1, L, 2))} if grouped else None
+    print(f"[aux] L={L} B={B} T={T} H={H} W={W} {dtype} grouped={grouped}", flush=True)
+    a = [t.detach().float().requires_grad_(True) for t in taus]    # reference in fp32
+    b = [t.detach().clone().requires_grad_(True) for t in taus]    # fused, tau's own dtype
+    ra = reference(a, groups)
+    fb = M.tension_aux_losses(b, groups)
+    for x, y in zip(ra, fb):
+        x, y = float(x.detach()), float(y.detach())
+        assert abs(x - y) <= 1e-5 * max(1.0, abs(x)), (x, y)
+    w = (0.7, 1.3, 2.1)   # distinct upstream weights per loss
+    sum(wi * x for wi, x in zip(w, ra)).backward()
+    sum(wi * y for wi, y in zip(w, fb)).backward()
+    for ga, gb in zip(a, b):
+        assert gb.grad.dtype == dtype
+        ref = ga.grad.double()
+        err = (gb.grad.double() - ref).abs().max().item()
+        scale = ref.abs().max().item()
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        assert err <= tol * max(scale, 1e-12) + 1e-12, (err, scale)
+
+
+def test_fused_aux_losses_in_the_model(dev):
+    """return_all taus of a bf16 model: fused and reference losses give the
+    same loss and the same parameter gradients (through the kernels' dTau)."""
+    cfg = M.TensionConfig(vocab_size=128, dim=128, num_layers=4, num_heads=2, window=64, max_seq_len=256,
+                          dropout=0.0, global_every=2, use_rope=True, use_triton=True)
+    torch.manual_seed(0)
+    m = M.TensionLM(cfg).to(dev).train()
+    ids = torch.randint(0, 128, (2, 200), generator=torch.Generator().manual_seed(1)).to(dev)
+    grads = []
+    for fused in (False, True):
+        m.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, hid, taus = m(ids, return_all=True)
+            if fused:
+                div, cons, ent = M.tension_aux_losses(taus, m.window_groups)
+            else:
+                f = [t.float() for t in taus]
+                div, cons, ent = reference(f, m.window_groups)
+            loss = 0.02 * div + 0.1 * cons + 0.05 * ent + 0.01 * M.manifold_closure_loss(hid)
+        loss.backward()
+        grads.append((float(loss), {n: p.grad.detach().float().clone() for n, p in m.named_parameters()
+                                    if p.grad is not None}))
+    (la, ga), (lb, gb) = grads
+    assert abs(la - lb) <= 1e-4 * abs(la)
+    for n in ga:
+        d = (ga[n] - gb[n]).norm().item()
+        r = ga[n].norm().item()
+        assert d <= 2e-2 * r + 1e-9, (n, d, r)
