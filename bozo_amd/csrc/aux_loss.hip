@@ -29,13 +29,36 @@ namespace {
 
 constexpr float kDivEps = 1e-8f;  // model.py:527-528
 
-// the eight values of lane chunk ch of a row (0 past W)
+// the eight values of lane chunk ch of a row (0 past W): one 16-byte load
+// for a whole aligned bf16 chunk, element loads otherwise
 __device__ __forceinline__ void row8(const Buf& b, int64_t off, int ch, int W, float* v) {
+  const int64_t o = off + 8 * ch;
+  if (b.dt == TENSION_BF16 && 8 * ch + 8 <= W && (o & 7) == 0) {
+    const bf16x8 x = __builtin_bit_cast(bf16x8, *(const u16x8*)((const bf16*)b.p + o));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)x[e];
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int w = 8 * ch + e;
     v[e] = w < W ? ld<float>(b, off + w) : 0.f;
   }
+}
+
+// store counterpart of row8
+__device__ __forceinline__ void row8_store(const Buf& b, int64_t off, int ch, int W, const float* v) {
+  const int64_t o = off + 8 * ch;
+  if (b.dt == TENSION_BF16 && 8 * ch + 8 <= W && (o & 7) == 0) {
+    bf16x8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (bf16)v[e];
+    *(u16x8*)((bf16*)b.p + o) = __builtin_bit_cast(u16x8, x);
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (8 * ch + e < W) st<float>(b, off + 8 * ch + e, v[e]);
 }
 
 __device__ __forceinline__ float at(const Buf& b, int64_t off) { return ld<float>(b, off); }
@@ -161,11 +184,7 @@ __global__ __launch_bounds__(256) void aux_loss_bwd_kernel(AuxLossParams p) {
       }
     }
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int w = 8 * ch + e;
-    if (w < p.W) st<float>(db, doff + w, g[e]);
-  }
+  row8_store(db, doff, ch, p.W, g);
 }
 
 int launch_aux_loss(bool bwd, const AuxLossParams& p, hipStream_t st, hipError_t* err) {

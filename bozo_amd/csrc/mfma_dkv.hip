@@ -169,7 +169,7 @@ void launch_mfma_dkv(const BandParams& p, hipStream_t st, unsigned nwg, int norm
 #ifndef TENSION_NO_GL_BWD
   // global block: the coefficients are in the workspace whichever way the dQ
   // phase produced them
-  if (p.glob && !bias && !dtau && norm == NORM_MASS_) {
+  if (p.glob && norm == NORM_MASS_) {  // bias and dtau_local included
     launch_gl_dkv(p, st);
     return;
   }

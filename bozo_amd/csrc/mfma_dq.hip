@@ -282,7 +282,7 @@ void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm)
     const int64_t threads = (int64_t)p.B * p.T * p.H * 8;
     hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, p);
 #ifndef TENSION_NO_GL_BWD
-    if (p.glob && !bias && !dtau) {
+    if (p.glob) {  // bias and dtau_local included
       launch_gl_dq(p, st);
       return;
     }

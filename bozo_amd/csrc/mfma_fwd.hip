@@ -470,7 +470,7 @@ void launch_gl_fwd(const BandParams& p, hipStream_t st);
 void launch_mfma_fwd(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
   const bool bias = p.bias.p != nullptr, tau = p.tau.p != nullptr;
 #ifndef TENSION_NO_GL_FWD
-  if (p.glob && !bias && !tau && norm == NORM_MASS_) {
+  if (p.glob && norm == NORM_MASS_) {  // bias and tau_local included
     launch_gl_fwd(p, st);
     return;
   }

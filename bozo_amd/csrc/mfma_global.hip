@@ -23,10 +23,26 @@
 
 namespace tension {
 
+// Optional operands of the global block, per (query, key) pair of one lane:
+// the pre-sigmoid bias [B, T, T] (head-agnostic) as -log2(e) * bias, and the
+// column of the down-sampled tau_local / dtau_local [B, T, H, Wl] (slot j =
+// key T-1-j, model.py:235-236), -1 when the pair has no slot there.  Rows and
+// keys past T are clamped for the bias load (those pairs are masked).
+__device__ __forceinline__ float gl_bias2(const BandParams& p, int b, int q, int k) {
+  const int qq = q < p.T ? q : p.T - 1, kk = k < p.T ? k : p.T - 1;
+  return -kLog2e * ld<float>(p.bias, (int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + (int64_t)kk * p.bias.s2);
+}
+
+__device__ __forceinline__ int gl_tau_col(const BandParams& p, int q, int k) {
+  const int j = p.T - 1 - k;
+  return (q < p.T && k < p.T && j < p.Wtau) ? j : -1;
+}
+
 #ifndef TENSION_GL_FWD_WPE
 #define TENSION_GL_FWD_WPE 3
 #endif
 
+template <bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_FWD_WPE, 8)))
 void gl_fwd(BandParams p) {
   // ring slots: K in lds[0..1], V in lds[2..3]; reused for the key-half merge
@@ -53,6 +69,16 @@ void gl_fwd(BandParams p) {
   bf16x8 qf[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) load_qfrag(qb_, p.q.s1, t0 + 32 * qh + 16 * i + c, T, g, qf[i]);
+  if (TAU) {
+    // tau_local slots of keys past this tile (j < T - 64 (tile + 1)) hold no
+    // pair of its queries: zero them; the visited blocks write every other
+    // slot, pair by pair, so no slot is written twice
+    const int ez = min(p.Wtau, max(0, T - (tile + 1) * kTile));
+    for (int i = tid; i < kTile * ez; i += kThreads) {
+      const int tq = t0 + i / ez;
+      if (tq < T) st<float>(p.tau, tau_off(p.tau, b, tq, h, i % ez), 0.f);
+    }
+  }
   const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
   tile_async_src(ksrc, 0, Kb[0], wave);
   tile_async_src(vsrc, 0, Vb[0], wave);
@@ -96,8 +122,14 @@ void gl_fwd(BandParams p) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[i][j][r] * k2));
+          const int key = blk * kTile + 32 * kh + 16 * j + 4 * g + r, query = t0 + dq;
+          const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
+          const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
           pr[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : pv;
+          if (TAU) {
+            const int col = gl_tau_col(p, query, key);
+            if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, query, h, col), pr[j][r]);
+          }
         }
       const bf16x8 pb = pack_b(pr[0], pr[1]);
       if (i == 0) {
@@ -189,6 +221,7 @@ void gl_fwd(BandParams p) {
 // dQ: query-centric like the forward.  Wave (qh = w & 1, kh = w >> 1):
 //   S^T = K Q^T, dP^T = V dO^T      (A = K / V rows from LDS)
 //   dQ^T += K^T G^T                  (A = K^T read transposed)
+template <bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DQ_WPE, 8)))
 void gl_dq(BandParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
@@ -265,8 +298,15 @@ void gl_dq(BandParams p) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[i][j][r] * k2));
-          const float gv = (dp[i][j][r] * ca[i] - cc[i]) * (x - x * x);
+          const int key = blk * kTile + 32 * kh + 16 * j + 4 * g + r, query = t0 + dq;
+          const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
+          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
+          float dt = dp[i][j][r] * ca[i] - cc[i];
+          if (DTAU) {
+            const int col = gl_tau_col(p, query, key);
+            if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, query, h, col));
+          }
+          const float gv = dt * (x - x * x);
           gd[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : gv;
         }
       const bf16x8 pb = pack_b(gd[0], gd[1]);
@@ -331,6 +371,7 @@ void gl_dq(BandParams p) {
 //                                      wave's K / V fragments)
 //   dV^T += dO^T (a P),  dK^T += Q^T G  (A = dO^T / Q^T read transposed)
 // Query rows past T get a = c = 0, which zeroes their P and G.
+template <bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DKV_WPE, 8)))
 void gl_dkv(BandParams p) {
   // one LDS object: the Q / dO ring (4 tiles) and, behind it, the
@@ -447,10 +488,17 @@ void gl_dkv(BandParams p) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[j][i][r] * k2));
+          const int query = (q_first + blk) * kTile + 32 * qh + 16 * j + 4 * g + r, key = k0 + dk_;
+          const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
+          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[j][i][r], k2, b2)));
           const bool off = diag && 32 * qh + 16 * j + 4 * g + r < dk_;  // query before key
+          float dt = dp[j][i][r] * a4[j][r] - c4[j][r];
+          if (DTAU) {
+            const int col = gl_tau_col(p, query, key);
+            if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, query, h, col));
+          }
           pa[j][r] = off ? 0.f : x * a4[j][r];
-          gd[j][r] = off ? 0.f : (dp[j][i][r] * a4[j][r] - c4[j][r]) * (x - x * x);
+          gd[j][r] = off ? 0.f : dt * (x - x * x);
         }
       const bf16x8 pb = pack_b(pa[0], pa[1]);
       const bf16x8 gbv = pack_b(gd[0], gd[1]);
@@ -544,19 +592,26 @@ void gl_dkv(BandParams p) {
                     g, c, lane, sb);
 }
 
-void launch_gl_dq(const BandParams& p, hipStream_t st) {
-  const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);
-  hipLaunchKernelGGL(gl_dq, dim3(n), dim3(kThreads), 0, st, p);
-}
+// the optional operands are template switches (BIAS: p.bias, TAU / DTAU:
+// p.tau / p.dtau)
+#define GL_LAUNCH(kernel, x, y)                                                        \
+  do {                                                                                 \
+    const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);                      \
+    if (x) {                                                                           \
+      if (y) hipLaunchKernelGGL((kernel<true, true>), dim3(n), dim3(kThreads), 0, st, p);   \
+      else hipLaunchKernelGGL((kernel<true, false>), dim3(n), dim3(kThreads), 0, st, p);    \
+    } else {                                                                           \
+      if (y) hipLaunchKernelGGL((kernel<false, true>), dim3(n), dim3(kThreads), 0, st, p);  \
+      else hipLaunchKernelGGL((kernel<false, false>), dim3(n), dim3(kThreads), 0, st, p);   \
+    }                                                                                  \
+  } while (0)
 
-void launch_gl_dkv(const BandParams& p, hipStream_t st) {
-  const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);
-  hipLaunchKernelGGL(gl_dkv, dim3(n), dim3(kThreads), 0, st, p);
-}
+void launch_gl_dq(const BandParams& p, hipStream_t st) { GL_LAUNCH(gl_dq, p.bias.p, p.dtau.p); }
 
-void launch_gl_fwd(const BandParams& p, hipStream_t st) {
-  const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);
-  hipLaunchKernelGGL(gl_fwd, dim3(n), dim3(kThreads), 0, st, p);
-}
+void launch_gl_dkv(const BandParams& p, hipStream_t st) { GL_LAUNCH(gl_dkv, p.bias.p, p.dtau.p); }
+
+void launch_gl_fwd(const BandParams& p, hipStream_t st) { GL_LAUNCH(gl_fwd, p.bias.p, p.tau.p); }
+
+#undef GL_LAUNCH
 
 }  // namespace tension

@@ -82,7 +82,7 @@ def test_fused_aux_losses_in_the_model(dev):
                 div, cons, ent = reference(f, m.window_groups)
             loss = 0.02 * div + 0.1 * cons + 0.05 * ent + 0.01 * M.manifold_closure_loss(hid)
         loss.backward()
-        grads.append((float(loss), {n: p.grad.detach().float().clone() for n, p in m.named_parameters()
+        grads.append((loss.item(), {n: p.grad.detach().float().clone() for n, p in m.named_parameters()
                                     if p.grad is not None}))
     (la, ga), (lb, gb) = grads
     assert abs(la - lb) <= 1e-4 * abs(la)

@@ -46,6 +46,19 @@ def check(hip, ref, dtype, tl_checked=False):
         assert max_abs(f64(hip[1]), ref[1]) <= lim
 
 
+@pytest.mark.parametrize("use_bias,use_tl", [(True, False), (False, True), (True, True)])
+def test_global_bf16_bias_tau_local(dev, use_bias, use_tl):
+    """The dedicated global kernels with each optional operand: bias [B,T,T]
+    and the tau_local output / dtau_local input (W_local = 64)."""
+    B, H, T, D = 2, 2, 200, 64
+    inp = make_inputs(B, T, H, D, seed=7, std=0.5, dtype=torch.bfloat16, W=64, dtau_std=0.1,
+                      bias_std=0.5, bias_shape=(B, T, T))
+    wl = 64 if use_tl else None
+    hip = hip_run(inp, 8.0, dev, W_local=wl, use_bias=use_bias, use_dtl=use_tl)
+    ref = oracle_run(inp, 8.0, W_local=wl, use_bias=use_bias, use_dtl=use_tl)
+    check(hip, ref, torch.bfloat16, use_tl)
+
+
 def test_config3_bf16_full_size(dev):
     """B4 H12 T2048 d64 bf16, full causal, tau-mass."""
     B, H, T, D = 4, 12, 2048, 64
