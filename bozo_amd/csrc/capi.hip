@@ -470,7 +470,7 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B, int64_t
 
 int64_t tension_aux_loss_partials(int64_t B, int64_t T, int64_t H) {
   const int64_t nrow = B * T * H;
-  return nrow > 0 ? (nrow * 8 + 255) / 256 : 0;
+  return nrow > 0 ? aux_loss_blocks(nrow) : 0;
 }
 
 int tension_aux_loss_fwd(const tension_buf* taus, int32_t L, int64_t B, int64_t T, int64_t H, int64_t W,

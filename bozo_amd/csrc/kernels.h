@@ -84,6 +84,9 @@ int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_aggregate(const TauAggParams& p, hipStream_t st, hipError_t* err);
 int launch_bias_insert(const BiasTableParams& p, hipStream_t st, hipError_t* err);
+// rows per aux-loss workgroup, and the workgroups (partial-sum slots) per layer
+constexpr int kAuxRowsPerBlock = 1024;
+inline int64_t aux_loss_blocks(int64_t nrow) { return (nrow + kAuxRowsPerBlock - 1) / kAuxRowsPerBlock; }
 int launch_aux_loss(bool bwd, const AuxLossParams& p, hipStream_t st, hipError_t* err);
 int launch_bias_build(int out_dtype, const BiasBuildParams& p, hipStream_t st, hipError_t* err);
 

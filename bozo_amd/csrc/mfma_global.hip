@@ -74,9 +74,20 @@ void gl_fwd(BandParams p) {
     // pair of its queries: zero them; the visited blocks write every other
     // slot, pair by pair, so no slot is written twice
     const int ez = min(p.Wtau, max(0, T - (tile + 1) * kTile));
-    for (int i = tid; i < kTile * ez; i += kThreads) {
-      const int tq = t0 + i / ez;
-      if (tq < T) st<float>(p.tau, tau_off(p.tau, b, tq, h, i % ez), 0.f);
+    const bool vec = p.tau.dt == TENSION_BF16 && (ez & 7) == 0 && ((p.tau.s0 | p.tau.s1 | p.tau.s2) & 7) == 0 &&
+                     ((uintptr_t)p.tau.p & 15) == 0;
+    if (vec) {  // 16-byte pieces of zeros
+      const int n8 = ez >> 3;
+      const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = tid; i < kTile * n8; i += kThreads) {
+        const int tq = t0 + i / n8;
+        if (tq < T) *(u16x8*)((bf16*)p.tau.p + tau_off(p.tau, b, tq, h, 8 * (i % n8))) = zero;
+      }
+    } else {
+      for (int i = tid; i < kTile * ez; i += kThreads) {
+        const int tq = t0 + i / ez;
+        if (tq < T) st<float>(p.tau, tau_off(p.tau, b, tq, h, i % ez), 0.f);
+      }
     }
   }
   const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
@@ -92,9 +103,10 @@ void gl_fwd(BandParams p) {
   f32x4 macc[2] = {};
 
   // one 64-key block: S, P, O += P V, mass += P 1 (diag: the last block,
-  // masked key <= query)
-  auto block = [&](int blk, auto diag_tag) {
+  // masked key <= query; TB: the block holds tau_local columns)
+  auto block = [&](int blk, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
     constexpr bool diag = decltype(diag_tag)::value;
+    constexpr bool TB = TAU && decltype(tau_tag)::value;
     const bf16* Ks = Kb[blk & 1];
     const bf16* Vs = Vb[blk & 1];
     // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
@@ -126,7 +138,7 @@ void gl_fwd(BandParams p) {
           const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
           const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
           pr[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : pv;
-          if (TAU) {
+          if (TB) {
             const int col = gl_tau_col(p, query, key);
             if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, query, h, col), pr[j][r]);
           }
@@ -142,12 +154,23 @@ void gl_fwd(BandParams p) {
       macc[i] = mfma(ones, pb, macc[i]);
     }
   };
+  // tau_local columns are keys T - Wtau .. T - 1: only the blocks that hold
+  // one run the per-pair column code
+  auto visit = [&](int blk, auto diag_tag) __attribute__((always_inline)) {
+    if constexpr (TAU) {
+      if ((blk + 1) * kTile > T - p.Wtau) {
+        block(blk, diag_tag, std::true_type{});
+        return;
+      }
+    }
+    block(blk, diag_tag, std::false_type{});
+  };
   // Off-diagonal blocks: the next block's copy (4 instructions) is always in
   // flight here, so the wait leaves exactly it outstanding.
   for (int blk = 0; blk + 1 < nblk; ++blk) {
     wait_vm<4>();
     lds_barrier();
-    block(blk, std::false_type{});
+    visit(blk, std::false_type{});
     if (blk + 2 < nblk) {
       lds_barrier();  // every wave is done with this ring slot
       tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
@@ -156,7 +179,7 @@ void gl_fwd(BandParams p) {
   }
   wait_vm<0>();
   lds_barrier();
-  block(nblk - 1, std::true_type{});
+  visit(nblk - 1, std::true_type{});
 
   // Key halves meet: wave (qh, kh) keeps query tile i = kh and hands its
   // partial of tile 1 - kh to its partner (qh, 1 - kh) through LDS:
@@ -266,8 +289,9 @@ void gl_dq(BandParams p) {
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 acc[2][4] = {};
 
-  auto block = [&](int blk, auto diag_tag) {
+  auto block = [&](int blk, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
     constexpr bool diag = decltype(diag_tag)::value;
+    constexpr bool TB = DTAU && decltype(tau_tag)::value;  // the block holds dtau_local columns
     const bf16* Ks = Kb[blk & 1];
     const bf16* Vs = Vb[blk & 1];
     f32x4 s[2][2], dp[2][2];
@@ -302,7 +326,7 @@ void gl_dq(BandParams p) {
           const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
           const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
           float dt = dp[i][j][r] * ca[i] - cc[i];
-          if (DTAU) {
+          if (TB) {
             const int col = gl_tau_col(p, query, key);
             if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, query, h, col));
           }
@@ -319,10 +343,19 @@ void gl_dq(BandParams p) {
       for (int m = 0; m < 4; ++m) acc[i][m] = mfma(kt[m], pb, acc[i][m]);
     }
   };
+  auto visit = [&](int blk, auto diag_tag) __attribute__((always_inline)) {  // as in the forward
+    if constexpr (DTAU) {
+      if ((blk + 1) * kTile > T - p.Wtau) {
+        block(blk, diag_tag, std::true_type{});
+        return;
+      }
+    }
+    block(blk, diag_tag, std::false_type{});
+  };
   for (int blk = 0; blk + 1 < nblk; ++blk) {  // as in the forward
     wait_vm<4>();
     lds_barrier();
-    block(blk, std::false_type{});
+    visit(blk, std::false_type{});
     if (blk + 2 < nblk) {
       lds_barrier();
       tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
@@ -331,7 +364,7 @@ void gl_dq(BandParams p) {
   }
   wait_vm<0>();
   lds_barrier();
-  block(nblk - 1, std::true_type{});
+  visit(nblk - 1, std::true_type{});
 
   // key halves meet (as in the forward): 16 floats per lane
   __syncthreads();
@@ -432,9 +465,11 @@ void gl_dkv(BandParams p) {
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   f32x4 dk[2][4] = {}, dv[2][4] = {};
 
-  // one 64-query block (diag: the first, masked query >= key)
-  auto block = [&](int blk, auto diag_tag) {
+  // one 64-query block (diag: the first, masked query >= key; TB: the key
+  // tile holds dtau_local columns)
+  auto block = [&](int blk, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
     constexpr bool diag = decltype(diag_tag)::value;
+    constexpr bool TB = DTAU && decltype(tau_tag)::value;
     // slot (blk + 1) & 1 was last read in block blk - 1: free past the barrier
     if (blk + 1 < nblk && tid < 128) coef[(blk + 1) & 1][tid >> 6][tid & 63] = cnext;
     // unconditional (clamped to the last block) for the same reason
@@ -493,7 +528,7 @@ void gl_dkv(BandParams p) {
           const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[j][i][r], k2, b2)));
           const bool off = diag && 32 * qh + 16 * j + 4 * g + r < dk_;  // query before key
           float dt = dp[j][i][r] * a4[j][r] - c4[j][r];
-          if (DTAU) {
+          if (TB) {
             const int col = gl_tau_col(p, query, key);
             if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, query, h, col));
           }
@@ -531,24 +566,36 @@ void gl_dkv(BandParams p) {
   // The diagonal block comes first; every block but the last has the next
   // block's copy (4 instructions) in flight.  The barriers also publish the
   // coefficient ring writes (lgkmcnt(0) before each).
+  // dtau_local columns are keys T - Wtau .. T - 1: only key tiles that hold
+  // one run the per-pair column code
+  const bool kt_tau = DTAU && k0 + kTile > T - p.Wtau;
+  auto visit = [&](int blk, auto diag_tag) __attribute__((always_inline)) {
+    if constexpr (DTAU) {
+      if (kt_tau) {
+        block(blk, diag_tag, std::true_type{});
+        return;
+      }
+    }
+    block(blk, diag_tag, std::false_type{});
+  };
   if (nblk == 1) {
     wait_vm<0>();
     lds_barrier();
-    block(0, std::true_type{});
+    visit(0, std::true_type{});
   } else {
     wait_vm<4>();
     lds_barrier();
-    block(0, std::true_type{});
+    visit(0, std::true_type{});
     refill(0);
     for (int blk = 1; blk + 1 < nblk; ++blk) {
       wait_vm<4>();
       lds_barrier();
-      block(blk, std::false_type{});
+      visit(blk, std::false_type{});
       refill(blk);
     }
     wait_vm<0>();
     lds_barrier();
-    block(nblk - 1, std::false_type{});
+    visit(nblk - 1, std::false_type{});
   }
 
   // query halves meet: wave (kh, qh) keeps key tile i = qh and hands tile
