@@ -39,16 +39,17 @@ namespace tension {
 #define TENSION_BWD_WAVES_PER_EU 2
 #endif
 
-// FAST (W = 64, T a multiple of 64, no bias / dTau): the band of every
+// FAST (W = 64, T a multiple of 64, no bias; dTau in bf16 rows): the band of every
 // 16-query group is the same five key groups -- slot 0 the old block's
 // diagonal group (key >= query - 64, i.e. 4g + r >= c within the group),
 // slots 1..3 entirely valid, slot 4 the new block's diagonal group (key <=
 // query - 1, i.e. 4g + r < c) -- so the masks are two per-lane constants and
-// no per-element index arithmetic is needed.
+// no per-element index arithmetic is needed.  With dTau, the step's dTau
+// rows wait in each wave's G exchange sub-tiles until phase 1 reads them.
 template <int NORM, bool BIAS, bool DTAU, bool FAST>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_BWD_WAVES_PER_EU, TENSION_BWD_WAVES_PER_EU)))
 void mfma_bwd_fused(BandParams p) {
-  static_assert(!FAST || (!BIAS && !DTAU), "the fast path has no bias / dTau");
+  static_assert(!FAST || !BIAS, "the fast path has no bias");
   __shared__ __attribute__((aligned(16))) bf16 Kt[2][kDTile];  // key block k in slot k & 1
   __shared__ __attribute__((aligned(16))) bf16 Vt[2][kDTile];
   __shared__ __attribute__((aligned(16))) bf16 Qt[kDTile];     // query tile of the step
@@ -83,23 +84,66 @@ void mfma_bwd_fused(BandParams p) {
   const SeqBuf sv = seq_view(p.v, b, h, T), so = seq_view(p.dout, b, h, T);
   const SeqBuf sdq = seq_view(p.dq, b, h, T), sdk = seq_view(p.dk, b, h, T);
   const SeqBuf sdv = seq_view(p.dv, b, h, T);
-  // thread tid moves 16 bytes of two staged tile rows (staged_row)
-  const uint32_t lq = seq_lane_off(sq, tid), lk = seq_lane_off(sk, tid);
-  const uint32_t lv = seq_lane_off(sv, tid), lo_ = seq_lane_off(so, tid);
+  constexpr bool FDT = FAST && DTAU;  // dTau rows staged in the exchange tiles
+  // thread tid moves 16 bytes of two staged tile rows (staged_row).  With
+  // dTau the offsets are formed where they are used, from an opaque copy of
+  // the thread index: as five loop-invariant registers they would push the
+  // full register file into scratch.
+  auto loff = [&](const SeqBuf& sb, uint32_t pre) -> uint32_t {
+    if constexpr (FDT) {
+      int x;
+      asm volatile("v_mov_b32 %0, %1" : "=v"(x) : "v"(tid));
+      return seq_lane_off(sb, x);
+    } else {
+      return pre;
+    }
+  };
+  const uint32_t lq0 = FDT ? 0u : seq_lane_off(sq, tid), lk0 = FDT ? 0u : seq_lane_off(sk, tid);
+  const uint32_t lv0 = FDT ? 0u : seq_lane_off(sv, tid), lo0 = FDT ? 0u : seq_lane_off(so, tid);
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
+  SeqBuf sdt;
+  if constexpr (FDT) sdt = seq_view(p.dtau, b, h, T);
+  // FAST dTau: this wave's 16 dTau rows wait in its own G exchange sub-tiles
+  // (free from the end of the previous phase 2 until this wave's phase 1
+  // writes G there), row c shifted by c: slot s of query c sits at position
+  // p = s + c of an 80-position row, position p in sub-tile p >> 4, column
+  // p & 15.  Lane (g, c) then finds the dTau of its pairs (slots 16 sl + 4 g
+  // + r - c) at sub-tile sl, row c, columns 4g..4g+3 -- exactly where it
+  // writes their G afterwards, so no other lane touches them in between.
+  auto dt_stage = [&](const TileRegs& x) {
+    const int ra = (lane >> 3) & 7, ch = lane & 7;
+    bf16* const base = XG + w * (kXSlots * kXSub);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = ra + 8 * hf;
+      const bf16x8 v = __builtin_bit_cast(bf16x8, hf ? x.b : x.a);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int pos = 8 * ch + e + row;
+        base[(pos >> 4) * kXSub + row * 16 + (pos & 15)] = v[e];
+      }
+    }
+  };
+  // the four dTau values of slot group sl of this lane's pairs, read just
+  // before their use: the empty asm keeps the compiler from hoisting all
+  // five reads (ten live registers) into the register-bound phase 1
+  auto dt_at = [&](int sl) -> bf16x4 {
+    asm volatile("" ::: "memory");
+    return __builtin_bit_cast(bf16x4, *(const u16x4*)(XG + (w * kXSlots + sl) * kXSub + c * 16 + 4 * g));
+  };
 
   // ---- prologue: blocks tA-1 (if any) and tA, tile tA
   {
     const uint32_t r0 = (uint32_t)(tA * kTile);
-    TileRegs k0 = seq_tile_load(sk, r0 * sk.rs2, lk);
-    TileRegs v0 = seq_tile_load(sv, r0 * sv.rs2, lv);
-    TileRegs q0 = seq_tile_load(sq, r0 * sq.rs2, lq);
-    TileRegs o0 = seq_tile_load(so, r0 * so.rs2, lo_);
+    TileRegs k0 = seq_tile_load(sk, r0 * sk.rs2, loff(sk, lk0));
+    TileRegs v0 = seq_tile_load(sv, r0 * sv.rs2, loff(sv, lv0));
+    TileRegs q0 = seq_tile_load(sq, r0 * sq.rs2, loff(sq, lq0));
+    TileRegs o0 = seq_tile_load(so, r0 * so.rs2, loff(so, lo0));
     if (tA >= 1) {
       const uint32_t rm = r0 - kTile;
-      TileRegs km = seq_tile_load(sk, rm * sk.rs2, lk);
-      TileRegs vm = seq_tile_load(sv, rm * sv.rs2, lv);
+      TileRegs km = seq_tile_load(sk, rm * sk.rs2, loff(sk, lk0));
+      TileRegs vm = seq_tile_load(sv, rm * sv.rs2, loff(sv, lv0));
       tile_store_direct(km, Kt[(tA - 1) & 1], tid);
       tile_store_direct(vm, Vt[(tA - 1) & 1], tid);
     }
@@ -107,6 +151,7 @@ void mfma_bwd_fused(BandParams p) {
     tile_store_direct(v0, Vt[tA & 1], tid);
     tile_store_direct(q0, Qt, tid);
     tile_store_direct(o0, Ot, tid);
+    if constexpr (FDT) dt_stage(seq_tile_load(sdt, r0 * sdt.rs2, loff(sdt, 0)));
   }
   __syncthreads();
   // this wave's Q/dO fragments (query 16w + c, features 8g.., 32+8g..)
@@ -118,13 +163,12 @@ void mfma_bwd_fused(BandParams p) {
 
   // dK/dV of block t-1 (key group w), carried from step t-1 to step t
   f32x4 dk_old[4] = {}, dv_old[4] = {};
+  TileRegs dnext;  // FAST dTau: the next step's rows
   // FAST: diagonal-group masks (1 valid, 0 not) for keys 4g + r of query c
-  float mo[4], mn[4];
+  // (lane conditions: the compiler keeps them as scalar lane masks)
+  bool mo[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    mo[r] = 4 * g + r >= c ? 1.f : 0.f;
-    mn[r] = 1.f - mo[r];
-  }
+  for (int r = 0; r < 4; ++r) mo[r] = 4 * g + r >= c;  // slot 0 keeps these; slot 4 the rest
 
   // FAST phase 1 with all five slots live (steps t >= 1; the halo only with
   // tau-mass normalisation): slot sl is key group w + sl of blocks t-1, t;
@@ -157,8 +201,8 @@ void mfma_bwd_fused(BandParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float x = sigmoid_scaled(sv[sl][r], k2, 0.f);
-        if (sl == 0) x *= mo[r];
-        if (sl == kXSlots - 1) x *= mn[r];
+        if (sl == 0) x = mo[r] ? x : 0.f;
+        if (sl == kXSlots - 1) x = mo[r] ? 0.f : x;
         pv[sl][r] = x;
       }
       // short sums instead of one 20-long dependent chain
@@ -182,10 +226,18 @@ void mfma_bwd_fused(BandParams p) {
 #pragma unroll
     for (int sl = 0; sl < kXSlots; ++sl) {
       float gq[4], pq[4];
+      bf16x4 dtv;
+      if constexpr (FDT) dtv = dt_at(sl);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float x = pv[sl][r];
-        gq[r] = fmaf(dv[sl][r], ca, -cc) * fmaf(-x, x, x);
+        float dt = fmaf(dv[sl][r], ca, -cc);
+        if constexpr (FDT) {
+          // positions outside the row (masked pairs, P = 0) hold stale bits
+          const float d = (float)dtv[r];
+          dt += (sl == 0 && !mo[r]) || (sl == kXSlots - 1 && mo[r]) ? 0.f : d;
+        }
+        gq[r] = dt * fmaf(-x, x, x);
         pq[r] = x * ca;
       }
       gb[sl] = bf16x4_bits(gq[0], gq[1], gq[2], gq[3]);
@@ -218,13 +270,23 @@ void mfma_bwd_fused(BandParams p) {
     const bool halo = t >= tB;
     const bool more = t < tE;
     // ---- prefetch of step t+1 into registers
+    // dTau rows of this step, loaded during the previous step's phase 2
+    // (the previous phase 2 has finished reading the exchange tiles)
+    if (FDT && t > tA) {
+      dt_stage(dnext);
+      // the writes stay here: sunk into phase 1 they would keep dnext's
+      // registers live where the register file is full
+      asm volatile("" ::: "memory");
+    }
     TileRegs kn, vn, qn, on;
     if (more) {
       const uint32_t r0 = (uint32_t)((t + 1) * kTile);
-      kn = seq_tile_load(sk, r0 * sk.rs2, lk);
-      vn = seq_tile_load(sv, r0 * sv.rs2, lv);
-      qn = seq_tile_load(sq, r0 * sq.rs2, lq);
-      on = seq_tile_load(so, r0 * so.rs2, lo_);
+      kn = seq_tile_load(sk, r0 * sk.rs2, loff(sk, lk0));
+      vn = seq_tile_load(sv, r0 * sv.rs2, loff(sv, lv0));
+      if constexpr (!FDT) {  // with dTau: issued at the start of phase 2
+        qn = seq_tile_load(sq, r0 * sq.rs2, loff(sq, lq0));
+        on = seq_tile_load(so, r0 * so.rs2, loff(so, lo0));
+      }
     }
 
     // ---- phase 1: queries 16w..16w+15 of tile t
@@ -280,8 +342,8 @@ void mfma_bwd_fused(BandParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float x = sigmoid_scaled(s[r], k2, 0.f);
-          if (sl == 0) x *= mo[r];
-          if (sl == kXSlots - 1) x *= mn[r];
+          if (sl == 0) x = mo[r] ? x : 0.f;
+          if (sl == kXSlots - 1) x = mo[r] ? 0.f : x;
           pv[sl][r] = x;
           if (NORM == NORM_MASS_) {
             msum += x;
@@ -327,10 +389,17 @@ void mfma_bwd_fused(BandParams p) {
 #pragma unroll
       for (int sl = 0; sl < kXSlots; ++sl) {
         float gq[4], pq[4];
+        bf16x4 dtv;
+        if constexpr (FDT) dtv = dt_at(sl);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float x = pv[sl][r];
-          gq[r] = fmaf(dpv[sl][r], ca, -cc) * fmaf(-x, x, x);
+          float dt = fmaf(dpv[sl][r], ca, -cc);
+          if constexpr (FDT) {
+            const float d = (float)dtv[r];
+            dt += (sl == 0 && !mo[r]) || (sl == kXSlots - 1 && mo[r]) ? 0.f : d;
+          }
+          gq[r] = dt * fmaf(-x, x, x);
           pq[r] = x * ca;
         }
         gb[sl] = bf16x4_bits(gq[0], gq[1], gq[2], gq[3]);
@@ -408,6 +477,14 @@ void mfma_bwd_fused(BandParams p) {
     if (more) {  // block t+1 replaces block t-1
       tile_store_direct(kn, Kt[(t + 1) & 1], tid);
       tile_store_direct(vn, Vt[(t + 1) & 1], tid);
+      if constexpr (FDT) {
+        // the next Q / dO tiles and dTau rows: loaded here rather than with
+        // K / V at the step's start, so that phase 1 has registers for dTau
+        const uint32_t r1 = (uint32_t)((t + 1) * kTile);
+        qn = seq_tile_load(sq, r1 * sq.rs2, loff(sq, lq0));
+        on = seq_tile_load(so, r1 * so.rs2, loff(so, lo0));
+        dnext = seq_tile_load(sdt, r1 * sdt.rs2, loff(sdt, 0));
+      }
     }
 
     // ---- phase 2: keys 16w..16w+15 of block t-1 (key group w) and of
@@ -490,7 +567,14 @@ static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, b
   if (bias) {
     if (dtau) go<NORM, true, true, false>(p, st, nwg); else go<NORM, true, false, false>(p, st, nwg);
   } else if (dtau) {
-    go<NORM, false, true, false>(p, st, nwg);
+    // bf16 dTau rows of 64 slots, 16-byte aligned: staged by the fast path
+    const Buf& d = p.dtau;
+    const bool rows16 = d.dt == TENSION_BF16 && ((d.s0 | d.s1 | d.s2) & 7) == 0 && ((uintptr_t)d.p & 15) == 0 &&
+                        (int64_t)(p.T + 2 * kTile) * d.s1 * 2 < (int64_t)1 << 32;
+    if (p.win == kTile && p.T % kTile == 0 && rows16)
+      go<NORM, false, true, true>(p, st, nwg);
+    else
+      go<NORM, false, true, false>(p, st, nwg);
   } else if (p.win == kTile && p.T % kTile == 0) {
     go<NORM, false, false, true>(p, st, nwg);
   } else {

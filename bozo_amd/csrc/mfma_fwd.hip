@@ -157,6 +157,31 @@ __device__ __forceinline__ void fwd_store_staged(const BandParams& p, int b, int
   if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)o.tq * p.mass.s1 + h * p.mass.s2, o.msum);
 }
 
+// FAST-path tau rows (W = 64, bf16, 16-byte rows): lane (g, c) holds the tau
+// of query c at slots 16 s5 + 4 g + r - c (s5 = 0..4, r = 0..3), of which
+// the ones inside [0, 64) -- each slot exactly once per query -- go to the
+// wave's 16 x 64 staging rows (swizzled as the output rows); the rows then
+// leave as 16-byte pieces.
+__device__ __forceinline__ void fwd_store_tau_staged(const BandParams& p, int b, int h, int g, int c, int lane,
+                                                     int w, int t0, const u16x4* tv, bf16* slot) {
+  unsigned short* sb = (unsigned short*)(slot + w * (16 * kTile));
+#pragma unroll
+  for (int s5 = 0; s5 < 5; ++s5)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = 16 * s5 + 4 * g + r - c;
+      if (col >= 0 && col < kTile) sb[c * kTile + 8 * ((col >> 3) ^ (c & 7)) + (col & 7)] = tv[s5][r];
+    }
+  bf16* tbase = (bf16*)p.tau.p + b * p.tau.s0 + h * p.tau.s2;
+  const int row0 = t0 + 16 * w;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int rr = (lane >> 3) + 8 * n, cc = lane & 7;
+    const u16x8 v = *(const u16x8*)(sb + rr * kTile + 8 * (cc ^ (rr & 7)));
+    __builtin_nontemporal_store(v, (u16x8*)(tbase + (int64_t)(row0 + rr) * p.tau.s1 + 8 * cc));
+  }
+}
+
 // ------------------------------------------------------------------ ring kernel (W <= 64)
 
 // One query tile at W = 64 with T % 64 == 0 (no bias, no tau): the band of
@@ -168,16 +193,28 @@ __device__ __forceinline__ void fwd_store_staged(const BandParams& p, int b, int
 // zero half where the pair sticks out of the band; the tau mass comes from
 // an all-ones A operand (the bf16 P the output is built from).  Sub-blocks
 // of block t-1 are absent on tile 0.  The wave index is a template argument
-// so that every band decision is static.
-template <int w>
+// so that every band decision is static.  TV: the tau of the lane's pairs,
+// sub-block s5 = 0..4 of the band, as bf16 bits in tv[s5] (zero where masked
+// or absent).
+template <int w, bool TV = false>
 __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb,
                                               bool has_prev, int g, int c, const bf16x8* qf, float k2,
-                                              const bool* mlo, const bool* mhi, f32x4* acc, f32x4& macc) {
+                                              const bool* mlo, const bool* mhi, f32x4* acc, f32x4& macc,
+                                              u16x4* tv = nullptr) {
   const bf16x8 ones = ones_bf16x8();
 #pragma unroll
   for (int pi = 0; pi < 3; ++pi) {
     const int pr = (w >> 1) + pi;  // 0..3
-    if (pr < 2 && !has_prev) continue;
+    if (pr < 2 && !has_prev) {
+      if constexpr (TV) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int s5 = 2 * pr + h2 - w;
+          if (s5 >= 0 && s5 <= 4) tv[s5] = u16x4{0, 0, 0, 0};
+        }
+      }
+      continue;
+    }
     const bf16* Kt = pr < 2 ? Ka : Kb;
     const bf16* Vt = pr < 2 ? Va : Vb;
     // V^T of the pair, read as counted asm (see dt_tr8_issue)
@@ -201,6 +238,10 @@ __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, co
       for (int r = 0; r < 4; ++r) {
         const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z[r] * k2));
         pv[h2][r] = s5 == 0 ? (mlo[r] ? x : 0.f) : (s5 == 4 ? (mhi[r] ? x : 0.f) : x);
+      }
+      if constexpr (TV) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tv[s5][r] = bf16_bits((bf16)pv[h2][r]);
       }
     }
     const bf16x8 pb = pack_b(pv[0], pv[1]);
@@ -269,16 +310,19 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
       tile_async_src(ksrc, (gb > 0 ? gb : 0) * kTile, Kd, wave);
       tile_async_src(vsrc, (gb > 0 ? gb : 0) * kTile, Vd, wave);
     };
+    // TAU: the tile's tau leaves through tv and fwd_store_tau_staged, every
+    // slot included (no separate zero fill)
+    u16x4 tv[5];
     auto fast_tile = [&](int t, const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb) -> OutRow {
       const int tq = t * kTile + wave * 16 + c;
       f32x4 acc[4] = {}, macc = {};
       switch (wave) {
-        case 0: fwd_tile_fast<0>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
-        case 1: fwd_tile_fast<1>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
-        case 2: fwd_tile_fast<2>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
-        default: fwd_tile_fast<3>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc); break;
+        case 0: fwd_tile_fast<0, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
+        case 1: fwd_tile_fast<1, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
+        case 2: fwd_tile_fast<2, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
+        default: fwd_tile_fast<3, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
       }
-      return fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, macc[0], true);
+      return fwd_finish<NORM, false>(p, b, h, tq, g, acc, macc[0], true);
     };
     if (pre) {
       load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
@@ -290,12 +334,14 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
       lds_barrier();
       const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1);
       wait_vm<0>();
-      lds_barrier();  // slot 0 (block t_first - 1) is free: it stages the rows
+      lds_barrier();  // slots K0 / V0 (block t_first - 1) are free: they stage the rows
       fwd_store_staged(p, b, h, g, c, lane, wave, o0, K0);
+      if constexpr (TAU) fwd_store_tau_staged(p, b, h, g, c, lane, wave, t_first * kTile, tv, V0);
       qf[0] = qn[0];
       qf[1] = qn[1];
       const OutRow o1 = fast_tile(t_first + 1, K1, V1, K2, V2);
       fwd_store_staged(p, b, h, g, c, lane, wave, o1, K0);
+      if constexpr (TAU) fwd_store_tau_staged(p, b, h, g, c, lane, wave, (t_first + 1) * kTile, tv, V0);
     } else {
       load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
       fetch_any(t_first - 1, K0, V0);
@@ -304,6 +350,7 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
       lds_barrier();
       const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1);
       fwd_store_staged(p, b, h, g, c, lane, wave, o0, K2);  // slot 2 holds no block
+      if constexpr (TAU) fwd_store_tau_staged(p, b, h, g, c, lane, wave, t_first * kTile, tv, V2);
     }
     return;
   }
@@ -442,11 +489,15 @@ static void go(const BandParams& p, hipStream_t st, unsigned nwg, bool ring) {
 #ifndef TENSION_NO_FAST_FWD
     // the staged output stores need a free ring slot: at most two tiles per
     // workgroup
-    if (!BIAS && !TAU && p.win == kTile && p.T % kTile == 0) {
+    // with tau: bf16 rows of 64 slots, 16-byte aligned (staged stores)
+    const Buf& tb = p.tau;
+    const bool tau_rows = !TAU || (tb.dt == TENSION_BF16 && ((tb.s0 | tb.s1 | tb.s2) & 7) == 0 &&
+                                   ((uintptr_t)tb.p & 15) == 0);
+    if (!BIAS && tau_rows && p.win == kTile && p.T % kTile == 0) {
       BandParams q = p;
       if (q.chunk > 2) q.chunk = 2;
       const unsigned nq = (unsigned)((int64_t)q.B * q.H * ((q.ntiles + q.chunk - 1) / q.chunk));
-      hipLaunchKernelGGL((mfma_fwd_ring<NORM, false, false, true>), dim3(nq), dim3(kThreads), 0, st, q);
+      hipLaunchKernelGGL((mfma_fwd_ring<NORM, false, TAU, true>), dim3(nq), dim3(kThreads), 0, st, q);
       return;
     }
 #endif

@@ -114,6 +114,19 @@ def test_config2_bf16_with_tau_and_dtau(dev):
     compare(hip, ref, torch.bfloat16, True)
 
 
+@pytest.mark.parametrize("normalize", [None, "count", "mass"])
+@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 320), (1, 12, 1024)])
+def test_fast_path_dtau_bf16(dev, normalize, B, H, T):
+    """The W = 64, T % 64 == 0 bf16 backward with a gradient through tau
+    (the model's aux-loss step): dTau rows staged per wave, every run length
+    and halo the launch produces for these (B, H)."""
+    D, W = 64, 64
+    inp = make_inputs(B, T, H, D, seed=T + H, std=0.5, dtype=torch.bfloat16, W=W, dtau_std=0.1)
+    hip = hip_run(inp, W, 8.0, dev, normalize=normalize, return_tau=True, use_dtau=True)
+    ref = oracle_run(inp, W, 8.0, normalize=normalize, use_dtau=True)
+    compare(hip, ref, torch.bfloat16, True)
+
+
 # ------------------------------------------------------------ reference kernel tests
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
