@@ -283,7 +283,7 @@ void mfma_bwd_fused(BandParams p) {
       const uint32_t r0 = (uint32_t)((t + 1) * kTile);
       kn = seq_tile_load(sk, r0 * sk.rs2, loff(sk, lk0));
       vn = seq_tile_load(sv, r0 * sv.rs2, loff(sv, lv0));
-      if constexpr (!FDT) {  // with dTau: issued at the start of phase 2
+      if constexpr (!FAST) {  // fast path: issued at the start of phase 2
         qn = seq_tile_load(sq, r0 * sq.rs2, loff(sq, lq0));
         on = seq_tile_load(so, r0 * so.rs2, loff(so, lo0));
       }
@@ -477,13 +477,13 @@ void mfma_bwd_fused(BandParams p) {
     if (more) {  // block t+1 replaces block t-1
       tile_store_direct(kn, Kt[(t + 1) & 1], tid);
       tile_store_direct(vn, Vt[(t + 1) & 1], tid);
-      if constexpr (FDT) {
-        // the next Q / dO tiles and dTau rows: loaded here rather than with
-        // K / V at the step's start, so that phase 1 has registers for dTau
+      if constexpr (FAST) {
+        // the next Q / dO tiles (and dTau rows): loaded here rather than with
+        // K / V at the step's start, which leaves phase 1 16 more registers
         const uint32_t r1 = (uint32_t)((t + 1) * kTile);
         qn = seq_tile_load(sq, r1 * sq.rs2, loff(sq, lq0));
         on = seq_tile_load(so, r1 * so.rs2, loff(so, lo0));
-        dnext = seq_tile_load(sdt, r1 * sdt.rs2, loff(sdt, 0));
+        if constexpr (FDT) dnext = seq_tile_load(sdt, r1 * sdt.rs2, loff(sdt, 0));
       }
     }
 
