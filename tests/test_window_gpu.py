@@ -352,3 +352,46 @@ def test_fused_backward_runs_bf16(dev, B, H, T, W, normalize):
     hip = hip_run(inp, W, 8.0, dev, normalize=normalize, use_bias=use_bias)
     ref = oracle_run(inp, W, 8.0, normalize=normalize, use_bias=use_bias)
     compare(hip, ref, torch.bfloat16, False)
+
+
+@pytest.mark.parametrize("pad", [8, 4])
+def test_tau_dtau_row_layouts_abi(dev, pad):
+    """Through the C ABI, tau / dTau rows padded to 64 + pad slots: pad 8
+    keeps 16-byte rows (the staged fast paths), pad 4 does not (the general
+    kernels).  Either way the results equal the contiguous run's."""
+    import ctypes
+    from bozo_amd import _lib as L
+    from bozo_amd import causal_tension
+    B, T, H, D, W, scale = 2, 256, 3, 64, 64, 8.0
+    g = torch.Generator(device=dev).manual_seed(pad)
+    q, k, v, do = ((torch.randn(B, T, H, D, device=dev, generator=g) * 0.5).to(torch.bfloat16) for _ in range(4))
+    dt = (torch.randn(B, T, H, W, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    qq, kk, vv = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out_ref, tau_ref = causal_tension(qq, kk, vv, W, scale, return_tau=True, normalize="mass")
+    torch.autograd.backward([out_ref, tau_ref], [do, dt])
+
+    lib = L.lib()
+    st = L.stream_handle(dev)
+    out = torch.empty_like(q)
+    taup = torch.full((B, T, H, W + pad), float("nan"), device=dev, dtype=torch.bfloat16)
+    tau = taup[..., :W]
+    L.check(lib.tension_window_fwd(L.buf(q), L.buf(k), L.buf(v), L.buf(out), L.buf(tau), None, None,
+                                   B, T, H, D, W, ctypes.c_double(scale), L.NORM_MASS, st), "fwd")
+    dtp = torch.zeros((B, T, H, W + pad), device=dev, dtype=torch.bfloat16)
+    dtp[..., :W] = dt
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    nws = lib.tension_window_bwd_workspace(B, T, H, L.F32, L.NORM_MASS)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+    L.check(lib.tension_window_bwd(L.buf(q), L.buf(k), L.buf(v), L.buf(do), L.buf(dtp[..., :W]), None,
+                                   L.buf(dq), L.buf(dk), L.buf(dv), ctypes.c_void_p(ws.data_ptr() if nws else None),
+                                   B, T, H, D, W, ctypes.c_double(scale), L.NORM_MASS, st), "bwd")
+    torch.cuda.synchronize()
+    if pad % 8 == 0:  # the same kernels as the contiguous run: the same bits
+        assert torch.equal(out, out_ref.detach())
+        assert torch.equal(tau, tau_ref.detach())
+    else:  # other kernels: bf16 rounding of the same fp32 values
+        assert (out.float() - out_ref.float()).abs().max().item() <= 2e-2 * out_ref.float().abs().max().item()
+        assert (tau.float() - tau_ref.float()).abs().max().item() <= 4e-3
+    assert torch.isnan(taup[..., W:]).all()  # the padding is not written
+    for a, b in ((dq, qq.grad), (dk, kk.grad), (dv, vv.grad)):
+        assert (a.float() - b.float()).abs().max().item() <= 2e-2 * b.float().abs().max().item()
