@@ -472,7 +472,7 @@ def _phase_regions(cur):
             msg = json.loads(ext or "{}").get("message", "")
         except ValueError:
             msg = ""
-        if msg.startswith(("step", "kernel:", "global", "decode")):
+        if msg.startswith(("step", "kernel:", "global", "decode", "model:")):
             out.append((msg, a, b))
     return out
 
@@ -649,11 +649,13 @@ def bench_model(dev, steps, warmup, aux):
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    torch.cuda.nvtx.range_push("model:" + ("aux" if aux else "ce"))  # a --summarize phase
     e0.record()
     for _ in range(steps):
         loss = step()
     e1.record()
     torch.cuda.synchronize()
+    torch.cuda.nvtx.range_pop()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     ms = e0.elapsed_time(e1) / steps
     res = {"config": "TensionLM-117M training step B8 T1024 bf16 autocast AdamW (config 5), "

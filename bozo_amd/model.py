@@ -383,6 +383,21 @@ def _cons_n(W: int, T: int) -> int:
     return n if T - (n + 1) > 0 else 0
 
 
+_GROUP_MATS: dict = {}
+
+
+def _group_mats(groups, L: int, nrow: int, dev):
+    key = (groups, L, nrow, str(dev))
+    if key not in _GROUP_MATS:
+        memb = torch.zeros(len(groups), L, dtype=torch.float64)
+        for gi, (_, idx) in enumerate(groups):
+            for i in idx:
+                memb[gi, i] = 1.0 / (len(idx) * nrow)
+        logw = torch.tensor([lw for lw, _ in groups], dtype=torch.float64)
+        _GROUP_MATS[key] = (memb.to(dev), logw.to(dev))
+    return _GROUP_MATS[key]
+
+
 class _AuxLossFn(torch.autograd.Function):
     """Diversity, consistency and entropy losses of every layer's tau in one
     HIP pass forward and one backward (tension_aux_loss_fwd / _bwd)."""
@@ -403,14 +418,13 @@ class _AuxLossFn(torch.autograd.Function):
                                               torch.cuda.current_stream(dev).cuda_stream), "tension_aux_loss_fwd")
         acc = part.sum(1)                                     # [L, 4]
         nrow = B * T * H
-        div = torch.zeros((), dtype=torch.float64, device=dev)
-        active = torch.zeros(L, dtype=torch.float64, device=dev)
-        for logw, idx in groups:
-            mean_ent = acc[list(idx), 0].sum() / (len(idx) * nrow)
-            gap = logw - mean_ent
-            div = div + F.relu(gap)
-            active[list(idx)] = (gap > 0).double() / (len(idx) * nrow)
-        div = div / max(len(groups), 1)
+        # window groups as a [G, L] membership matrix scaled by 1 / (|group|
+        # nrow), built once per (groups, L, device): indexing by Python lists
+        # here would copy the index to the device and stall the host
+        memb, logw = _group_mats(groups, L, nrow, dev)
+        gap = logw - memb @ acc[:, 0]                         # [G]
+        div = F.relu(gap).sum() / max(len(groups), 1)
+        active = memb.t() @ (gap > 0).double()                # [L]: 1 / (|group| nrow) where active
         n = _cons_n(W, T)
         cons = torch.zeros((), dtype=torch.float64, device=dev)
         if n:
