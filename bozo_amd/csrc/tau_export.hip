@@ -33,6 +33,32 @@ __device__ __forceinline__ double block_sum(double x, double* red) {
   return s;
 }
 
+constexpr int kStatVals = 128;  // values per thread of the register-resident select (T W <= 65536)
+
+// The next order statistic after xk (xk again when more than k + 1 values
+// are <= xk, else the smallest value above it: le / gt are this thread's
+// counts), the interpolated quantile and the head's four statistics.
+__device__ void head_quantile_out(const TauStatParams& p, int l, int h, int64_t n, double g, int64_t k, float xk,
+                                  double le, float gt, double sum, double rmax, double rarg, int T, double* red) {
+  const int tid = threadIdx.x;
+  le = block_sum(le, red);
+  for (int o = 32; o > 0; o >>= 1) gt = fminf(gt, __shfl_down(gt, o, 64));
+  __shared__ float gred[kStatThreads / 64];
+  if ((tid & 63) == 0) gred[tid >> 6] = gt;
+  __syncthreads();
+  if (tid == 0) {
+    float gm = gred[0];
+    for (int i = 1; i < kStatThreads / 64; ++i) gm = fminf(gm, gred[i]);
+    const float xk1 = (k + 1 >= n || le >= (double)(k + 2)) ? xk : gm;
+    const double frac = g - (double)k;
+    float* o = p.stats + ((int64_t)l * p.H + h) * 4;
+    o[0] = (float)(sum / (double)n);
+    o[1] = (float)((double)xk + frac * ((double)xk1 - (double)xk));
+    o[2] = (float)(rarg / (double)T);
+    o[3] = (float)(rmax / (double)T);
+  }
+}
+
 }  // namespace
 
 // One workgroup per (layer, head): mean of tau over (t, w), mean over t of
@@ -42,7 +68,8 @@ __device__ __forceinline__ double block_sum(double x, double* red) {
 // select over the float bit patterns (tau >= 0, so they order as unsigned
 // integers): four 8-bit passes with an LDS histogram, then one pass for the
 // next value up.
-__global__ __launch_bounds__(kStatThreads) void tau_head_stats_kernel(TauStatParams p) {
+__global__ __launch_bounds__(kStatThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tau_head_stats_kernel(TauStatParams p) {
   const int l = blockIdx.x / p.H, h = blockIdx.x % p.H;
   const Buf tb = p.tau[l];
   const int T = p.T, W = p.W, B = p.B;
@@ -53,6 +80,129 @@ __global__ __launch_bounds__(kStatThreads) void tau_head_stats_kernel(TauStatPar
   __shared__ unsigned sel[2];  // prefix bits, rank left within the prefix
 
   double sum = 0.0, rmax = 0.0, rarg = 0.0;
+  const int64_t n = (int64_t)T * W;
+  const double g = 0.99 * (double)(n - 1);
+  const int64_t k = (int64_t)g;
+  if (tid == 0) {
+    sel[0] = 0u;
+    sel[1] = (unsigned)k;
+  }
+  if (B == 1 && W <= 64 && kStatThreads % W == 0 && n <= (int64_t)kStatThreads * kStatVals &&
+      (tb.dt == TENSION_BF16 || tb.dt == TENSION_F32)) {
+    // the head's values stay in registers for every radix pass: thread tid
+    // holds slot w0 = tid % W of rows t0 + (512 / W) j, i.e. flat values
+    // tid + 512 j; per-wave histograms keep the LDS atomics of clustered
+    // values (a few top bytes) from serialising on one address
+    const int nn = (int)n;
+    const int w0 = tid % W, t0 = tid / W, rstep = kStatThreads / W;
+    float v[kStatVals];
+    auto load_all = [&](auto tag) {
+      using E = decltype(tag);
+      const E* base = (const E*)tb.p + (int64_t)h * tb.s2 + w0;
+#pragma unroll
+      for (int j = 0; j < kStatVals; ++j) {
+        const int t = t0 + rstep * j;
+        const bool in = t < T && !(vo && t + w0 < W);
+        v[j] = in ? (float)base[(int64_t)t * tb.s1] : 0.f;
+      }
+    };
+    if (tb.dt == TENSION_BF16)
+      load_all(bf16{});
+    else
+      load_all(float{});
+    // row sum, maximum and first arg-max: a row is W adjacent lanes (one
+    // per slot), reduced by xor shuffles inside the W-lane segment
+#pragma unroll
+    for (int j = 0; j < kStatVals; ++j) {
+      float rs = v[j], m = v[j];
+      int am = w0;
+      for (int o = 1; o < W; o <<= 1) {
+        rs += __shfl_xor(rs, o, 64);
+        const float m2 = __shfl_xor(m, o, 64);
+        const int a2 = __shfl_xor(am, o, 64);
+        if (m2 > m || (m2 == m && a2 < am)) {
+          m = m2;
+          am = a2;
+        }
+      }
+      if (w0 == 0 && t0 + rstep * j < T) {
+        sum += rs;
+        rmax += m;
+        rarg += am;
+      }
+    }
+    sum = block_sum(sum, red);
+    rmax = block_sum(rmax, red);
+    rarg = block_sum(rarg, red);
+    __shared__ unsigned whist[kStatThreads / 64][256 + 1];  // +1: the waves' copies of a bin in different banks
+    __shared__ unsigned tot[256];
+    unsigned* const my = whist[tid >> 6];
+    // batch-mean-free bf16 input has zero low 16 bits: two passes decide it
+    const bool exact16 = B == 1 && tb.dt == TENSION_BF16;
+    unsigned msk = 0u;
+    for (int shift = 24; shift >= (exact16 ? 16 : 0); shift -= 8) {
+      for (int i = tid; i < (kStatThreads / 64) * 257; i += kStatThreads) (&whist[0][0])[i] = 0u;
+      __syncthreads();
+      const unsigned prefix = sel[0];
+      {
+#pragma unroll
+        for (int j = 0; j < kStatVals; ++j) {
+          const unsigned bits = __float_as_uint(v[j]);
+          if (tid + kStatThreads * j < nn && (bits & msk) == prefix) atomicAdd(&my[(bits >> shift) & 255u], 1u);
+        }
+      }
+      __syncthreads();
+      if (tid < 256) {
+        unsigned c = 0u;
+#pragma unroll
+        for (int wv = 0; wv < kStatThreads / 64; ++wv) c += whist[wv][tid];
+        tot[tid] = c;
+      }
+      __syncthreads();
+      if (tid < 64) {
+        // wave 0 finds the bin holding rank r: lane L owns bins 4L..4L+3;
+        // an inclusive scan of the lanes' counts brackets r in one lane
+        const unsigned r = sel[1];
+        unsigned c4[4], own = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          c4[q] = tot[4 * tid + q];
+          own += c4[q];
+        }
+        unsigned inc = own;
+        for (int o = 1; o < 64; o <<= 1) {
+          const unsigned up = __shfl_up(inc, o, 64);
+          if (tid >= o) inc += up;
+        }
+        unsigned c = inc - own;
+        if (c <= r && r < inc) {
+          int bin = 4 * tid;
+#pragma unroll
+          for (int q = 0; q < 3; ++q) {
+            if (c + c4[q] > r) break;
+            c += c4[q];
+            ++bin;
+          }
+          sel[0] = prefix | ((unsigned)bin << shift);
+          sel[1] = r - c;
+        }
+      }
+      __syncthreads();
+      msk |= 255u << shift;
+    }
+    const float xk = __uint_as_float(sel[0]);
+    double le = 0.0;
+    float gt = 3.0e38f;
+#pragma unroll
+    for (int j = 0; j < kStatVals; ++j) {
+      if (tid + kStatThreads * j < nn) {
+        if (v[j] <= xk) le += 1.0;
+        else gt = fminf(gt, v[j]);
+      }
+    }
+    head_quantile_out(p, l, h, n, g, k, xk, le, gt, sum, rmax, rarg, T, red);
+    return;
+  }
   for (int t = tid; t < T; t += kStatThreads) {
     float m = -1.f, s = 0.f;
     int am = 0;
@@ -72,13 +222,6 @@ __global__ __launch_bounds__(kStatThreads) void tau_head_stats_kernel(TauStatPar
   rmax = block_sum(rmax, red);
   rarg = block_sum(rarg, red);
 
-  const int64_t n = (int64_t)T * W;
-  const double g = 0.99 * (double)(n - 1);
-  const int64_t k = (int64_t)g;
-  if (tid == 0) {
-    sel[0] = 0u;
-    sel[1] = (unsigned)k;
-  }
   unsigned mask = 0u;
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = tid; i < 256; i += kStatThreads) hist[i] = 0u;
@@ -114,22 +257,7 @@ __global__ __launch_bounds__(kStatThreads) void tau_head_stats_kernel(TauStatPar
     if (v <= xk) le += 1.0;
     else gt = fminf(gt, v);
   }
-  le = block_sum(le, red);
-  for (int o = 32; o > 0; o >>= 1) gt = fminf(gt, __shfl_down(gt, o, 64));
-  __shared__ float gred[kStatThreads / 64];
-  if ((tid & 63) == 0) gred[tid >> 6] = gt;
-  __syncthreads();
-  if (tid == 0) {
-    float gm = gred[0];
-    for (int i = 1; i < kStatThreads / 64; ++i) gm = fminf(gm, gred[i]);
-    const float xk1 = (k + 1 >= n || le >= (double)(k + 2)) ? xk : gm;
-    const double frac = g - (double)k;
-    float* o = p.stats + ((int64_t)l * p.H + h) * 4;
-    o[0] = (float)(sum / (double)n);
-    o[1] = (float)((double)xk + frac * ((double)xk1 - (double)xk));
-    o[2] = (float)(rarg / (double)T);
-    o[3] = (float)(rmax / (double)T);
-  }
+  head_quantile_out(p, l, h, n, g, k, xk, le, gt, sum, rmax, rarg, T, red);
 }
 
 // aggregated[t, w] = mean over the selected (layer, head) pairs of the batch
