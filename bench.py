@@ -201,10 +201,50 @@ def kernel_bytes(B, T, H, D, W, el=2):
     }
 
 
+def host_cpus():
+    """The host's CPUs as this process sees them: os.cpu_count(), the CPUs
+    it may run on (affinity), the cgroup CPU quota, the CPU model, and the
+    thread count the CPU baselines use -- every CPU the process can use
+    (os.cpu_count() when nothing restricts it, as the reference's timing
+    recipe sets torch.set_num_threads(os.cpu_count())), no more than the
+    quota and the OMP_NUM_THREADS share the GPU box assigns to one GPU."""
+    total = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = total
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+            if q != "max":
+                quota = float(q) / float(per)
+    except (OSError, ValueError):
+        pass
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = affinity
+    if quota is not None:
+        threads = min(threads, max(1, int(quota)))
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        threads = min(threads, int(share))
+    return {"cpu_count": total, "affinity": affinity, "cgroup_quota": quota, "model": model,
+            "threads": max(1, threads)}
+
+
 def cpu_baseline(B, T, H, D, W, seconds=10.0):
     """Reference CPU path (unfold + tau-mass + autograd, fp32) on the host."""
     from oracle import torch_ref as R
-    cores = min(16, os.cpu_count() or 1)
+    hc = host_cpus()
+    cores = hc["threads"]
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(1)
     b = 1  # bounded sample: one sequence of the batch
@@ -225,18 +265,11 @@ def cpu_baseline(B, T, H, D, W, seconds=10.0):
         el = time.perf_counter() - t0
         if el >= seconds or n >= 200:
             break
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {"value": round(b * T * n / el, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "host": {k: hc[k] for k in ("model", "cpu_count", "affinity", "cgroup_quota")},
             "sample": f"{n} fwd+bwd passes of 1 sequence (T={T}, H={H}, d={D}, W={W}) fp32, "
-                      f"unfold+tau-mass+autograd (oracle/torch_ref.py), {el:.1f} s on {cpu}"}
+                      f"unfold+tau-mass+autograd (oracle/torch_ref.py), {el:.1f} s on {cores} threads "
+                      f"of {hc['model']} (os.cpu_count()={hc['cpu_count']})"}
 
 
 class _ReferenceCpuOps:
@@ -276,7 +309,7 @@ def cpu_model_baselines(seconds=10.0):
     context for one new token)."""
     import torch.nn.functional as F
     from bozo_amd import model as M
-    cores = min(16, os.cpu_count() or 1)
+    cores = host_cpus()["threads"]
     torch.set_num_threads(cores)
     cfg = M.config_117m(use_triton=False, dropout=0.0)
     torch.manual_seed(4)

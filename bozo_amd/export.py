@@ -398,9 +398,17 @@ class StreamingTauExporter(TauExporter):
     def ingest_step(self, ctx_ids, all_tensions: list, tokenizer, query_abs_pos: int) -> int:
         """Edges from the last query of ``ctx_ids`` to its W keys.  Each
         entry of ``all_tensions`` is a layer's [B,T,H,W] tau (its last row is
-        used) or the [B,H,W] row of a cached decode step; None entries
-        (global layers of a decode step) are skipped."""
-        rows = [t if t.dim() == 3 else t[:, -1] for t in all_tensions if t is not None]
+        used) or the [B,H,W] row of a cached decode step, one entry per layer
+        as ``model(ctx, return_all=True)`` lists them: the locked (layer,
+        head) pairs index that list (after the most-common-shape rule), so a
+        missing layer would shift them.  Decode rows come from
+        ``TensionKVCache(model, N, return_all=True).step(ids,
+        return_tau=True)``, which includes the global layers' rows."""
+        if any(t is None for t in all_tensions):
+            raise ValueError(
+                "ingest_step needs a tau row for every layer (None given): use the rows of "
+                "TensionKVCache(model, N, return_all=True).step(..., return_tau=True)")
+        rows = [t if t.dim() == 3 else t[:, -1] for t in all_tensions]
         if not rows or not ctx_ids:
             return 0
         local = self._local_subset(rows)

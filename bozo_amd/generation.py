@@ -44,9 +44,16 @@ class TensionKVCache:
     ``step(next_ids)`` advances one token per sequence and returns its
     logits [N, vocab].  The model must be in eval mode (dropout off)."""
 
-    def __init__(self, model, N: int):
+    def __init__(self, model, N: int, return_all: bool = False):
+        """``return_all``: every step computes what ``model(ctx,
+        return_all=True)`` gives for the new token -- the forward the
+        reference's streaming exporter runs per step (ts_bridge/streaming.py
+        :26-33): local layers tau-mass normalised (model.py:250-258) and,
+        with ``return_tau``, the global layers' down-sampled ``tau_local``
+        row (model.py:231-237) beside the local layers' tau rows."""
         self.model = model
         self.N = N
+        self.return_all = bool(return_all)
         self.t = 0  # tokens cached per sequence
         cfg = model.cfg
         self.windows = [cfg.max_seq_len if b.global_layer else cfg.window for b in model.blocks]
@@ -68,9 +75,10 @@ class TensionKVCache:
         c.pos[c.cur].fill_(T)
 
     @torch.no_grad()
-    def prefill(self, ids: Tensor) -> Tensor:
+    def prefill(self, ids: Tensor):
         """Forward over the prompt ids [N, T] (T <= max_seq_len) filling the
-        caches; returns the logits [N, T, vocab]."""
+        caches; returns the logits [N, T, vocab], or with ``return_all``
+        (logits, taus) of ``model(ids, return_all=True)``."""
         model = self.model
         N, T = ids.shape
         if N != self.N:
@@ -83,12 +91,12 @@ class TensionKVCache:
         for i, layer in enumerate(layers):
             layer.kv_sink = (lambda k, v, i=i: self._fill(i, k, v))
         try:
-            logits = model(ids)
+            res = model(ids, return_all=True) if self.return_all else model(ids)
         finally:
             for layer in layers:
                 layer.kv_sink = None
         self.t = T
-        return logits
+        return (res[0], res[2]) if self.return_all else res
 
     def _check_step(self):
         cfg = self.model.cfg
@@ -108,11 +116,13 @@ class TensionKVCache:
     def step(self, next_ids: Tensor, return_tau: bool = False):
         """Advance every sequence by one token (ids [N]) at position ``t``;
         returns logits [N, vocab] and, with ``return_tau``, the new token's
-        tau row [N, H, W] of every local layer (None for global layers) --
-        the last row of the full forward's tau."""
+        tau row [N, H, W] of every local layer -- the last row of the full
+        forward's tau -- and, in ``return_all`` mode, the global layers'
+        ``tau_local`` row [N, H, min(W, t + 1)] (slot j = key t - j, the
+        last row of model.py:231-237); None for global layers otherwise."""
         self._check_step()
         taus = [] if return_tau else None
-        logits = self._step_device(next_ids, [c.cur for c in self.layers], taus)
+        logits = self._step_device(next_ids, [c.cur for c in self.layers], taus, self.t)
         self._advance()
         return (logits, taus) if return_tau else logits
 
@@ -141,7 +151,7 @@ class TensionKVCache:
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):  # warm-up launches (library set-up) outside the capture
             for par in (0, 1):
-                self._step_device(self._ids, [par] * len(self.layers), None)
+                self._step_device(self._ids, [par] * len(self.layers), None, None)
         torch.cuda.current_stream(dev).wait_stream(side)
         torch.cuda.synchronize(dev)
         for c, (k, v, p0, p1) in zip(self.layers, saved):
@@ -154,16 +164,17 @@ class TensionKVCache:
         for par in (0, 1):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=pool):
-                logits.append(self._step_device(self._ids, [par] * len(self.layers), None))
+                logits.append(self._step_device(self._ids, [par] * len(self.layers), None, None))
             pool = g.pool()
             graphs.append(g)
         torch.cuda.synchronize(dev)
         self._graphs, self._logits = graphs, logits
 
-    def _step_device(self, next_ids: Tensor, parities, taus):
+    def _step_device(self, next_ids: Tensor, parities, taus, t):
         """One token through the model with its position read from the layer
         caches' device counters (no host value of t), so the same launches
-        can be captured once and replayed at every position."""
+        can be captured once and replayed at every position.  ``t`` (host
+        position) is only needed for the global layers' tau rows."""
         model = self.model
         N = next_ids.shape[0]
         c0 = self.layers[0]
@@ -179,7 +190,7 @@ class TensionKVCache:
         fpos = None
         for blk, c, par in zip(model.blocks, self.layers, parities):
             h = blk.pre_norm(x)
-            h = _layer_step(blk.tension, h, c, par, rot, taus)
+            h = _layer_step(blk.tension, h, c, par, rot, taus, self.return_all, t)
             if blk.oscillate is not None:
                 osc = blk.oscillate
                 if fpos is None:
@@ -192,10 +203,13 @@ class TensionKVCache:
         return model.lm_head(model.final_norm(x))[:, 0]
 
 
-def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, par: int, rot, taus):
+def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, par: int, rot, taus,
+                return_all: bool = False, t: Optional[int] = None):
     """One token through a tension layer: x [N, 1, D]; ``rot`` the RoPE
     (cos, sin) rows [1, HD/2] of its position; cache counters pos[par] ->
-    pos[1 - par]."""
+    pos[1 - par].  ``return_all``: the normalisation of the return_all
+    forward (tau mass in every local layer) and, when taus are collected,
+    the global layer's tau_local row for position ``t``."""
     N, _, D = x.shape
     H, HD = layer.num_heads, layer.head_dim
     q = layer.wq(x).view(N, 1, H, HD)
@@ -210,15 +224,27 @@ def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, par: int, rot, taus
     if layer.global_layer:
         out = decode_step(q, k, v, cache.k, cache.v, pin, pout, cache.scale, "mass", None, True)
         if taus is not None:
-            taus.append(None)
+            taus.append(_global_tau_row(layer, q, cache, t) if return_all else None)
     else:
         tau = None
         if taus is not None:
             tau = torch.empty(N, H, cache.W, dtype=q.dtype, device=q.device)
             taus.append(tau)
-        out = decode_step(q, k, v, cache.k, cache.v, pin, pout, cache.scale,
-                          "count" if layer.count_norm else "mass", tau)
+        norm = "count" if layer.count_norm and not return_all else "mass"
+        out = decode_step(q, k, v, cache.k, cache.v, pin, pout, cache.scale, norm, tau)
     return layer.norm(x + layer.wo(out.reshape(N, 1, D)).to(x.dtype))
+
+
+def _global_tau_row(layer, q: Tensor, cache: TensionDecodeCache, t: int) -> Tensor:
+    """Last row of a global layer's ``tau_local`` at position t (the cache
+    already holds keys 0..t, slot = position): slot j = sigmoid(q . k_{t-j}
+    / scale) for j < min(W_local, t + 1), the flipped, cut-down score row of
+    model.py:231-237.  A side output of the streaming export (float32
+    scores, rounded to q's dtype), computed from the cached keys."""
+    Wl = min(layer.local_window, t + 1)
+    keys = cache.k[:, :, t + 1 - Wl:t + 1].flip(2).float()            # [N, H, Wl, D]
+    s = torch.matmul(keys, q.float()[..., None])[..., 0] / cache.scale  # [N, H, Wl]
+    return torch.sigmoid(s).to(q.dtype)
 
 
 def sample_next(logits: Tensor, history: list, temp: float = 0.8, top_p: float = 0.92,

@@ -50,3 +50,22 @@ def rel_l2(a, b):
 
 def scale_of(D):
     return math.sqrt(D)
+
+
+def fused_geometry(B, H, T, tile=64, wg_target=512):
+    """Launch geometry of the bf16 W <= 64 band kernels, restated from their
+    host dispatch (bozo_amd/csrc/mfma.hip ``launch_mfma``; the fast forward
+    with tau caps its tiles per workgroup at 2, mfma_fwd.hip ``go``).
+
+    Returns (fwd_tiles_per_workgroup, bwd_runs_per_sequence,
+    longest_bwd_run_in_tiles).  A backward run of r tiles takes r own steps
+    plus one recomputed halo step; runs longer than one tile hand dTau rows
+    and the previous key block's partial dK/dV from step to step."""
+    ntiles = -(-T // tile)
+    bh = B * H
+    chunk = 1
+    while chunk < 4 and bh * (-(-ntiles // (2 * chunk))) >= 768:
+        chunk *= 2
+    runs = min(max(1, (wg_target + bh // 2) // bh), ntiles)
+    longest = max((r + 1) * ntiles // runs - r * ntiles // runs for r in range(runs))
+    return chunk, runs, longest

@@ -38,11 +38,17 @@ def reference(taus, groups):
     (2, 1, 12, 2, 2, torch.float32, False),    # no consistency terms (W < 3)
     (2, 1, 5, 2, 8, torch.float32, False),     # T too short for the terms
     (12, 2, 64, 4, 64, torch.bfloat16, True),  # the model's shape class
+    # more than one workgroup per layer (1024 rows each): blocks that start
+    # mid-sequence and mid-row-group, neighbours across block edges, and the
+    # host sum of the partials; T = 1000 is not a multiple of the block
+    (12, 2, 1024, 12, 64, torch.bfloat16, True),
+    (3, 2, 1000, 12, 64, torch.float32, True),
 ])
 def test_fused_aux_losses_match_reference(dev, L, B, T, H, W, dtype, grouped):
     taus = taus_of(L * 100 + W, L, B, T, H, W, dtype, dev)
     groups = {W: list(range(0, L, 2)), 1024: list(range(1, L, 2))} if grouped else None
-    print(f"[aux] L={L} B={B} T={T} H={H} W={W} {dtype} grouped={grouped}", flush=True)
+    print(f"[aux] L={L} B={B} T={T} H={H} W={W} {dtype} grouped={grouped} "
+          f"workgroups/layer={-(-B * T * H // 1024)}", flush=True)
     a = [t.detach().float().requires_grad_(True) for t in taus]    # reference in fp32
     b = [t.detach().clone().requires_grad_(True) for t in taus]    # fused, tau's own dtype
     ra = reference(a, groups)

@@ -76,9 +76,22 @@ def test_bias_feeds_the_model_and_table_refresh(dev):
         a = m(x)
         b = m(x, tau_bias=lb, tau_bias_global=gbias)
     assert torch.isfinite(b).all() and not torch.allclose(a, b)
-    # a new edge after the first build is seen once the map's size changes
+    # a new edge after the first build is seen (the map's size changes)
     contents = [tok.id_to_token(i) or f"<{i}>" for i in ids]
     gb.edge_map[(contents[0], contents[1])] = 5.0
     lb2, st2 = gb.local_bias(ids, tok, window=8, device=dev)
-    if 1 - (8 - 7) >= 0:
-        assert lb2[0, 1, 7].item() == pytest.approx(2.5)
+    assert lb2[0, 1, 7].item() == pytest.approx(2.5)
+    # in-place changes that keep the size: a new weight, and one key swapped
+    # for another; each build equals the reference's lookup loop
+    gb.edge_map[(contents[0], contents[1])] = 3.0
+    lb3, _ = gb.local_bias(ids, tok, window=8, device=dev)
+    assert lb3[0, 1, 7].item() == pytest.approx(1.5)
+    del gb.edge_map[(contents[0], contents[1])]
+    gb.edge_map[(contents[2], contents[3])] = 4.0
+    lb4, _ = gb.local_bias(ids, tok, window=8, device=dev)
+    got = lb4[0].cpu().numpy()
+    for t in range(len(ids)):
+        for w in range(8):
+            s = t - (8 - w)
+            wt = 0.0 if s < 0 else gb.lookup(contents[s], contents[t])
+            assert got[t, w] == np.float32(0.5 * wt if wt > 0 else 0.0), (t, w)

@@ -134,26 +134,41 @@ def test_ingest_matches_reference_pipeline(dev):
     assert np.allclose([e["weight"] for e in a["edges"]], [e["weight"] for e in b["edges"]], atol=1e-6)
 
 
-def test_streaming_step_rows_from_decode(dev):
-    """ingest_step on the decode step's tau rows equals ingest_step on the
-    full forward's last rows."""
+@pytest.mark.parametrize("use_triton", [False, True])
+def test_streaming_step_rows_from_decode(dev, use_triton):
+    """ingest_step on the cached decode step's rows (return_all mode) equals
+    ingest_step on the full return_all forward's last rows (the reference's
+    streaming loop, ts_bridge/streaming.py:26-33).  Six layers with global
+    layers 2 and 5 in the middle and at the end; locked heads on either side
+    of them and on a global layer, so a shifted layer index would show.
+    With use_triton the plain forward normalises by the valid count, the
+    return_all forward by tau mass: the cache must follow the latter."""
     from bozo_amd import model as M
     from bozo_amd.generation import TensionKVCache
-    cfg = M.TensionConfig(vocab_size=60, dim=64, num_layers=4, num_heads=4, window=8, max_seq_len=64,
-                          dropout=0.0, global_every=4, use_rope=True, use_triton=False)
+    cfg = M.TensionConfig(vocab_size=60, dim=64, num_layers=6, num_heads=4, window=8, max_seq_len=64,
+                          dropout=0.0, global_every=3, use_rope=True, use_triton=use_triton)
     torch.manual_seed(1)
     m = M.TensionLM(cfg).to(dev).eval()
     ids = torch.randint(0, 60, (1, 30), generator=torch.Generator().manual_seed(2)).to(dev)
-    cache = TensionKVCache(m, 1)
+    cache = TensionKVCache(m, 1, return_all=True)
     tok = Tok()
+    heads = [(0, 1), (2, 3), (3, 2), (4, 0), (5, 1)]
     with torch.no_grad():
-        cache.prefill(ids[:, :20])
+        logits, ptaus = cache.prefill(ids[:, :20])
+        flg, _, ftaus = m(ids[:, :20], return_all=True)
+        assert torch.equal(logits, flg)
+        assert len(ptaus) == 6 and all(torch.equal(a, b) for a, b in zip(ptaus, ftaus))
         for t in range(20, 30):
-            _, rows = cache.step(ids[:, t], return_tau=True)
-            _, _, full = m(ids[:, :t + 1], return_all=True)
+            lg, rows = cache.step(ids[:, t], return_tau=True)
+            flg, _, full = m(ids[:, :t + 1], return_all=True)
+            assert len(rows) == 6 and all(r is not None for r in rows)
+            assert (lg - flg[:, -1]).abs().max().item() <= 1e-4 * flg.abs().max().item()
+            for i, (r, f) in enumerate(zip(rows, full)):
+                assert r.shape == f[:, -1].shape, i
+                assert (r - f[:, -1]).abs().max().item() < 1e-5, (t, i)
             ga, gb = E.UniversalLivingGraph(), E.UniversalLivingGraph()
-            sa = E.StreamingTauExporter(ga, edge_threshold=0.0, head_override=[(0, 1), (2, 3)])
-            sb = E.StreamingTauExporter(gb, edge_threshold=0.0, head_override=[(0, 1), (2, 3)])
+            sa = E.StreamingTauExporter(ga, edge_threshold=0.0, head_override=heads)
+            sb = E.StreamingTauExporter(gb, edge_threshold=0.0, head_override=heads)
             na = sa.ingest_step(ids[0, :t + 1].tolist(), rows, tok, query_abs_pos=t)
             nb = sb.ingest_step(ids[0, :t + 1].tolist(), full, tok, query_abs_pos=t)
             assert na == nb == 8
@@ -161,3 +176,12 @@ def test_streaming_step_rows_from_decode(dev):
             wb = [e.weight for e in gb.edges]
             assert np.allclose(wa, wb, atol=1e-5)
             assert [e.src for e in ga.edges] == [e.src for e in gb.edges]
+    # rows of a plain cache carry None for the global layers: refused
+    plain = TensionKVCache(m, 1)
+    with torch.no_grad():
+        plain.prefill(ids[:, :20])
+        _, rows = plain.step(ids[:, 20], return_tau=True)
+    assert rows[2] is None
+    with pytest.raises(ValueError):
+        E.StreamingTauExporter(E.UniversalLivingGraph(), edge_threshold=0.0).ingest_step(
+            ids[0, :21].tolist(), rows, tok, query_abs_pos=20)

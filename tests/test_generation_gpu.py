@@ -2,7 +2,10 @@
 
 The reference generates by re-running the forward over the context for every
 token (model.py:617-652,719-768); the cached step must give the same logits
-as that forward's last row, layer caches filled by a prefill.  Checked per
+as that forward's last row, layer caches filled by a prefill.  The float32
+steps are checked against the float64 functional restatement of the
+reference forward (oracle/model_ref.py) and against the HIP model's own
+full forward.  Checked per
 step on float32 models (exact decode kernel, 1e-5 relative) and bf16
 autocast at head_dim 64 (the fast decode kernel, including a global layer
 window of max_seq_len slots, 2e-2 relative), plus the sampled token
@@ -16,6 +19,7 @@ import torch
 
 from bozo_amd import model as M
 from bozo_amd.generation import TensionKVCache, generate_cached, sample_next
+from oracle import model_ref
 from tests._util import rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -61,6 +65,40 @@ def test_cached_steps_match_full_forward_f32(dev, use_rope, use_triton):
     assert cache.t == L
     with pytest.raises(ValueError):
         cache.step(ids[:, 0])
+
+
+@pytest.mark.parametrize("use_rope,use_triton", [(True, True), (True, False), (False, True)])
+def test_cached_steps_match_oracle_f64(dev, use_rope, use_triton):
+    """Prefill and every cached step (float32 model, exact decode kernel)
+    against the functional float64 restatement of the reference forward
+    (oracle/model_ref.py, same state_dict) over the whole context, last row:
+    what the reference's generation loop computes per token
+    (model.py:617-652,719-768).  W = 6 and 31 steps past a 9-token prompt,
+    so every local ring wraps several times; the global layers' caches fill
+    to max_seq_len."""
+    cfg = M.TensionConfig(vocab_size=80, dim=64, num_layers=4, num_heads=4, window=6,
+                          max_seq_len=40, dropout=0.0, global_every=2, use_rope=use_rope,
+                          use_triton=use_triton)
+    m = make_model(cfg, 13, dev)
+    sd = {k: v.detach().double().cpu() for k, v in m.state_dict().items()}
+    g = torch.Generator().manual_seed(15)
+    N, P, L = 2, 9, 40
+    ids = torch.randint(0, cfg.vocab_size, (N, L), generator=g)
+    print(f"[gen oracle] rope={use_rope} triton={use_triton}", flush=True)
+    cache = TensionKVCache(m, N)
+    worst = 0.0
+    with torch.no_grad():
+        pre = cache.prefill(ids[:, :P].to(dev)).double().cpu().numpy()
+        ref = model_ref.forward(sd, cfg, ids[:, :P]).numpy()
+        err = rel_l2(pre, ref)
+        assert err < 1e-5, ("prefill", err)
+        for t in range(P, L):
+            got = cache.step(ids[:, t].to(dev)).double().cpu().numpy()
+            ref = model_ref.forward(sd, cfg, ids[:, :t + 1])[:, -1].numpy()
+            err = rel_l2(got, ref)
+            worst = max(worst, err)
+            assert err < 1e-5, (t, err)
+    print(f"  worst step rel L2 {worst:.2e}", flush=True)
 
 
 @pytest.mark.parametrize("use_triton", [True, False])

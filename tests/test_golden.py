@@ -19,9 +19,10 @@ def load(name):
 
 
 def near(a, b, tol):
+    """Absolute max-abs bound (raw sums included)."""
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
     err = float(np.max(np.abs(a - b))) if a.size else 0.0
-    assert err <= tol * max(1.0, float(np.max(np.abs(b)))), err
+    assert err <= tol, f"max abs err {err:.3e} > {tol:.1e} (|ref| max {float(np.max(np.abs(b))):.3g})"
 
 
 # ------------------------------------------------------------------ CPU

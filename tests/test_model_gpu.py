@@ -175,6 +175,34 @@ def test_bf16_autocast_model_vs_reference_ops(dev, use_triton, return_all):
     assert e_grads[worst] < 4e-2, (worst, e_grads[worst])
 
 
+@pytest.mark.parametrize("return_all", [False, True])
+def test_117m_shape_step_vs_reference_ops(dev, return_all):
+    """Config 5's model (12 layers, dim 768, 12 heads, head_dim 64, vocab
+    32768, W = 64, global layers 3, 7, 11, RoPE) on one 1024-token sequence
+    under bf16 autocast: the kernels' logits, loss and every parameter
+    gradient against the same model with its tension ops swapped for the
+    reference's float32 math.  ``return_all`` is the reference-default step
+    (tau from every layer, the aux losses through dTau); without it, the
+    cross-entropy step (valid-count local layers)."""
+    cfg = M.config_117m(dropout=0.0, use_triton=True)
+    torch.manual_seed(4)
+    m = M.TensionLM(cfg).to(dev).train()
+    g = torch.Generator().manual_seed(14)
+    ids = torch.randint(0, cfg.vocab_size, (1, 1025), generator=g).to(dev)
+    print(f"[model 117m] return_all={return_all} params={m.num_params}", flush=True)
+    lg, loss, grads = _run_bf16(m, ids[:, :-1], ids[:, 1:], return_all)
+    with reference_ops():
+        lr, loss_r, grads_r = _run_bf16(m, ids[:, :-1], ids[:, 1:], return_all)
+    e_logits = rel_l2(lg, lr)
+    e_grads = {n: rel_l2(grads[n], grads_r[n]) for n in grads}
+    worst = max(e_grads, key=e_grads.get)
+    print(f"  logits rel {e_logits:.2e} loss {loss:.5f} vs {loss_r:.5f} worst grad {worst} "
+          f"{e_grads[worst]:.2e}", flush=True)
+    assert e_logits < 2e-2
+    assert abs(loss - loss_r) < 2e-2 * abs(loss_r)
+    assert e_grads[worst] < 2e-2, (worst, e_grads[worst])
+
+
 def test_adamw_steps_lower_the_loss(dev):
     cfg = M.TensionConfig(vocab_size=256, dim=128, num_layers=4, num_heads=2, window=64,
                           max_seq_len=256, dropout=0.1, global_every=2, use_rope=True,
