@@ -27,6 +27,9 @@ FORCE_EXACT = 1 << 3
 DECODE_SELF = 1 << 4
 TAU_VALID_ONLY = 1 << 5
 
+# bytes of the fixed device scratch of tension_global_bwd_noalloc
+NOALLOC_SCRATCH_BYTES = 8 << 20
+
 # status codes
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 _STATUS = {ERR_ARG: "bad argument", ERR_UNSUPPORTED: "unsupported", ERR_LAUNCH: "launch failure"}
@@ -53,6 +56,7 @@ SIGNATURES = {
     "tension_global_fwd": (_i32, [BufP] * 7 + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_global_bwd_workspace": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "tension_global_bwd": (_i32, [BufP] * 11 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
+    "tension_global_bwd_noalloc": (_i32, [BufP] * 11 + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_decode_step": (_i32, [BufP] * 7 + [_vp, _vp] + [_i64] * 4 + [_f64, _i32, _vp]),
     "tension_rope": (_i32, [BufP, BufP, _vp, _vp] + [_i64] * 6 + [_i32, _vp]),
     "tension_tau_head_stats": (_i32, [BufP, _i32] + [_i64] * 4 + [_vp, _i32, _vp]),

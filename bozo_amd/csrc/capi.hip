@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "kernels.h"
@@ -265,6 +266,42 @@ int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* 
 
 }  // namespace
 
+// ---------------------------------------------------------------- fixed scratch
+// Device workspace of tension_global_bwd_noalloc: one copy of this array per
+// GPU the library runs on, held until the process ends.  Host code reaches it
+// only through the address hipGetSymbolAddress returns for the current device
+// (the array's name in host code is not a device address).
+static __device__ __align__(256) unsigned char scratch[TENSION_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// Address of the current device's copy of `scratch`, looked up once per
+// device (the first call with that device current).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TENSION_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TENSION_ERR_UNSUPPORTED, "device %d: the fixed scratch supports devices 0..%d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TENSION_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* tension_last_error(void) { return g_err.c_str(); }
@@ -341,6 +378,28 @@ int tension_global_bwd(const tension_buf* q, const tension_buf* k, const tension
                        const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H, int64_t D, int64_t Wl,
                        double scale, int32_t flags, tension_stream_t stream) {
   const Shape sh{B, T, H, D};
+  TRY(band_bwd_dq(q, k, v, dout, dtau_local, bias, dq, ws, sh, Wl, scale, flags, stream, true, out, mass));
+  return band_bwd_dkv(q, k, v, dout, dtau_local, bias, dk, dv, ws, sh, Wl, scale, flags, stream, true);
+}
+
+int tension_global_bwd_noalloc(const tension_buf* q, const tension_buf* k, const tension_buf* v,
+                               const tension_buf* dout, const tension_buf* dtau_local, const tension_buf* bias,
+                               const tension_buf* out, const tension_buf* mass, const tension_buf* dq,
+                               const tension_buf* dk, const tension_buf* dv, int64_t B, int64_t T, int64_t H,
+                               int64_t D, int64_t Wl, double scale, int32_t flags, tension_stream_t stream) {
+  const Shape sh{B, T, H, D};
+  bool empty = false;
+  TRY(check_shape(sh, scale, &empty));
+  if (empty) return ok();
+  const int32_t acc = any_f64(q, k, v) ? TENSION_F64 : TENSION_F32;
+  const int64_t need = ws_bytes(B, T, H, acc, flags | TENSION_NORM_MASS);
+  if (need > (int64_t)TENSION_NOALLOC_SCRATCH_BYTES)
+    return fail(TENSION_ERR_ARG,
+                "tension_global_bwd_noalloc: B*T*H = %lld queries need %lld bytes of workspace, more than the "
+                "fixed scratch of %lld bytes (use tension_global_bwd with a caller workspace)",
+                (long long)(B * T * H), (long long)need, (long long)TENSION_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  TRY(scratch_ptr(&ws));
   TRY(band_bwd_dq(q, k, v, dout, dtau_local, bias, dq, ws, sh, Wl, scale, flags, stream, true, out, mass));
   return band_bwd_dkv(q, k, v, dout, dtau_local, bias, dk, dv, ws, sh, Wl, scale, flags, stream, true);
 }

@@ -19,7 +19,8 @@
  *  - A NULL tension_buf pointer means "absent" (no tau, no bias, ...).
  *  - The library never allocates device memory.  Work is enqueued on the
  *    given stream; no call synchronises the device.  All functions are
- *    reentrant; the only global state is the per-thread error string.
+ *    reentrant; the only global state is the per-thread error string and
+ *    the fixed device scratch of tension_global_bwd_noalloc.
  *  - Return value: TENSION_OK or a TENSION_ERR_* code; tension_last_error()
  *    describes the last failure on the calling thread.  Nothing throws
  *    across the ABI.
@@ -173,6 +174,32 @@ int tension_global_bwd(const tension_buf* q, const tension_buf* k,
                        const tension_buf* dv, void* workspace, int64_t B,
                        int64_t T, int64_t H, int64_t D, int64_t Wl,
                        double scale, int32_t flags, tension_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * tension_global_bwd without a caller workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as tension_global_bwd minus
+ * `workspace`; the per-query coefficients live in a fixed device array inside
+ * the library, TENSION_NOALLOC_SCRATCH_BYTES per GPU (one copy per device,
+ * held until the process ends; its address is looked up on the first call
+ * with that device current).  The call allocates nothing.  It needs
+ * 2 * B * T * H * 4 bytes (8 with f64 activations) of that array; larger
+ * requests return TENSION_ERR_ARG.  Every call on one GPU shares the array:
+ * calls that overlap on one GPU (several streams, several host threads) race
+ * and must be serialised by the caller.
+ * ------------------------------------------------------------------------- */
+#define TENSION_NOALLOC_SCRATCH_BYTES (8 << 20)
+
+int tension_global_bwd_noalloc(const tension_buf* q, const tension_buf* k,
+                               const tension_buf* v, const tension_buf* dout,
+                               const tension_buf* dtau_local,
+                               const tension_buf* bias, const tension_buf* out,
+                               const tension_buf* mass, const tension_buf* dq,
+                               const tension_buf* dk, const tension_buf* dv,
+                               int64_t B, int64_t T, int64_t H, int64_t D,
+                               int64_t Wl, double scale, int32_t flags,
+                               tension_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Streaming decode step over a ring K/V cache (no reference kernel: the
