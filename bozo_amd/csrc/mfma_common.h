@@ -511,4 +511,69 @@ __device__ __forceinline__ bf16x8 tr_join(const TrRead& t) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// ---------------------------------------------------------------------------
+// Ring loops with static slots.  A loop unrolled by the ring depth knows each
+// slot at compile time, so every LDS fragment address is a loop-invariant
+// per-lane register plus an immediate offset, and every copy source is a
+// uniform (scalar) base plus a loop-invariant 32-bit per-lane offset: no
+// vector arithmetic per block for either.
+// ---------------------------------------------------------------------------
+
+// Byte offset, within a direct tile, of the 16-byte row fragment (row, chunk).
+__device__ __forceinline__ uint32_t dt_row_off(int row, int chunk) {
+  return (uint32_t)(row * kTile + 8 * (chunk ^ dsw(row))) * 2u;
+}
+
+// Byte offsets, within a direct tile, of the two 8-byte halves a transposed
+// read (dt_tr8) of feature group m starting at tile row k0 addresses.
+__device__ __forceinline__ void dt_tr_off(int m, int k0, int g, int j, uint32_t* lo, uint32_t* hi) {
+  const int col = 16 * m + 4 * (j & 3);
+  const int r1 = k0 + 4 * g + (j >> 2), r2 = r1 + 16;
+  *lo = (uint32_t)(r1 * kTile + 8 * ((col >> 3) ^ dsw(r1)) + (col & 4)) * 2u;
+  *hi = (uint32_t)(r2 * kTile + 8 * ((col >> 3) ^ dsw(r2)) + (col & 4)) * 2u;
+}
+
+// 16-byte row fragment at LDS byte address addr + OFF.
+template <uint32_t OFF>
+__device__ __forceinline__ bf16x8 lds_row8(const bf16* lds0, uint32_t addr) {
+  return __builtin_bit_cast(bf16x8, *(const u16x8*)((const char*)lds0 + OFF + addr));
+}
+
+// dt_tr8_issue with precomputed byte addresses and a compile-time offset.
+template <uint32_t OFF>
+__device__ __forceinline__ TrRead tr8_issue_at(uint32_t lo, uint32_t hi) {
+  TrRead t;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(t.lo) : "v"(lo), "i"(OFF));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(t.hi) : "v"(hi), "i"(OFF));
+  return t;
+}
+
+// Per-lane source offsets of a direct-tile copy: lane L of wave w copies the
+// chunks q_n = (4n + w) * 64 + L (n = 0, 1) of the tile, i.e. row q_n / 8 and
+// logical chunk (q_n & 7) ^ dsw(row), at byte offset off[n] from the tile's
+// first row (the host keeps 64 rows of a tensor within 32-bit offsets).
+struct TileLane {
+  uint32_t off[2];
+};
+
+__device__ __forceinline__ TileLane tile_lane(int64_t rs, int wave, int lane) {
+  TileLane t;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int q = (n * 4 + wave) * 64 + lane;
+    const int r = q >> 3;
+    t.off[n] = (uint32_t)(((int64_t)r * rs + 8 * ((q & 7) ^ dsw(r))) * 2);
+  }
+  return t;
+}
+
+// Copy the 64 rows that start at `first` (a uniform pointer to a tile's first
+// row; every row must exist) into a direct tile.
+__device__ __forceinline__ void tile_dma(const bf16* first, const TileLane& tl, bf16* tile, int wave) {
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+    __builtin_amdgcn_global_load_lds((const void*)((const char*)first + tl.off[n]),
+                                     (lds_void*)(tile + (n * 4 + wave) * 512), 16, 0, 0);
+}
+
 }  // namespace tension

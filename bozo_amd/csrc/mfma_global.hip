@@ -41,23 +41,22 @@ __device__ __forceinline__ int gl_tau_col(const BandParams& p, int q, int k) {
 #ifndef TENSION_GL_FWD_WPE
 #define TENSION_GL_FWD_WPE 3
 #endif
+// with a bias or tau_local the per-pair operands need more registers: two
+// waves per SIMD instead of spilling
+#ifndef TENSION_GL_FWD_WPE_OPT
+#define TENSION_GL_FWD_WPE_OPT 2
+#endif
 
+// One 64-query tile of the forward, on the calling workgroup's LDS `lds`
+// (two ring slots: K in lds[s], V in lds[2 + s]; reused for the key-half
+// merge and the output staging).
 template <bool BIAS, bool TAU>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_FWD_WPE, 8)))
-void gl_fwd(BandParams p) {
-  // ring slots: K in lds[0..1], V in lds[2..3]; reused for the key-half merge
-  __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
-  bf16(*Kb)[kDTile] = lds;
-  bf16(*Vb)[kDTile] = lds + 2;
+__device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b, int h, bf16 (*lds)[kDTile]) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int qh = wave & 1, kh = wave >> 1;
-  const int BH = p.B * p.H;
-  const int id = (int)blockIdx.x;
-  const int tile = p.ntiles - 1 - id / BH;  // heaviest first
-  const int bh = id % BH;
-  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int T = p.T;
   const int t0 = tile * kTile;
   const int nblk = tile + 1;
 
@@ -90,31 +89,62 @@ void gl_fwd(BandParams p) {
       }
     }
   }
-  const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
-  tile_async_src(ksrc, 0, Kb[0], wave);
-  tile_async_src(vsrc, 0, Vb[0], wave);
-  if (nblk > 1) {
-    tile_async_src(ksrc, kTile, Kb[1], wave);
-    tile_async_src(vsrc, kTile, Vb[1], wave);
+  // Copies: every block before the diagonal one lies inside [0, T) and is
+  // read at a uniform base plus this lane's fixed offsets; the diagonal block
+  // (the last) has rows past T when T is ragged, and those are clamped.  A
+  // copy past the last block is clamped to it: it fills a free slot nothing
+  // reads, which keeps every copy unconditional.
+  const TileLane kl = tile_lane(p.k.s1, wave, lane), vl = tile_lane(p.v.s1, wave, lane);
+  const int64_t kstep = (int64_t)kTile * p.k.s1, vstep = (int64_t)kTile * p.v.s1;
+  const bool ragged = (T % kTile) != 0;
+  auto copy = [&](int blk, auto slot_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(slot_tag)::value;
+    blk = blk < nblk ? blk : nblk - 1;
+    if (ragged && blk == nblk - 1) {
+      tile_async(kb_, p.k.s1, blk * kTile, T, lds[S], wave, lane);
+      tile_async(vb_, p.v.s1, blk * kTile, T, lds[2 + S], wave, lane);
+    } else {
+      tile_dma(kb_ + blk * kstep, kl, lds[S], wave);
+      tile_dma(vb_ + blk * vstep, vl, lds[2 + S], wave);
+    }
+  };
+  // this lane's LDS fragment offsets within a tile (loop-invariant; the ring
+  // slot is an immediate offset)
+  uint32_t ko[2][2], vlo[4], vhi[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    ko[j][0] = dt_row_off(32 * kh + 16 * j + c, g);
+    ko[j][1] = dt_row_off(32 * kh + 16 * j + c, 4 + g);
   }
+  const uint32_t lbase = lds_addr(&lds[0][0]);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    dt_tr_off(m, 32 * kh, g, c, &vlo[m], &vhi[m]);
+    vlo[m] += lbase;
+    vhi[m] += lbase;
+  }
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  copy(0, S0{});
+  copy(1, S1{});
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
   const bf16x8 ones = ones_bf16x8();
   f32x4 acc[2][4] = {};
   f32x4 macc[2] = {};
 
-  // one 64-key block: S, P, O += P V, mass += P 1 (diag: the last block,
-  // masked key <= query; TB: the block holds tau_local columns)
-  auto block = [&](int blk, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
+  // one 64-key block in ring slot S: S, P, O += P V, mass += P 1 (diag: the
+  // last block, masked key <= query; TB: the block holds tau_local columns)
+  auto block = [&](int blk, auto slot_tag, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(slot_tag)::value;
     constexpr bool diag = decltype(diag_tag)::value;
     constexpr bool TB = TAU && decltype(tau_tag)::value;
-    const bf16* Ks = Kb[blk & 1];
-    const bf16* Vs = Vb[blk & 1];
+    constexpr uint32_t KO = S * kDTile * 2, VO = (2 + S) * kDTile * 2;
     // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
     f32x4 s[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const bf16x8 a0 = dt_row8(Ks, 32 * kh + 16 * j + c, g);
-      const bf16x8 a1 = dt_row8(Ks, 32 * kh + 16 * j + c, 4 + g);
+      const bf16x8 a0 = lds_row8<KO>(&lds[0][0], ko[j][0]);
+      const bf16x8 a1 = lds_row8<KO>(&lds[0][0], ko[j][1]);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         f32x4 z = {};
@@ -124,7 +154,7 @@ void gl_fwd(BandParams p) {
     }
     TrRead vr[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) vr[m] = dt_tr8_issue(Vs, m, 32 * kh, g, c);
+    for (int m = 0; m < 4; ++m) vr[m] = tr8_issue_at<VO>(vlo[m], vhi[m]);
     bf16x8 vt[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -156,34 +186,49 @@ void gl_fwd(BandParams p) {
   };
   // tau_local columns are keys T - Wtau .. T - 1: only the blocks that hold
   // one run the per-pair column code
-  auto visit = [&](int blk, auto diag_tag) __attribute__((always_inline)) {
+  auto visit = [&](int blk, auto slot_tag, auto diag_tag) __attribute__((always_inline)) {
     if constexpr (TAU) {
       if ((blk + 1) * kTile > T - p.Wtau) {
-        block(blk, diag_tag, std::true_type{});
+        block(blk, slot_tag, diag_tag, std::true_type{});
         return;
       }
     }
-    block(blk, diag_tag, std::false_type{});
+    block(blk, slot_tag, diag_tag, std::false_type{});
   };
-  // Off-diagonal blocks: the next block's copy (4 instructions) is always in
-  // flight here, so the wait leaves exactly it outstanding.
-  for (int blk = 0; blk + 1 < nblk; ++blk) {
+  // Two-slot ring, two blocks per trip (slot 0 then slot 1), both before
+  // the diagonal block.  Each wait leaves exactly the next block's copy (4
+  // instructions) in flight: the loop only continues when block blk + 3
+  // exists, and its copy was issued in the previous trip or the prologue.
+  int blk = 0;
+  for (; blk + 2 < nblk; blk += 2) {
     wait_vm<4>();
     lds_barrier();
-    visit(blk, std::false_type{});
-    if (blk + 2 < nblk) {
-      lds_barrier();  // every wave is done with this ring slot
-      tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
-      tile_async_src(vsrc, (blk + 2) * kTile, Vb[blk & 1], wave);
-    }
+    visit(blk, S0{}, std::false_type{});
+    lds_barrier();  // every wave is done with slot 0
+    copy(blk + 2, S0{});
+    wait_vm<4>();
+    lds_barrier();
+    visit(blk + 1, S1{}, std::false_type{});
+    lds_barrier();
+    copy(blk + 3, S1{});
   }
-  wait_vm<0>();
-  lds_barrier();
-  visit(nblk - 1, std::true_type{});
+  if (blk + 2 == nblk) {  // an off-diagonal block in slot 0, the diagonal in slot 1
+    wait_vm<4>();
+    lds_barrier();
+    visit(blk, S0{}, std::false_type{});
+    wait_vm<0>();
+    lds_barrier();
+    visit(blk + 1, S1{}, std::true_type{});
+  } else {  // the diagonal block in slot 0
+    wait_vm<0>();
+    lds_barrier();
+    visit(blk, S0{}, std::true_type{});
+  }
 
   // Key halves meet: wave (qh, kh) keeps query tile i = kh and hands its
   // partial of tile 1 - kh to its partner (qh, 1 - kh) through LDS:
   // red[slot][e][lane], slot = 2 qh + kh, 17 floats (16 of O^T, 1 mass).
+  wait_vm<0>();     // a copy past the last block may still be in flight
   __syncthreads();  // the ring slots are free
   float* red = (float*)&lds[0][0];  // 4 x 17 x 64 floats = 17 KB of the 32 KB
   auto give = [&](const f32x4* a, const f32x4& mm) {
@@ -223,6 +268,21 @@ void gl_fwd(BandParams p) {
                     1.f / (m > kMassEps ? m : kMassEps), g, c, lane, &lds[0][0] + wave * (16 * kTile));
   const int tq = r0 + c;
   if (tq < T && p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, m);
+}
+
+// A workgroup owns one 64-query tile of one (b, h); workgroups go out
+// heaviest tile first, and blockIdx -> (b, h) = id % (B H) keeps the tiles of
+// one (b, h) on one XCD (round-robin dispatch).  (Pairing a heavy and a light
+// tile per workgroup, one round of equal workgroups, measured slower.)
+template <bool BIAS, bool TAU>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(BIAS || TAU ? TENSION_GL_FWD_WPE_OPT : TENSION_GL_FWD_WPE, 8)))
+void gl_fwd(BandParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
+  const int BH = p.B * p.H;
+  const int id = (int)blockIdx.x;
+  const int bh = id % BH;
+  gl_fwd_tile<BIAS, TAU>(p, p.ntiles - 1 - id / BH, bh / p.H, bh % p.H, lds);
 }
 
 // ---------------------------------------------------------------- backward
