@@ -1,6 +1,6 @@
 """Benchmark of the MI355X sigmoid-tension hot path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic]
 
 Workload (the 117M-model shape the metric is quoted
 on): windowed tension fwd+bwd, B=8 H=12 T=1024 d=64 W=64, bf16 storage with
@@ -18,6 +18,12 @@ synchronize.  Each kernel is then timed alone the same way (graphs of its
 launches over the rotated sets, on the same stream) for the roofline entry;
 ``rocprofv3 --kernel-trace --marker-trace --stats`` of this command, read
 back with ``--summarize``, gives the per-kernel durations in profiles/.
+
+HBM traffic (``roofline.traffic``) is measured in the same run: two
+``rocprofv3 --pmc`` passes (FETCH_SIZE, then WRITE_SIZE) over this script's
+``--profile-kernels`` driver run as child processes, each counter calibrated
+by the driver's 256 MiB device copy (``--no-traffic`` skips them; the field
+is then null).
 
 The CPU baseline times the reference's CPU path (unfold gather + tau-mass +
 autograd, restated in oracle/torch_ref.py) in float32 on the host cores, on
@@ -413,11 +419,6 @@ def bench_window(args, dev):
                  "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                  "kernels": per_kernel},
     }
-    tfile = os.path.join(ROOT, "profiles", "traffic_window_c2.json")
-    if os.path.exists(tfile):
-        with open(tfile) as f:
-            tr = json.load(f)
-        result["roofline"]["traffic"] = tr.get("bytes_per_launch", {}).get(result["roofline"]["kernel"])
 
     # secondary variants: raw contract, and tau materialised + dTau (export path)
     del steps
@@ -510,10 +511,10 @@ def _phase_regions(cur):
     return out
 
 
-def summarize(paths):
-    """Per-phase kernel statistics and calibrated HBM traffic from rocprofv3
+def _collect(paths):
+    """Kernel durations per phase and per-dispatch counter means from rocprofv3
     rocpd databases (the *_results.db of --kernel-trace [--marker-trace] or
-    --pmc FETCH_SIZE / --pmc WRITE_SIZE runs of this script)."""
+    --pmc runs of this script)."""
     import glob
     import sqlite3
     import statistics
@@ -521,7 +522,8 @@ def summarize(paths):
     for path in paths:
         dbs += [path] if path.endswith(".db") else sorted(glob.glob(os.path.join(path, "**", "*.db"),
                                                                     recursive=True))
-    counters = {}  # counter -> kernel -> mean value per dispatch
+    durations = []  # (db, [(phase, {kernel: [us, ...]})])
+    counters = {}   # counter -> kernel -> (mean value per dispatch, dispatches)
     for db in dbs:
         cur = sqlite3.connect(db).cursor()
         kern = cur.execute("select name, start, end from kernels").fetchall()
@@ -540,15 +542,46 @@ def summarize(paths):
                 if big:
                     counters[cn]["__amd_rocclr_copyBuffer"] = (statistics.mean(big), len(big))
             continue
+        if not kern:
+            continue
         phases = _phase_regions(cur) or [("all", min(k[1] for k in kern), max(k[2] for k in kern))]
-        print(f"# kernel durations: {os.path.basename(os.path.dirname(db))}/{os.path.basename(db)}")
-        print("| phase | kernel | dispatches | mean us | median us | min us | max us |")
-        print("|---|---|---|---|---|---|---|")
+        per = []
         for pname, a, b in phases:
             by = {}
             for n, s0, s1 in kern:
                 if s0 >= a and s1 <= b:
                     by.setdefault(n.split("(")[0], []).append((s1 - s0) / 1e3)
+            per.append((pname, by))
+        durations.append((db, per))
+    return durations, counters
+
+
+def hbm_traffic(counters):
+    """Copy-calibrated HBM bytes per launch {kernel: (read, write)} from
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) readings, or {} without them."""
+    copy = "__amd_rocclr_copyBuffer"
+    fe, wr = counters.get("FETCH_SIZE", {}), counters.get("WRITE_SIZE", {})
+    if copy not in fe or copy not in wr:
+        return {}, None
+    known_kib = 256 * 1024  # the profile driver copies 256 MiB
+    sf, sw = known_kib / fe[copy][0], known_kib / wr[copy][0]
+    out = {}
+    for n in sorted(set(fe) & set(wr)):
+        if n == copy or "tension::" not in n:
+            continue
+        out[n] = (fe[n][0] * sf * 1024, wr[n][0] * sw * 1024)
+    return out, (sf, sw)
+
+
+def summarize(paths):
+    """Print per-phase kernel statistics, counters and calibrated HBM traffic."""
+    import statistics
+    durations, counters = _collect(paths)
+    for db, per in durations:
+        print(f"# kernel durations: {os.path.basename(os.path.dirname(db))}/{os.path.basename(db)}")
+        print("| phase | kernel | dispatches | mean us | median us | min us | max us |")
+        print("|---|---|---|---|---|---|---|")
+        for pname, by in per:
             tot = sum(sum(x) for x in by.values())
             for n, d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
                 if sum(d) < 0.01 * tot:
@@ -563,19 +596,47 @@ def summarize(paths):
         for cn, by in counters.items():
             for n, (v, cnt) in by.items():
                 print(f"| {n[:70]} | {cn} | {v:.1f} | {cnt} |")
-        copy = "__amd_rocclr_copyBuffer"
-        fe, wr = counters.get("FETCH_SIZE", {}), counters.get("WRITE_SIZE", {})
-        if copy in fe and copy in wr:
-            known_kib = 256 * 1024  # the profile driver copies 256 MiB
-            sf, sw = known_kib / fe[copy][0], known_kib / wr[copy][0]
-            print(f"\ncopy-kernel calibration: FETCH_SIZE x{sf:.3f}, WRITE_SIZE x{sw:.3f}")
+        traffic, cal = hbm_traffic(counters)
+        if cal:
+            print(f"\ncopy-kernel calibration: FETCH_SIZE x{cal[0]:.3f}, WRITE_SIZE x{cal[1]:.3f}")
             print("\n| kernel | HBM read MB | HBM write MB | total MB per launch |")
             print("|---|---|---|---|")
-            for n in sorted(set(fe) & set(wr)):
-                if n == copy or "tension::" not in n:
-                    continue
-                r, w = fe[n][0] * sf * 1024 / 1e6, wr[n][0] * sw * 1024 / 1e6
-                print(f"| {n} | {r:.2f} | {w:.2f} | {r + w:.2f} |")
+            for n, (r, w) in traffic.items():
+                print(f"| {n} | {r / 1e6:.2f} | {w / 1e6:.2f} | {(r + w) / 1e6:.2f} |")
+
+
+def measure_traffic(n=16, timeout=240):
+    """HBM bytes per launch, measured now: two rocprofv3 --pmc passes
+    (FETCH_SIZE, then WRITE_SIZE) over this script's --profile-kernels
+    driver, run as child processes on the same GPU, calibrated by the
+    driver's 256 MiB device copy.  Returns ({kernel: bytes}, note)."""
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return {}, "rocprofv3 not found: traffic not measured"
+    tmp = tempfile.mkdtemp(prefix="bench_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = os.path.join(tmp, counter)
+        cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--", sys.executable, os.path.abspath(__file__),
+               "--profile-kernels", str(n)]
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, env=env, cwd=ROOT)
+        except subprocess.TimeoutExpired:
+            return {}, f"rocprofv3 --pmc {counter} timed out: traffic not measured"
+        # rocprofv3 itself may end with a segmentation fault after the program
+        # finished and its results are whole; the results decide
+        if r.returncode not in (0, -11, 139) or "profile-kernels:" not in (r.stdout + r.stderr):
+            return {}, f"rocprofv3 --pmc {counter} failed (rc {r.returncode}): traffic not measured"
+    _, counters = _collect([tmp])
+    traffic, cal = hbm_traffic(counters)
+    if not traffic:
+        return {}, "no calibrated FETCH_SIZE / WRITE_SIZE readings: traffic not measured"
+    return ({k: int(r + w) for k, (r, w) in traffic.items()},
+            f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE in this run, {n} launches per kernel, "
+            f"copy-calibrated x{cal[0]:.3f} / x{cal[1]:.3f}")
 
 
 def bench_global(dev, steps, warmup):
@@ -625,11 +686,7 @@ def bench_decode(dev, reps):
     run = Runner([lambda: [caches[i % NC].step(q[i], k[i], v[i]) for i in range(S)]], warm=1)
     ms = time_units(run, reps, 1, "decode") / S
     step_bytes = 2 * N * H * W * D * 2 + 4 * N * H * D * 2
-    traffic = None  # HBM bytes per launch from the committed rocprofv3 --pmc summary
-    tfile = os.path.join(ROOT, "profiles", "traffic_window_c2.json")
-    if os.path.exists(tfile):
-        with open(tfile) as f:
-            traffic = json.load(f).get("bytes_per_launch", {}).get("decode_bf16_d64")
+    traffic = None  # filled in by main() from this run's counter passes
     return {"config": "decode 64 seqs H16 d64 W256 bf16, 4 rotated caches, 512 steps per graph (config 4)",
             "us_per_step": round(ms * 1e3, 3), "steps_per_s": round(1e3 / ms, 1),
             "alg_bytes_per_step": step_bytes,
@@ -856,6 +913,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes that measure HBM traffic")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                     help="only launch each band kernel N times (counter collection)")
@@ -914,6 +973,24 @@ def main():
     others.append(bench_generation(dev))
     log(f"[bench] {others[-1]}")
     result["other_configs"] = others
+    if not args.no_traffic:
+        log("[bench] HBM traffic: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes ...")
+        traffic, note = measure_traffic()
+        pick = lambda key: next((v for k, v in traffic.items() if key in k), None)  # noqa: E731
+        result["roofline"]["traffic"] = pick({"mfma_bwd_fused": "mfma_bwd_fused<1, false, false, true>",
+                                              "mfma_fwd_ring": "mfma_fwd_ring<1, false, false, true>"}
+                                             [result["roofline"]["kernel"]])
+        result["roofline"]["traffic_source"] = note
+        for name, key in (("fwd", "mfma_fwd_ring<1, false, false, true>"),
+                          ("bwd", "mfma_bwd_fused<1, false, false, true>")):
+            result["step"]["kernels"][name]["traffic"] = pick(key)
+        for o in others:
+            if o["config"].startswith("decode"):
+                o["traffic"] = pick("decode_bf16_d64")
+            if o["config"].startswith("global block"):
+                o["traffic"] = {k.split("::")[-1]: v for k, v in traffic.items()
+                                if "gl_" in k or "coef_from_out" in k} or None
+        log(f"[bench] traffic: {note}; {result['roofline']['traffic']} bytes per dominant launch")
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(1, 1024, 12, 64, 64, args.cpu_seconds)
