@@ -432,6 +432,17 @@ def bench_window(args, dev):
     result["variants"]["tau_materialised_ms"] = round(
         time_units(tau, args.steps, args.warmup, "step:tau"), 5)
     del tau
+    # the reference's autocast dtype flow: fp32 RoPE'd Q / K, bf16 V, fp32 out
+    # and dOut (the split-operand kernels)
+    mixed = []
+    for s in sets:
+        mixed.append(dict(Q=s["Q"].detach().float().requires_grad_(True),
+                          K=s["K"].detach().float().requires_grad_(True),
+                          V=s["V"], dO=s["dO"].float()))
+    del sets
+    mx = Runner([window_step_fn(s, W, scale, "mass") for s in mixed])
+    result["variants"]["mixed_dtype_ms"] = round(time_units(mx, args.steps, args.warmup, "step:mixed"), 5)
+    del mx, mixed
     return result
 
 
@@ -695,20 +706,21 @@ def bench_decode(dev, reps):
             "traffic": traffic}
 
 
-def bench_model(dev, steps, warmup, aux):
+def bench_model(dev, steps, warmup, aux, fast_rope=False):
     """Config 5: one TensionLM-117M training step (random init, bf16
     autocast, AdamW as train.py:894-902, clip 1.0) on B8 x T1024 token ids
     ~ U[0, 32768).  ``aux``: the reference default, return_all with tau
     emitted by every layer and the four aux losses computed (weights 0.01,
     0.02, 0, 0 as train.py:135-140 -- all four are evaluated there too; the
     three tau losses in the fused kernels); otherwise CE only (local layers
-    on the valid-count path, no tau)."""
+    on the valid-count path, no tau).  ``fast_rope``: rotated Q / K stay bf16
+    (the bf16 kernels) instead of the reference's float32 promotion."""
     import gc
     import torch.nn.functional as F
     from bozo_amd import model as M
     gc.collect()
     torch.cuda.empty_cache()  # blocks cached by the earlier benches would be split for this one
-    cfg = M.config_117m(use_triton=True)
+    cfg = M.config_117m(use_triton=True, fast_rope=fast_rope)
     torch.manual_seed(4)
     m = M.TensionLM(cfg).to(dev).train()
     opt = M.configure_adamw(m, lr=3e-4, weight_decay=0.1, fused=True)
@@ -749,7 +761,8 @@ def bench_model(dev, steps, warmup, aux):
     wall = (time.perf_counter() - t0) * 1e3 / steps
     ms = e0.elapsed_time(e1) / steps
     res = {"config": "TensionLM-117M training step B8 T1024 bf16 autocast AdamW (config 5), "
-                     + ("aux losses + tau (reference default)" if aux else "CE only"),
+                     + ("aux losses + tau (reference default)" if aux else "CE only")
+                     + (", bf16 Q/K (fast_rope)" if fast_rope else ", fp32 RoPE'd Q/K (reference dtype flow)"),
            "ms_per_step": round(ms, 3), "wall_ms_per_step": round(wall, 3),
            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "params": m.num_params,
            "final_loss": round(float(loss.item()), 4)}
@@ -947,8 +960,9 @@ def main():
         print(json.dumps(bench_bias(dev)), flush=True)
         return
     if args.model_only:
-        for aux in (False, True):
-            print(json.dumps(bench_model(dev, args.steps, args.warmup, aux)), flush=True)
+        for fast in (False, True):
+            for aux in (False, True):
+                print(json.dumps(bench_model(dev, args.steps, args.warmup, aux, fast)), flush=True)
         if not args.no_cpu:
             print(json.dumps({"cpu_model_baselines": cpu_model_baselines(args.cpu_seconds)}), flush=True)
         return
@@ -959,10 +973,11 @@ def main():
     log("[bench] decode (config 4) ...")
     others.append(bench_decode(dev, 4))
     log(f"[bench] {others[-1]}")
-    for aux in (False, True):
-        log(f"[bench] TensionLM-117M training step (config 5, aux={aux}) ...")
-        others.append(bench_model(dev, 10, 5, aux))
-        log(f"[bench] {others[-1]}")
+    for fast in (False, True):
+        for aux in (False, True):
+            log(f"[bench] TensionLM-117M training step (config 5, aux={aux}, fast_rope={fast}) ...")
+            others.append(bench_model(dev, 10, 5, aux, fast))
+            log(f"[bench] {others[-1]}")
     log("[bench] tau export reductions ...")
     others.append(bench_export(dev))
     log(f"[bench] {others[-1]}")

@@ -25,6 +25,7 @@ ARCH = os.environ.get("TENSION_OFFLOAD_ARCH", "gfx950")
 SOURCES = [
     "capi.hip", "exact.hip", "decode.hip",
     "mfma.hip", "mfma_fwd.hip", "mfma_dq.hip", "mfma_dkv.hip", "mfma_bwd_fused.hip", "mfma_global.hip",
+    "mfma_mixed.hip",
     "tau_export.hip", "graph_bias.hip", "aux_loss.hip",
     "exact_fwd_f32.hip", "exact_dq_f32.hip", "exact_dkv_f32.hip",
     "exact_fwd_f64.hip", "exact_dq_f64.hip", "exact_dkv_f64.hip",

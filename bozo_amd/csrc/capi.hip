@@ -121,9 +121,30 @@ void set_global(BandParams& p, int64_t Wl) {
   p.Wtau = (int)Wl;
 }
 
-int run_band(int phase, bool mfma, bool f64, const BandParams& p, tension_stream_t stream, const char* what) {
+// 16-byte aligned float32 rows (head dim multiple of 4, unit innermost stride)
+bool aligned_f32_rows(const tension_buf* b) {
+  if (!b || b->dtype != TENSION_F32) return false;
+  if (((uintptr_t)b->ptr & 15) != 0) return false;
+  return (b->s[0] % 4 == 0) && (b->s[1] % 4 == 0) && (b->s[2] % 4 == 0);
+}
+
+// The reference's autocast flow (float32 rotated Q / K, bfloat16 V, float32
+// out and dOut) on the split-operand MFMA kernels: local windows W <= 64,
+// head dim 64.
+bool mixed_ok(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* bias,
+              int64_t D, int64_t W, int flags, bool global) {
+  if (global || (flags & TENSION_FORCE_EXACT) || D != 64 || W < 1 || W > 64) return false;
+  if (!aligned_f32_rows(q) || !aligned_f32_rows(k) || !aligned_bf16_rows(v)) return false;
+  return !bias || bias->dtype == TENSION_F32;
+}
+
+enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_MIXED = 2 };
+
+int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_t stream, const char* what) {
   hipError_t e = hipSuccess;
-  int r = mfma ? launch_mfma(phase, p, hs(stream), &e) : launch_exact(phase, f64, p, hs(stream), &e);
+  int r = kind == KERNEL_MIXED ? launch_mixed(phase, p, hs(stream), &e)
+          : kind == KERNEL_MFMA ? launch_mfma(phase, p, hs(stream), &e)
+                                : launch_exact(phase, f64, p, hs(stream), &e);
   if (r != 0)
     return fail(TENSION_ERR_UNSUPPORTED, "%s: head dim %d not supported (exact path: 8,16,32,64,128)", what, p.D);
   return launched(e, what);
@@ -164,7 +185,8 @@ int band_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, c
   p.out = make_buf(out); p.tau = make_buf(tau); p.bias = make_buf(bias); p.mass = make_buf(mass);
   const bool mf = !(flags & TENSION_FORCE_EXACT) && sh.D == 64 && aligned_bf16_rows(q) && aligned_bf16_rows(k) &&
                   aligned_bf16_rows(v) && aligned_bf16_rows(out) && (!bias || bias->dtype == TENSION_F32);
-  return run_band(0, mf, any_f64(q, k, v), p, stream, what);
+  const bool mx = !mf && mixed_ok(q, k, v, bias, sh.D, Wparam, flags, global) && aligned_f32_rows(out);
+  return run_band(0, mx ? KERNEL_MIXED : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream, what);
 }
 
 // ---------------------------------------------------------------- backward
@@ -236,6 +258,8 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
   BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, Wparam, scale, flags, global);
   p.dq = make_buf(dq);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dq, nullptr, sh.D, flags);
+  const bool mx = !mf && mixed_ok(q, k, v, bias, sh.D, Wparam, flags, global) && aligned_f32_rows(dout) &&
+                  aligned_f32_rows(dq);
   if (mf && out && mass) {
     TRY(check_buf(out, "out", true, 3));
     TRY(check_buf(mass, "mass", true, -1));
@@ -245,7 +269,8 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
       p.coef_pre = 1;
     }
   }
-  return run_band(1, mf, any_f64(q, k, v), p, stream, global ? "tension_global_bwd(dq)" : "tension_window_bwd_dq");
+  return run_band(1, mx ? KERNEL_MIXED : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
+                  global ? "tension_global_bwd(dq)" : "tension_window_bwd_dq");
 }
 
 int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
@@ -261,7 +286,10 @@ int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* 
   p.dk = make_buf(dk);
   p.dv = make_buf(dv);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dk, dv, sh.D, flags);
-  return run_band(2, mf, any_f64(q, k, v), p, stream, global ? "tension_global_bwd(dkv)" : "tension_window_bwd_dkv");
+  const bool mx = !mf && mixed_ok(q, k, v, bias, sh.D, Wparam, flags, global) && aligned_f32_rows(dout) &&
+                  aligned_f32_rows(dk) && aligned_bf16_rows(dv);
+  return run_band(2, mx ? KERNEL_MIXED : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
+                  global ? "tension_global_bwd(dkv)" : "tension_window_bwd_dkv");
 }
 
 }  // namespace
@@ -354,7 +382,7 @@ int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension
       p.dq = make_buf(dq);
       p.dk = make_buf(dk);
       p.dv = make_buf(dv);
-      return run_band(3, true, false, p, stream, "tension_window_bwd");
+      return run_band(3, KERNEL_MFMA, false, p, stream, "tension_window_bwd");
     }
   }
   TRY(band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, sh, W, scale, flags, stream, false));
@@ -445,8 +473,17 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 1024 && a16(q, false) &&
                     a16(k_new, false) && a16(v_new, false) && a16(out, false) && a16(k_cache, true) &&
                     a16(v_cache, true) && slab_fits(k_cache) && slab_fits(v_cache);
+  // the reference's autocast flow: float32 q / K (promoted by RoPE), bf16 V
+  auto f16b = [](const tension_buf* b, bool four) {  // 16-byte aligned float32 rows
+    if (b->dtype != TENSION_F32 || ((uintptr_t)b->ptr & 15)) return false;
+    return b->s[0] % 4 == 0 && b->s[1] % 4 == 0 && (!four || b->s[2] % 4 == 0);
+  };
+  const bool kf32 = !fast && !(flags & TENSION_FORCE_EXACT) && !(flags & TENSION_DECODE_SELF) && D == 64 &&
+                    W <= 1024 && f16b(q, false) && f16b(k_new, false) && f16b(out, false) && f16b(k_cache, true) &&
+                    a16(v_new, false) && a16(v_cache, true) && k_cache->s[2] >= 64 &&
+                    W * k_cache->s[2] * 4 < ((int64_t)1 << 31) && slab_fits(v_cache);
   hipError_t e = hipSuccess;
-  launch_decode(fast, is_f64(q) || is_f64(k_cache) || is_f64(v_cache), p, hs(stream), &e);
+  launch_decode(fast || kf32, is_f64(q) || is_f64(k_cache) || is_f64(v_cache), p, hs(stream), &e, kf32);
   return launched(e, "tension_decode_step");
 }
 

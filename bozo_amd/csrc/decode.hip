@@ -47,31 +47,47 @@ constexpr int kCacheAux = 2;
 
 }  // namespace
 
-template <int NW, int NP>
+// KF32: q, k_new, the K cache and out in float32 with a bf16 V cache (the
+// reference's autocast dtype flow: rotated Q / K promoted to float32); a K
+// row is then 256 bytes, two 16-byte loads per lane, and the dot products
+// are float32 products.  Not with TENSION_DECODE_SELF.
+template <int NW, int NP, bool KF32 = false>
 __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   constexpr int kRows = 8 * NW;  // cache rows per pass
+  constexpr int kKBytes = KF32 ? 4 : 2;   // bytes per K / q / out element
+  constexpr int kKChunks = KF32 ? 16 : 8;  // 16-byte chunks of a K row
   __shared__ float red[NW * 4][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ch = lane & 7, rw = lane >> 3;  // d-chunk, row within a pass
   const int n = blockIdx.x / p.H, h = blockIdx.x % p.H;
   const int W = p.W;
 
-  const bf16* qrow = (const bf16*)p.q.p + n * p.q.s0 + h * p.q.s1;
-  const u16x8 qbits = *(const u16x8*)(qrow + 8 * ch);
+  // this lane's 8 query features (8 ch .. +7)
+  u16x8 qbits, qbits2;
+  if constexpr (KF32) {
+    const float* qrow = (const float*)p.q.p + n * p.q.s0 + h * p.q.s1 + 8 * ch;
+    qbits = *(const u16x8*)qrow;
+    qbits2 = *(const u16x8*)(qrow + 4);
+  } else {
+    const bf16* qrow = (const bf16*)p.q.p + n * p.q.s0 + h * p.q.s1;
+    qbits = *(const u16x8*)(qrow + 8 * ch);
+  }
   // The new token's K / V rows are appended after the reduction, but fetched
   // now so their latency hides under the cache stream: lanes a = tid - 64 in
-  // [0, 8) hold 16-byte chunk a of k_new, [8, 16) chunk a - 8 of v_new.  The
-  // descriptors span one 128-byte row; every other lane's offset is out of
-  // range and reads zero without a memory access, so the loads need no branch.
+  // [0, kKChunks) hold 16-byte chunk a of k_new, the next 8 chunk
+  // a - kKChunks of v_new.  The descriptors span one row; every other lane's
+  // offset is out of range and reads zero without a memory access, so the
+  // loads need no branch.
   const int ai = tid - 64;
   const __amdgpu_buffer_rsrc_t knr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const bf16*)p.kn.p + n * p.kn.s0 + h * p.kn.s1), (short)0, 128, kRawBufWord3);
+      (void*)((const char*)p.kn.p + (n * p.kn.s0 + h * p.kn.s1) * kKBytes), (short)0, 16 * kKChunks,
+      kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vnr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const bf16*)p.vn.p + n * p.vn.s0 + h * p.vn.s1), (short)0, 128, kRawBufWord3);
   const u16x8 knew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-      knr, (ai >= 0 && ai < 8) ? 16 * ai : 128, 0, 0));
+      knr, (ai >= 0 && ai < kKChunks) ? 16 * ai : 16 * kKChunks, 0, 0));
   const u16x8 vnew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-      vnr, (ai >= 8 && ai < 16) ? 16 * (ai - 8) : 128, 0, 0));
+      vnr, (ai >= kKChunks && ai < kKChunks + 8) ? 16 * (ai - kKChunks) : 128, 0, 0));
 
   // One descriptor per cache slab; loads of rows past its range return
   // zeros.  The range is W rows, or, for a self-key step (a global layer's
@@ -84,20 +100,24 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
     const int pe = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
     rows = pe < W ? pe : W;
   }
-  const bf16* kbase = (const bf16*)p.kc.p + n * p.kc.s0 + h * p.kc.s1;
+  const char* kbase = (const char*)p.kc.p + (n * p.kc.s0 + h * p.kc.s1) * kKBytes;
   const bf16* vbase = (const bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1;
   const __amdgpu_buffer_rsrc_t kr_ = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)kbase, (short)0, (int)((int64_t)rows * p.kc.s2 * 2), kRawBufWord3);
+      (void*)kbase, (short)0, (int)((int64_t)rows * p.kc.s2 * kKBytes), kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vr_ = __builtin_amdgcn_make_buffer_rsrc(
       (void*)vbase, (short)0, (int)((int64_t)rows * p.vc.s2 * 2), kRawBufWord3);
   const uint32_t row0 = (uint32_t)(wave * 8 + rw);
-  const uint32_t kstep = (uint32_t)(kRows * p.kc.s2 * 2), vstep = (uint32_t)(kRows * p.vc.s2 * 2);
-  const uint32_t koff = row0 * (uint32_t)(p.kc.s2 * 2) + 16 * ch;
+  const uint32_t kstep = (uint32_t)(kRows * p.kc.s2 * kKBytes), vstep = (uint32_t)(kRows * p.vc.s2 * 2);
+  const uint32_t koff = row0 * (uint32_t)(p.kc.s2 * kKBytes) + 8 * kKBytes * ch;
   const uint32_t voff = row0 * (uint32_t)(p.vc.s2 * 2) + 16 * ch;
-  u16x8 kr[NP], vr[NP];
+  u16x8 kr[NP], kr2[KF32 ? NP : 1], vr[NP];
 #pragma unroll
-  for (int i = 0; i < NP; ++i)
+  for (int i = 0; i < NP; ++i) {
     kr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(kr_, (int)(koff + i * kstep), 0, kCacheAux));
+    if constexpr (KF32)
+      kr2[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(kr_, (int)(koff + i * kstep + 16), 0,
+                                                                               kCacheAux));
+  }
 #pragma unroll
   for (int i = 0; i < NP; ++i)
     vr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(vr_, (int)(voff + i * vstep), 0, kCacheAux));
@@ -106,19 +126,34 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   const int live = pos < W ? pos : W;  // slots [0, live) hold tokens
   // Whole-vector bit casts only: a bit cast of one subscripted vector
   // element (bit_cast<bf16>(v[i])) compiles to element 0 for every i.
-  const bf16x8 qv = __builtin_bit_cast(bf16x8, qbits);
   float q[8];
+  if constexpr (KF32) {
+    const f32x4 qa = __builtin_bit_cast(f32x4, qbits), qb = __builtin_bit_cast(f32x4, qbits2);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) q[e] = (float)qv[e] * p.inv_scale;
+    for (int e = 0; e < 4; ++e) {
+      q[e] = qa[e] * p.inv_scale;
+      q[4 + e] = qb[e] * p.inv_scale;
+    }
+  } else {
+    const bf16x8 qv = __builtin_bit_cast(bf16x8, qbits);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = (float)qv[e] * p.inv_scale;
+  }
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float msum = 0.f;
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int slot = i * kRows + (int)row0;
-    const bf16x8 kv = __builtin_bit_cast(bf16x8, kr[i]);
     float part = 0.f;
+    if constexpr (KF32) {
+      const f32x4 ka = __builtin_bit_cast(f32x4, kr[i]), kb = __builtin_bit_cast(f32x4, kr2[i]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part += q[e] * (float)kv[e];
+      for (int e = 0; e < 4; ++e) part += q[e] * ka[e] + q[4 + e] * kb[e];
+    } else {
+      const bf16x8 kv = __builtin_bit_cast(bf16x8, kr[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += q[e] * (float)kv[e];
+    }
     part = row_sum8(part);
     const float tau = slot < live ? sigmoid_fast(part) : 0.f;
     if (p.tau.p && ch == 0 && slot < W)
@@ -134,7 +169,7 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   // form the dot, lanes 8-15 take its sigmoid through the row rotate and
   // scale their v chunk; the results meet the cache sums in LDS.
   __shared__ float sred[65];
-  if (self_key && wave == 1) {
+  if (!KF32 && self_key && wave == 1) {
     const bf16x8 kv = __builtin_bit_cast(bf16x8, knew);
     float part = 0.f;
 #pragma unroll
@@ -175,19 +210,23 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
       m += sred[64];
     }
     const float inv = decode_norm(p.flags, m, live + (self_key ? 1 : 0));
-    bf16* orow = (bf16*)p.out.p + n * p.out.s0 + h * p.out.s1;
-    orow[tid] = (bf16)(o * inv);
-  } else if (ai < 16) {
-    // append k_new / v_new at slot pos % W (8 lanes x 16 bytes each)
+    if constexpr (KF32) {
+      ((float*)p.out.p)[n * p.out.s0 + h * p.out.s1 + tid] = o * inv;
+    } else {
+      bf16* orow = (bf16*)p.out.p + n * p.out.s0 + h * p.out.s1;
+      orow[tid] = (bf16)(o * inv);
+    }
+  } else if (ai < kKChunks + 8) {
+    // append k_new / v_new at slot pos % W (16 bytes per lane)
     const int slot = pos % W;
-    if (ai < 8) {
-      bf16* dst = (bf16*)p.kc.p + n * p.kc.s0 + h * p.kc.s1 + (int64_t)slot * p.kc.s2;
-      *(u16x8*)(dst + 8 * ai) = knew;
+    if (ai < kKChunks) {
+      char* dst = (char*)p.kc.p + (n * p.kc.s0 + h * p.kc.s1 + (int64_t)slot * p.kc.s2) * kKBytes;
+      *(u16x8*)(dst + 16 * ai) = knew;
     } else {
       bf16* dst = (bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1 + (int64_t)slot * p.vc.s2;
-      *(u16x8*)(dst + 8 * (ai - 8)) = vnew;
+      *(u16x8*)(dst + 8 * (ai - kKChunks)) = vnew;
     }
-  } else if (ai == 16 && h == 0 && p.pos_out) {
+  } else if (ai == kKChunks + 8 && h == 0 && p.pos_out) {
     p.pos_out[n] = pos + 1;
   }
 }
@@ -250,8 +289,23 @@ __global__ __launch_bounds__(64) void decode_exact(DecodeParams p) {
   if (h == 0 && p.pos_out) p.pos_out[n] = pos + 1;
 }
 
-int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err) {
-  if (fast) {
+int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32) {
+  if (fast && kf32) {
+    // float32 q / K / out, bf16 V (D == 64, W <= 1024, no self key)
+    const dim3 grid((unsigned)(p.N * p.H));
+    if (p.W <= 32)
+      hipLaunchKernelGGL((decode_bf16_d64<4, 1, true>), grid, dim3(256), 0, st, p);
+    else if (p.W <= 64)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 1, true>), grid, dim3(512), 0, st, p);
+    else if (p.W <= 128)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 2, true>), grid, dim3(512), 0, st, p);
+    else if (p.W <= 256)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 4, true>), grid, dim3(512), 0, st, p);
+    else if (p.W <= 512)
+      hipLaunchKernelGGL((decode_bf16_d64<8, 8, true>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((decode_bf16_d64<8, 16, true>), grid, dim3(512), 0, st, p);
+  } else if (fast) {
     // fast requires D == 64, W <= 1024
     const dim3 grid((unsigned)(p.N * p.H));
     if (p.W <= 32)

@@ -78,7 +78,11 @@ struct AuxLossParams {
 // *err), -1 when no kernel exists for the request.
 int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
-int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err);
+// kf32 (with fast): float32 q / k_new / K cache / out and a bf16 V
+int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32 = false);
+// float32 Q / K / dOut with a bfloat16 V (local windows W <= 64, head dim 64);
+// phase 0 forward, 1 dQ, 2 dK / dV
+int launch_mixed(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);

@@ -33,7 +33,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from .ops import TensionDecodeCache, decode_step, rope
+from .ops import TensionDecodeCache, autocast_inputs, decode_step, rope
 
 
 class TensionKVCache:
@@ -63,9 +63,9 @@ class TensionKVCache:
         N, T, H, HD = k.shape
         layer = self.model.blocks[i].tension
         c = self.layers[i]
-        if c is None or c.k.dtype != k.dtype:
+        if c is None or c.k.dtype != k.dtype or c.v.dtype != v.dtype:
             c = TensionDecodeCache(N, H, HD, self.windows[i], dtype=k.dtype, device=k.device,
-                                   scale=layer.scale)
+                                   scale=layer.scale, v_dtype=v.dtype)
             self.layers[i] = c
         W = c.W
         s = max(0, T - W)
@@ -216,10 +216,14 @@ def _layer_step(layer, x: Tensor, cache: TensionDecodeCache, par: int, rot, taus
     if layer.rope_enabled:
         k = layer.wk(x).view(N, 1, H, HD)
         v = layer.wv(x).view(N, 1, H, HD)
-        q, k = rope(q, *rot), rope(k, *rot)
+        # promoted like the full forward's RoPE (model.py:75-81) unless fast_rope
+        out = torch.promote_types(q.dtype, rot[0].dtype) if layer.rope.promote else None
+        q, k = rope(q, *rot, out_dtype=out), rope(k, *rot, out_dtype=out)
     else:
         k, v = layer.wkv(x).view(N, 1, H, 2 * HD).split(HD, dim=-1)
     q, k, v = q[:, 0], k[:, 0], v[:, 0]
+    if layer.global_layer:  # the full forward's autocast inputs of the global block
+        q, k, v = autocast_inputs(q, k, v)
     pin, pout = cache.pos[par], cache.pos[1 - par]
     if layer.global_layer:
         out = decode_step(q, k, v, cache.k, cache.v, pin, pout, cache.scale, "mass", None, True)

@@ -18,11 +18,17 @@ initialisation, so a reference checkpoint's ``state_dict`` loads as is.
 Class, function and argument names follow the reference (``TensionConfig``,
 ``TensionLM``, the four aux losses of ``model.py:489-611``).
 
+Dtype flow: RoPE promotes like the reference's (``model.py:75-81``: a bf16
+projection times the float32 tables gives float32 Q / K under autocast), so
+the local layers see float32 Q / K with a bf16 V, which the op runs on its
+split-operand MFMA kernels; global layers under autocast take bf16 Q / K /
+V, as the reference's autocast einsum does (``model.py:219,230``).  With
+``TensionConfig.fast_rope`` the rotated Q / K stay in the projection's dtype
+instead (bf16 under autocast: the bf16 MFMA kernels, half the Q / K bytes).
+
 Differences, by design:
 * there is no CPU path (the kernels run on the GPU only);
-* under bf16 autocast the rotated Q/K stay bf16 (the reference promotes them
-  to float32, ``model.py:75-81``) so the tension op runs on the bf16 MFMA
-  kernels; the op itself accumulates in float32 either way;
+* ``fast_rope`` (default off) is an addition;
 * gradient checkpointing (``use_grad_checkpoint``) recomputes the block with
   ``torch.utils.checkpoint`` as the reference does.
 """
@@ -37,7 +43,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 from torch.utils.checkpoint import checkpoint
 
-from .ops import causal_tension, global_tension, rope
+from .ops import autocast_inputs, causal_tension, global_tension, rope
 
 
 @dataclass
@@ -56,6 +62,9 @@ class TensionConfig:
     use_rope: bool = False
     use_triton: bool = False  # selects the reference's Triton-path normalisation (see the layer)
     global_every: int = 0
+    # not in the reference: keep rotated Q / K in the projection's dtype
+    # instead of promoting them to the float32 tables' dtype (model.py:75-81)
+    fast_rope: bool = False
 
     @property
     def head_dim(self) -> int:
@@ -77,8 +86,9 @@ class RotaryEmbedding(nn.Module):
     """Half-split rotary embedding; theta_i = base^(-i/half), float32 cos/sin
     tables of max_seq_len rows (``model.py:54-81``)."""
 
-    def __init__(self, head_dim: int, max_seq_len: int, base: int = 10_000):
+    def __init__(self, head_dim: int, max_seq_len: int, base: int = 10_000, promote: bool = True):
         super().__init__()
+        self.promote = promote
         half = head_dim // 2
         # float32 throughout, as the reference builds its tables
         inv = 1.0 / (base ** (torch.arange(half, dtype=torch.float32) / half))
@@ -87,7 +97,9 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("sin", ang.sin(), persistent=False)
 
     def forward(self, x: Tensor, T: int, pos_offset: int = 0) -> Tensor:
-        return rope(x, self.cos, self.sin, pos_offset)
+        # the reference's x * cos - ... promotes to the wider of x and the tables
+        out = torch.promote_types(x.dtype, self.cos.dtype) if self.promote else None
+        return rope(x, self.cos, self.sin, pos_offset, out_dtype=out)
 
 
 class RMSNorm(nn.Module):
@@ -128,7 +140,7 @@ class MultiHeadCausalTensionLayer(nn.Module):
             self.wk = nn.Linear(D, D, bias=False)
             self.wv = nn.Linear(D, D, bias=False)
             self.wkv = None
-            self.rope = RotaryEmbedding(cfg.head_dim, cfg.max_seq_len)
+            self.rope = RotaryEmbedding(cfg.head_dim, cfg.max_seq_len, promote=not cfg.fast_rope)
         else:
             self.wkv = nn.Linear(D, 2 * D, bias=False)
             self.wk = self.wv = None
@@ -155,6 +167,8 @@ class MultiHeadCausalTensionLayer(nn.Module):
     def forward(self, x: Tensor, return_tensions: bool = False, tau_bias: Optional[Tensor] = None):
         B, T, D = x.shape
         q, k, v = self._qkv(x)
+        if self.global_layer:
+            q, k, v = autocast_inputs(q, k, v)
         if self.kv_sink is not None:
             self.kv_sink(k, v)
         if self.global_layer:
@@ -398,6 +412,9 @@ def _group_mats(groups, L: int, nrow: int, dev):
     return _GROUP_MATS[key]
 
 
+_AUX_DTYPES = (torch.float32, torch.bfloat16, torch.float16, torch.float64)
+
+
 class _AuxLossFn(torch.autograd.Function):
     """Diversity, consistency and entropy losses of every layer's tau in one
     HIP pass forward and one backward (tension_aux_loss_fwd / _bwd)."""
@@ -461,13 +478,15 @@ def tension_aux_losses(all_tensions: list, window_groups: Optional[dict] = None)
     """(tension_diversity_loss, constraint_consistency_loss,
     tension_entropy_loss) of the same taus, in one fused pass on the GPU
     when every tau has one [B, T, H, W] shape with W <= 64 (the model's
-    layers); otherwise the three functions above."""
+    layers; each layer in its own float dtype, e.g. the float32 tau of the
+    local layers beside the global layers' bf16 tau_local under autocast,
+    all read into float32); otherwise the three functions above."""
     if not all_tensions:
         z = torch.tensor(0.0)
         return z, z, z
     shape = tuple(all_tensions[0].shape)
     fused = (all_tensions[0].is_cuda and len(all_tensions) <= 32 and shape[-1] <= 64
-             and all(tuple(t.shape) == shape and t.dtype == all_tensions[0].dtype for t in all_tensions))
+             and all(tuple(t.shape) == shape and t.is_cuda and t.dtype in _AUX_DTYPES for t in all_tensions))
     if not fused:
         return (tension_diversity_loss(all_tensions, window_groups),
                 constraint_consistency_loss(all_tensions), tension_entropy_loss(all_tensions))

@@ -263,9 +263,9 @@ class TensionDecodeCache:
     swapped each step, so a captured HIP graph can replay steps)."""
 
     def __init__(self, N: int, H: int, D: int, W: int, dtype=torch.bfloat16,
-                 device="cuda", scale: Optional[float] = None):
+                 device="cuda", scale: Optional[float] = None, v_dtype=None):
         self.k = torch.zeros(N, H, W, D, dtype=dtype, device=device)
-        self.v = torch.zeros(N, H, W, D, dtype=dtype, device=device)
+        self.v = torch.zeros(N, H, W, D, dtype=v_dtype or dtype, device=device)
         self.pos = [torch.zeros(N, dtype=torch.int32, device=device),
                     torch.zeros(N, dtype=torch.int32, device=device)]
         self.cur = 0
@@ -281,6 +281,16 @@ class TensionDecodeCache:
                           include_self)
         self.cur = 1 - self.cur
         return (out, tau) if return_tau else out
+
+
+def autocast_inputs(*ts: Tensor):
+    """Under CUDA autocast, the tensors in the autocast dtype: the dtype the
+    reference's global block computes its einsums in (model.py:219,230);
+    unchanged otherwise."""
+    if ts[0].is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        return tuple(t.to(dt) for t in ts)
+    return ts
 
 
 # ----------------------------------------------------------------- RoPE

@@ -68,6 +68,29 @@ def test_fused_aux_losses_match_reference(dev, L, B, T, H, W, dtype, grouped):
         assert err <= tol * max(scale, 1e-12) + 1e-12, (err, scale)
 
 
+def test_fused_aux_losses_mixed_layer_dtypes(dev):
+    """fp32 taus of local layers beside bf16 tau_local of global layers (the
+    reference dtype flow under autocast): one fused pass, each layer read in
+    its own dtype, dTau returned in it."""
+    L, B, T, H, W = 6, 2, 300, 4, 64
+    taus = taus_of(99, L, B, T, H, W, torch.float32, dev)
+    taus = [t.to(torch.bfloat16) if l % 3 == 2 else t for l, t in enumerate(taus)]
+    groups = {W: [0, 1, 3, 4], 1024: [2, 5]}
+    a = [t.detach().float().requires_grad_(True) for t in taus]
+    b = [t.detach().clone().requires_grad_(True) for t in taus]
+    ra = reference(a, groups)
+    fb = M.tension_aux_losses(b, groups)
+    for x, y in zip(ra, fb):
+        assert abs(float(x) - float(y)) <= 1e-5 * max(1.0, abs(float(x))), (float(x), float(y))
+    sum(wi * x for wi, x in zip((0.7, 1.3, 2.1), ra)).backward()
+    sum(wi * y for wi, y in zip((0.7, 1.3, 2.1), fb)).backward()
+    for ga, gb, t in zip(a, b, taus):
+        assert gb.grad.dtype == t.dtype
+        ref = ga.grad.double()
+        tol = 1e-5 if t.dtype == torch.float32 else 1e-2
+        assert (gb.grad.double() - ref).abs().max().item() <= tol * ref.abs().max().item() + 1e-12
+
+
 def test_fused_aux_losses_in_the_model(dev):
     """return_all taus of a bf16 model: fused and reference losses give the
     same loss and the same parameter gradients (through the kernels' dTau)."""

@@ -81,6 +81,33 @@ def test_decode_count_matches_window_rows(dev, dtype, W, prefill):
             assert rel_l2(f64(out), ref[:, t]) <= 2e-2
 
 
+@pytest.mark.parametrize("W,prefill", [(64, 64), (64, 5), (256, 260), (100, 7), (1024, 1030), (32, 3)])
+@pytest.mark.parametrize("normalize", ["mass", "count"])
+def test_decode_fp32_qk_bf16_v(dev, W, prefill, normalize):
+    """The reference's autocast flow in generation: float32 (RoPE-promoted)
+    q / K cache with a bf16 V cache -- the float32-K fast kernel; out and tau
+    float32, held to max-abs 1e-5."""
+    from bozo_amd import TensionDecodeCache
+    N, H, D, S = 3, 4, 64, 6
+    L = prefill + S
+    q, k, v = seq_inputs(N, L, H, D, seed=W + prefill + 5)
+    v = v.to(torch.bfloat16)
+    cache = TensionDecodeCache(N, H, D, W, dtype=torch.float32, device=dev, v_dtype=torch.bfloat16)
+    for t in range(prefill):
+        cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev), normalize=normalize)
+    msg, tau = O.window_forward(f64(q), f64(k), f64(v), W, math.sqrt(D))
+    ref = O.normalize_mass(msg, tau)[0] if normalize == "mass" else O.normalize_count(msg, W)
+    for t in range(prefill, L):
+        out, tt = cache.step(q[:, t].to(dev), k[:, t].to(dev), v[:, t].to(dev), normalize=normalize,
+                             return_tau=True)
+        torch.cuda.synchronize()
+        assert out.dtype == torch.float32 and tt.dtype == torch.float32
+        assert max_abs(f64(out), ref[:, t]) <= 1e-5, (t, max_abs(f64(out), ref[:, t]))
+        assert max_abs(f64(tt), tau[:, t]) <= 1e-5
+    kd = cache.k[:, :, (L - 1) % W].cpu()
+    assert torch.equal(kd, k[:, L - 1])  # the append keeps float32 keys exactly
+
+
 @pytest.mark.parametrize("dtype,W,prefill", [
     (torch.bfloat16, 1024, 1000),  # fast path, 16 passes, nearly full
     (torch.bfloat16, 1024, 0),     # fast path, empty cache: the first rows are self only

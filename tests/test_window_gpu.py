@@ -319,18 +319,59 @@ def test_strided_views_like_wkv_split(dev):
     check_bf16(out, ref, "out")
 
 
-def test_mixed_dtypes_autocast_like(dev):
-    """Under autocast the reference feeds fp32 (RoPE'd) Q/K with bf16 V."""
-    inp = make_inputs(2, 96, 2, 64, seed=6, std=0.5)
-    inp["V"] = inp["V"].to(torch.bfloat16)
-    hip = hip_run(inp, 32, 8.0, dev, normalize="mass")
-    ref = oracle_run(inp, 32, 8.0, normalize="mass")
-    out, _, grads = hip
-    assert out.dtype == torch.float32 and grads[2].dtype == torch.bfloat16
-    check_fp32(out, ref[0], "out")
-    check_fp32(grads[0], ref[2][0], "dQ")
-    check_fp32(grads[1], ref[2][1], "dK")
+def check_mixed(hip, ref, tau_checked):
+    """The split-operand kernels carry every float32 operand as a bf16 pair
+    (about 16 significant bits, residual <= 2^-18 relative per term): the
+    float32 outputs (out, dQ, dK, tau) are held to max-abs 1e-5 relative to
+    max(1, |ref|max) -- absolute 1e-5 for normalised outputs and tau, 1e-5 of
+    the largest value for raw sums -- and the bf16 dV to 2e-2 relative L2."""
+    out, tau, grads = hip
+    assert out.dtype == torch.float32 and grads[0].dtype == torch.float32
+    assert grads[1].dtype == torch.float32 and grads[2].dtype == torch.bfloat16
+    scaled = lambda want: 1e-5 * max(1.0, float(np.max(np.abs(want))))  # noqa: E731
+    check_fp32(out, ref[0], "out", scaled(ref[0]))
+    check_fp32(grads[0], ref[2][0], "dQ", scaled(ref[2][0]))
+    check_fp32(grads[1], ref[2][1], "dK", scaled(ref[2][1]))
     check_bf16(grads[2], ref[2][2], "dV")
+    if tau_checked:
+        assert tau.dtype == torch.float32
+        check_fp32(tau, ref[1], "tau")
+
+
+def mixed_inputs(B, T, H, seed, W=None, dtau_std=None, bias_std=None):
+    """The reference's autocast flow: fp32 RoPE'd Q / K (model.py:75-81), bf16 V."""
+    inp = make_inputs(B, T, H, 64, seed=seed, std=0.5, W=W, dtau_std=dtau_std, bias_std=bias_std,
+                      bias_shape=(B, T, W) if bias_std else None)
+    inp["V"] = inp["V"].to(torch.bfloat16)
+    return inp
+
+
+def test_mixed_dtypes_autocast_like(dev):
+    """Under autocast the reference feeds fp32 (RoPE'd) Q/K with bf16 V: the
+    split-operand MFMA kernels (W <= 64, head dim 64)."""
+    inp = mixed_inputs(2, 96, 2, seed=6)
+    check_mixed(hip_run(inp, 32, 8.0, dev, normalize="mass"), oracle_run(inp, 32, 8.0, normalize="mass"), False)
+
+
+@pytest.mark.parametrize("normalize", [None, "mass", "count"])
+def test_mixed_dtypes_117m_geometry(dev, normalize):
+    """The reference's autocast dtype flow at the 117M layer shape (B8 H12
+    T1024 W64): fp32 Q / K, bf16 V, tau emitted (fp32) and a gradient
+    through it."""
+    inp = mixed_inputs(8, 1024, 12, seed=21, W=64, dtau_std=0.1)
+    print(f"[mixed 117m] normalize={normalize}", flush=True)
+    hip = hip_run(inp, 64, 8.0, dev, normalize=normalize, return_tau=True, use_dtau=True)
+    ref = oracle_run(inp, 64, 8.0, normalize=normalize, use_dtau=True)
+    check_mixed(hip, ref, True)
+
+
+@pytest.mark.parametrize("T,W", [(1, 4), (70, 64), (100, 17), (130, 64), (64, 1)])
+def test_mixed_dtypes_band_edges_bias(dev, T, W):
+    """Ragged T, W < 64, one-key windows and the bias on the mixed kernels."""
+    inp = mixed_inputs(2, T, 3, seed=T + W, W=W, dtau_std=0.1, bias_std=0.5)
+    hip = hip_run(inp, W, 8.0, dev, normalize="mass", return_tau=True, use_bias=True, use_dtau=True)
+    ref = oracle_run(inp, W, 8.0, normalize="mass", use_bias=True, use_dtau=True)
+    check_mixed(hip, ref, True)
 
 
 def test_empty_batch(dev):
