@@ -706,7 +706,7 @@ def bench_decode(dev, reps):
             "traffic": traffic}
 
 
-def bench_model(dev, steps, warmup, aux, fast_rope=False):
+def bench_model(dev, steps, warmup, aux, fast_rope=False, compiled=False):
     """Config 5: one TensionLM-117M training step (random init, bf16
     autocast, AdamW as train.py:894-902, clip 1.0) on B8 x T1024 token ids
     ~ U[0, 32768).  ``aux``: the reference default, return_all with tau
@@ -714,7 +714,11 @@ def bench_model(dev, steps, warmup, aux, fast_rope=False):
     0.02, 0, 0 as train.py:135-140 -- all four are evaluated there too; the
     three tau losses in the fused kernels); otherwise CE only (local layers
     on the valid-count path, no tau).  ``fast_rope``: rotated Q / K stay bf16
-    (the bf16 kernels) instead of the reference's float32 promotion."""
+    (the bf16 kernels) instead of the reference's float32 promotion.
+    ``compiled``: the model under torch.compile(dynamic=False,
+    mode="default") as train.py:776-780 runs it (the tension kernels enter
+    the graph as the bozo:: custom operators); compilation happens in the
+    warmup steps."""
     import gc
     import torch.nn.functional as F
     from bozo_amd import model as M
@@ -724,6 +728,11 @@ def bench_model(dev, steps, warmup, aux, fast_rope=False):
     torch.manual_seed(4)
     m = M.TensionLM(cfg).to(dev).train()
     opt = M.configure_adamw(m, lr=3e-4, weight_decay=0.1, fused=True)
+    fwd = m
+    if compiled:
+        torch._dynamo.reset()
+        fwd = torch.compile(m, dynamic=False, mode="default")
+    t_c = time.perf_counter()
     B, T = 8, 1024
     g = torch.Generator(device=dev).manual_seed(4)
     ids = torch.randint(0, cfg.vocab_size, (B, T + 1), device=dev, generator=g)
@@ -732,9 +741,9 @@ def bench_model(dev, steps, warmup, aux, fast_rope=False):
     def step():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             if aux:
-                logits, hidden, taus = m(inputs, return_all=True)
+                logits, hidden, taus = fwd(inputs, return_all=True)
             else:
-                logits = m(inputs)
+                logits = fwd(inputs)
             loss = F.cross_entropy(logits.reshape(-1, cfg.vocab_size), targets.reshape(-1))
             if aux:  # all four computed, as the reference does; the tau ones fused
                 div, cons, ent = M.tension_aux_losses(taus, m.window_groups)
@@ -749,9 +758,10 @@ def bench_model(dev, steps, warmup, aux, fast_rope=False):
     for _ in range(warmup):
         loss = step()
     torch.cuda.synchronize()
+    warm_s = time.perf_counter() - t_c
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    torch.cuda.nvtx.range_push("model:" + ("aux" if aux else "ce"))  # a --summarize phase
+    torch.cuda.nvtx.range_push("model:" + ("aux" if aux else "ce") + (":compiled" if compiled else ""))
     e0.record()
     for _ in range(steps):
         loss = step()
@@ -762,11 +772,15 @@ def bench_model(dev, steps, warmup, aux, fast_rope=False):
     ms = e0.elapsed_time(e1) / steps
     res = {"config": "TensionLM-117M training step B8 T1024 bf16 autocast AdamW (config 5), "
                      + ("aux losses + tau (reference default)" if aux else "CE only")
-                     + (", bf16 Q/K (fast_rope)" if fast_rope else ", fp32 RoPE'd Q/K (reference dtype flow)"),
+                     + (", bf16 Q/K (fast_rope)" if fast_rope else ", fp32 RoPE'd Q/K (reference dtype flow)")
+                     + (", torch.compile (train.py:776-780)" if compiled else ", eager"),
            "ms_per_step": round(ms, 3), "wall_ms_per_step": round(wall, 3),
+           "warmup_s": round(warm_s, 1),
            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "params": m.num_params,
            "final_loss": round(float(loss.item()), 4)}
-    del m, opt
+    del m, opt, fwd
+    if compiled:
+        torch._dynamo.reset()
     torch.cuda.empty_cache()
     return res
 
@@ -960,9 +974,12 @@ def main():
         print(json.dumps(bench_bias(dev)), flush=True)
         return
     if args.model_only:
-        for fast in (False, True):
-            for aux in (False, True):
-                print(json.dumps(bench_model(dev, args.steps, args.warmup, aux, fast)), flush=True)
+        for compiled in (False, True):
+            for fast in (False, True):
+                for aux in (False, True):
+                    log(f"[bench] config 5, aux={aux}, fast_rope={fast}, compiled={compiled} ...")
+                    print(json.dumps(bench_model(dev, args.steps, args.warmup, aux, fast, compiled)),
+                          flush=True)
         if not args.no_cpu:
             print(json.dumps({"cpu_model_baselines": cpu_model_baselines(args.cpu_seconds)}), flush=True)
         return
@@ -973,10 +990,11 @@ def main():
     log("[bench] decode (config 4) ...")
     others.append(bench_decode(dev, 4))
     log(f"[bench] {others[-1]}")
-    for fast in (False, True):
+    for fast, compiled in ((False, False), (True, False), (False, True)):
         for aux in (False, True):
-            log(f"[bench] TensionLM-117M training step (config 5, aux={aux}, fast_rope={fast}) ...")
-            others.append(bench_model(dev, 10, 5, aux, fast))
+            log(f"[bench] TensionLM-117M training step (config 5, aux={aux}, fast_rope={fast}, "
+                f"compiled={compiled}) ...")
+            others.append(bench_model(dev, 10, 5, aux, fast, compiled))
             log(f"[bench] {others[-1]}")
     log("[bench] tau export reductions ...")
     others.append(bench_export(dev))

@@ -79,6 +79,12 @@ def _ptr(t: Optional[Tensor]):
     return None if t is None else t.data_ptr()
 
 
+def _grads_like(*ts: Tensor):
+    """Fresh contiguous gradient buffers (the layout the fake kernels of the
+    registered operators report, whatever the inputs' strides)."""
+    return tuple(torch.empty(t.shape, dtype=t.dtype, device=t.device) for t in ts)
+
+
 # ----------------------------------------------------------------- local window
 
 def _window_fwd(Q, K, V, W, scale, tau, bias, flags, mass):
@@ -114,25 +120,26 @@ class _CausalTensionFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grads):
         Q, K, V, Bias = ctx.saved_tensors
-        B, T, H, D = Q.shape
-        dOut = _rows(grads[0])
-        dTau = _rows(grads[1]) if ctx.return_tau else None
-        if dOut is None:
-            dOut = torch.zeros_like(Q)
-        dQ = torch.empty_like(Q)
-        dK = torch.empty_like(K)
-        dV = torch.empty_like(V)
-        lib = L.lib()
-        ws = _ws(lib.tension_window_bwd_workspace(B, T, H, _acc_code(Q, K, V), ctx.flags), Q.device)
-        with torch.cuda.device(Q.device):
-            L.check(lib.tension_window_bwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias),
-                L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.W,
-                float(ctx.scale), ctx.flags, _stream(Q)), "tension_window_bwd")
+        dTau = grads[1] if ctx.return_tau else None
+        dQ, dK, dV = _window_bwd(Q, K, V, grads[0], dTau, Bias, ctx.W, ctx.scale, ctx.flags)
         return dQ, dK, dV, None, None, None, None, None
 
 
-@torch._dynamo.disable
+def _window_bwd(Q, K, V, dOut, dTau, Bias, W, scale, flags):
+    B, T, H, D = Q.shape
+    dOut = _rows(dOut) if dOut is not None else torch.zeros_like(Q)
+    dTau = _rows(dTau)
+    dQ, dK, dV = _grads_like(Q, K, V)
+    lib = L.lib()
+    ws = _ws(lib.tension_window_bwd_workspace(B, T, H, _acc_code(Q, K, V), flags), Q.device)
+    with torch.cuda.device(Q.device):
+        L.check(lib.tension_window_bwd(
+            L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias),
+            L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, W,
+            float(scale), flags, _stream(Q)), "tension_window_bwd")
+    return dQ, dK, dV
+
+
 def causal_tension(Q: Tensor, K: Tensor, V: Tensor, window: int, scale: float,
                    return_tau: bool = False, bias: Optional[Tensor] = None, *,
                    normalize: Optional[str] = None):
@@ -158,6 +165,11 @@ def causal_tension(Q: Tensor, K: Tensor, V: Tensor, window: int, scale: float,
         raise ValueError(f"normalize must be one of {list(_NORMS)}")
     if int(window) < 1:
         raise ValueError("window must be >= 1")
+    if torch.compiler.is_compiling():  # the registered op, which torch.compile traces through
+        Bias = _side(bias, Q)
+        out, tau = torch.ops.bozo.window_fwd(Q, K, V, int(window), float(scale), bool(return_tau), Bias,
+                                             _NORMS[normalize])
+        return (out, tau) if return_tau else out
     return _CausalTensionFn.apply(_rows(Q), _rows(K), _rows(V), int(window), float(scale),
                                   bool(return_tau), bias, normalize)
 
@@ -175,15 +187,7 @@ class _GlobalTensionFn(torch.autograd.Function):
         if Bias is not None and tuple(Bias.shape) != (B, T, T):
             raise ValueError(f"global bias must be [B, T, T]=[{B}, {T}, {T}], got {tuple(Bias.shape)}")
         Wl = 0 if W_local is None else min(int(W_local), T)
-        tl = torch.empty(B, T, H, Wl, dtype=Q.dtype, device=Q.device) if Wl > 0 else None
-        out = torch.empty_like(Q)
-        # the tau mass per query, kept with the output so the backward gets
-        # its per-query coefficients from these rows (no band recompute)
-        mass = torch.empty(B, T, H, dtype=torch.float32, device=Q.device)
-        with torch.cuda.device(Q.device):
-            L.check(L.lib().tension_global_fwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), L.buf(mass),
-                B, T, H, D, Wl, float(scale), 0, _stream(Q)), "tension_global_fwd")
+        out, tl, mass = _global_fwd(Q, K, V, scale, Bias, Wl)
         ctx.save_for_backward(Q, K, V, Bias, out, mass)
         ctx.scale, ctx.Wl = scale, Wl
         if tl is not None:
@@ -193,23 +197,41 @@ class _GlobalTensionFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grads):
         Q, K, V, Bias, out, mass = ctx.saved_tensors
-        B, T, H, D = Q.shape
-        dOut = _rows(grads[0])
-        if dOut is None:
-            dOut = torch.zeros_like(Q)
-        dTl = _rows(grads[1]) if ctx.Wl > 0 else None
-        dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
-        lib = L.lib()
-        ws = _ws(lib.tension_global_bwd_workspace(B, T, H, _acc_code(Q, K, V), 0), Q.device)
-        with torch.cuda.device(Q.device):
-            L.check(lib.tension_global_bwd(
-                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias), L.buf(out),
-                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, ctx.Wl,
-                float(ctx.scale), 0, _stream(Q)), "tension_global_bwd")
+        dTl = grads[1] if ctx.Wl > 0 else None
+        dQ, dK, dV = _global_bwd(Q, K, V, grads[0], dTl, Bias, out, mass, ctx.Wl, ctx.scale)
         return dQ, dK, dV, None, None, None
 
 
-@torch._dynamo.disable
+def _global_fwd(Q, K, V, scale, Bias, Wl):
+    """out, tau_local (None when Wl is 0) and the tau mass of the global block."""
+    B, T, H, D = Q.shape
+    tl = torch.empty(B, T, H, Wl, dtype=Q.dtype, device=Q.device) if Wl > 0 else None
+    out = torch.empty_like(Q)
+    # the tau mass per query, kept with the output so the backward gets
+    # its per-query coefficients from these rows (no band recompute)
+    mass = torch.empty(B, T, H, dtype=torch.float32, device=Q.device)
+    with torch.cuda.device(Q.device):
+        L.check(L.lib().tension_global_fwd(
+            L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), L.buf(mass),
+            B, T, H, D, Wl, float(scale), 0, _stream(Q)), "tension_global_fwd")
+    return out, tl, mass
+
+
+def _global_bwd(Q, K, V, dOut, dTl, Bias, out, mass, Wl, scale):
+    B, T, H, D = Q.shape
+    dOut = _rows(dOut) if dOut is not None else torch.zeros_like(Q)
+    dTl = _rows(dTl) if Wl > 0 else None
+    dQ, dK, dV = _grads_like(Q, K, V)
+    lib = L.lib()
+    ws = _ws(lib.tension_global_bwd_workspace(B, T, H, _acc_code(Q, K, V), 0), Q.device)
+    with torch.cuda.device(Q.device):
+        L.check(lib.tension_global_bwd(
+            L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTl), L.buf(Bias), L.buf(out),
+            L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, Wl,
+            float(scale), 0, _stream(Q)), "tension_global_bwd")
+    return dQ, dK, dV
+
+
 def global_tension(Q: Tensor, K: Tensor, V: Tensor, scale: float,
                    bias: Optional[Tensor] = None, W_local: Optional[int] = None):
     """Global layer of the reference (model.py:217-238) as one fused op.
@@ -221,6 +243,14 @@ def global_tension(Q: Tensor, K: Tensor, V: Tensor, scale: float,
     _on_gpu(Q, K, V, bias)
     if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
         raise ValueError("Q, K, V must share one [B, T, H, HD] shape")
+    if torch.compiler.is_compiling():  # the registered op, which torch.compile traces through
+        B, T = Q.shape[:2]
+        Bias = _side(bias, Q)
+        if Bias is not None and tuple(Bias.shape) != (B, T, T):
+            raise ValueError(f"global bias must be [B, T, T]=[{B}, {T}, {T}], got {tuple(Bias.shape)}")
+        Wl = 0 if W_local is None else min(int(W_local), T)
+        out, tl, _ = torch.ops.bozo.global_fwd(Q, K, V, float(scale), Bias, Wl)
+        return (out, tl) if Wl > 0 else out
     return _GlobalTensionFn.apply(_rows(Q), _rows(K), _rows(V), float(scale), bias, W_local)
 
 
@@ -332,4 +362,135 @@ def rope(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int = 0,
     T, half = x.shape[1], x.shape[-1] // 2
     if cos.shape[-1] != half or cos.shape[0] < pos_offset + T or sin.shape != cos.shape:
         raise ValueError("cos/sin tables do not cover the requested positions")
+    if torch.compiler.is_compiling():  # the registered op, which torch.compile traces through
+        return torch.ops.bozo.rope(x, cos.contiguous(), sin.contiguous(), int(pos_offset),
+                                   out_dtype or x.dtype, 0)
     return _RopeFn.apply(_rows(x), cos.contiguous(), sin.contiguous(), int(pos_offset), out_dtype)
+
+
+# ----------------------------------------------------------------- torch.library registration
+#
+# The same kernels as custom operators (bozo::window_fwd / window_bwd,
+# global_fwd / global_bwd, rope) with fake-tensor shape functions and
+# autograd formulas, so torch.compile traces a model through them without a
+# graph break (the reference compiles its model, train.py:776-780).  The
+# public functions call them while torch.compile traces and the autograd
+# Functions above in eager mode.
+
+@torch.library.custom_op("bozo::window_fwd", mutates_args=(), device_types="cuda")
+def _op_window_fwd(Q: Tensor, K: Tensor, V: Tensor, window: int, scale: float, return_tau: bool,
+                   bias: Optional[Tensor], flags: int) -> tuple[Tensor, Tensor]:
+    B, T, H, _ = Q.shape
+    if bias is not None and tuple(bias.shape) != (B, T, window):
+        raise ValueError(f"bias must be [B, T, W]=[{B}, {T}, {window}], got {tuple(bias.shape)}")
+    Q, K, V = _rows(Q), _rows(K), _rows(V)
+    tau = torch.empty(B, T, H, window, dtype=Q.dtype, device=Q.device) if return_tau else Q.new_empty(0)
+    out = _window_fwd(Q, K, V, window, scale, tau if return_tau else None, bias, flags, None)
+    return out, tau
+
+
+@_op_window_fwd.register_fake
+def _(Q, K, V, window, scale, return_tau, bias, flags):
+    B, T, H, D = Q.shape
+    tau = Q.new_empty((B, T, H, window)) if return_tau else Q.new_empty(0)
+    return Q.new_empty((B, T, H, D)), tau
+
+
+@torch.library.custom_op("bozo::window_bwd", mutates_args=(), device_types="cuda")
+def _op_window_bwd(Q: Tensor, K: Tensor, V: Tensor, dOut: Tensor, dTau: Optional[Tensor],
+                   bias: Optional[Tensor], window: int, scale: float, flags: int) -> tuple[Tensor, Tensor, Tensor]:
+    return _window_bwd(_rows(Q), _rows(K), _rows(V), dOut, dTau, bias, window, scale, flags)
+
+
+@_op_window_bwd.register_fake
+def _(Q, K, V, dOut, dTau, bias, window, scale, flags):
+    return _grads_like(Q, K, V)
+
+
+def _window_setup(ctx, inputs, output):
+    Q, K, V, window, scale, return_tau, bias, flags = inputs
+    ctx.save_for_backward(Q, K, V, bias)
+    ctx.window, ctx.scale, ctx.return_tau, ctx.flags = window, scale, return_tau, flags
+
+
+def _window_grad(ctx, d_out, d_tau):
+    Q, K, V, bias = ctx.saved_tensors
+    d_out = d_out if d_out is not None else torch.zeros_like(Q)
+    dQ, dK, dV = torch.ops.bozo.window_bwd(Q, K, V, d_out, d_tau if ctx.return_tau else None, bias,
+                                           ctx.window, ctx.scale, ctx.flags)
+    return dQ, dK, dV, None, None, None, None, None
+
+
+_op_window_fwd.register_autograd(_window_grad, setup_context=_window_setup)
+
+
+@torch.library.custom_op("bozo::global_fwd", mutates_args=(), device_types="cuda")
+def _op_global_fwd(Q: Tensor, K: Tensor, V: Tensor, scale: float, bias: Optional[Tensor],
+                   Wl: int) -> tuple[Tensor, Tensor, Tensor]:
+    out, tl, mass = _global_fwd(_rows(Q), _rows(K), _rows(V), scale, bias, Wl)
+    return out, (tl if tl is not None else Q.new_empty(0)), mass
+
+
+@_op_global_fwd.register_fake
+def _(Q, K, V, scale, bias, Wl):
+    B, T, H, D = Q.shape
+    tl = Q.new_empty((B, T, H, Wl)) if Wl > 0 else Q.new_empty(0)
+    return Q.new_empty((B, T, H, D)), tl, Q.new_empty((B, T, H), dtype=torch.float32)
+
+
+@torch.library.custom_op("bozo::global_bwd", mutates_args=(), device_types="cuda")
+def _op_global_bwd(Q: Tensor, K: Tensor, V: Tensor, dOut: Tensor, dTl: Optional[Tensor],
+                   bias: Optional[Tensor], out: Tensor, mass: Tensor, Wl: int,
+                   scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    return _global_bwd(_rows(Q), _rows(K), _rows(V), dOut, dTl, bias, out, mass, Wl, scale)
+
+
+@_op_global_bwd.register_fake
+def _(Q, K, V, dOut, dTl, bias, out, mass, Wl, scale):
+    return _grads_like(Q, K, V)
+
+
+def _global_setup(ctx, inputs, output):
+    Q, K, V, scale, bias, Wl = inputs
+    ctx.save_for_backward(Q, K, V, bias, output[0], output[2])
+    ctx.scale, ctx.Wl = scale, Wl
+
+
+def _global_grad(ctx, d_out, d_tl, d_mass):
+    Q, K, V, bias, out, mass = ctx.saved_tensors
+    d_out = d_out if d_out is not None else torch.zeros_like(Q)
+    dQ, dK, dV = torch.ops.bozo.global_bwd(Q, K, V, d_out, d_tl if ctx.Wl > 0 else None, bias, out, mass,
+                                           ctx.Wl, ctx.scale)
+    return dQ, dK, dV, None, None, None
+
+
+_op_global_fwd.register_autograd(_global_grad, setup_context=_global_setup)
+
+
+@torch.library.custom_op("bozo::rope", mutates_args=(), device_types="cuda")
+def _op_rope(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, out_dtype: torch.dtype,
+             inverse: int) -> Tensor:
+    x = _rows(x)
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    _rope_call(x, y, cos, sin, pos_offset, inverse)
+    return y
+
+
+@_op_rope.register_fake
+def _(x, cos, sin, pos_offset, out_dtype, inverse):
+    return torch.empty(x.shape, dtype=out_dtype, device=x.device)
+
+
+def _rope_setup(ctx, inputs, output):
+    x, cos, sin, pos_offset, out_dtype, inverse = inputs
+    ctx.save_for_backward(cos, sin)
+    ctx.pos_offset, ctx.in_dtype, ctx.inverse = pos_offset, x.dtype, inverse
+
+
+def _rope_grad(ctx, dy):
+    cos, sin = ctx.saved_tensors
+    return (torch.ops.bozo.rope(dy, cos, sin, ctx.pos_offset, ctx.in_dtype, 1 - ctx.inverse),
+            None, None, None, None, None)
+
+
+_op_rope.register_autograd(_rope_grad, setup_context=_rope_setup)
