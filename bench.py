@@ -448,7 +448,8 @@ def bench_window(args, dev):
 
 def profile_kernels(n, dev):
     """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
-    of each band kernel on rotated config-2 sets, n config-4 decode steps
+    of each band kernel on rotated config-2 sets (bf16, then fp32 Q / K with
+    bf16 V), n config-4 decode steps
     over 4 rotated caches and n config-3 global forward + backward calls, then
     a plain device copy of
     known size (256 MiB read + 256 MiB written) whose FETCH_SIZE/WRITE_SIZE
@@ -461,7 +462,18 @@ def profile_kernels(n, dev):
         for i in range(n):
             fns[i % NSETS][0][name]()
         torch.cuda.synchronize()
-    del fns, sets
+    del fns
+    # the reference's autocast dtype flow: fp32 (RoPE'd) Q / K, bf16 V, fp32
+    # out / dOut (the split-operand kernels mx_fwd / mx_dq / mx_dkv)
+    mixed = [dict(Q=s["Q"].detach().float(), K=s["K"].detach().float(), V=s["V"].detach(),
+                  dO=s["dO"].float()) for s in sets[:2]]
+    del sets
+    fns = [kernel_fns(s, W, math.sqrt(D), L.NORM_MASS) for s in mixed]
+    for name in ("fwd", "dq", "dkv"):
+        for i in range(n):
+            fns[i % 2][0][name]()
+        torch.cuda.synchronize()
+    del fns, mixed
     # config-4 decode steps over 4 rotated caches, fresh q / k / v per step
     from bozo_amd import TensionDecodeCache
     N, Hd, Wd, NC = 64, 16, 256, 4
@@ -616,38 +628,92 @@ def summarize(paths):
                 print(f"| {n} | {r / 1e6:.2f} | {w / 1e6:.2f} | {(r + w) / 1e6:.2f} |")
 
 
-def measure_traffic(n=16, timeout=240):
-    """HBM bytes per launch, measured now: two rocprofv3 --pmc passes
-    (FETCH_SIZE, then WRITE_SIZE) over this script's --profile-kernels
-    driver, run as child processes on the same GPU, calibrated by the
-    driver's 256 MiB device copy.  Returns ({kernel: bytes}, note)."""
+def rocprof_passes(passes, n=16, timeout=240):
+    """Run this script's --profile-kernels driver under rocprofv3 once per
+    pass, as child processes on the same GPU: a pass is a tuple of counters
+    (one --pmc run; each run stays within the per-block counter limits) or
+    None (a --kernel-trace run).  Returns (durations, counters, error): the
+    parsed results of _collect, or the reason nothing was measured."""
     import shutil
     import subprocess
     import tempfile
     exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
     if not os.path.exists(exe):
-        return {}, "rocprofv3 not found: traffic not measured"
+        return [], {}, "rocprofv3 not found"
     tmp = tempfile.mkdtemp(prefix="bench_pmc_", dir="/tmp")
     env = dict(os.environ, TMPDIR="/tmp")
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        out = os.path.join(tmp, counter)
-        cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--", sys.executable, os.path.abspath(__file__),
-               "--profile-kernels", str(n)]
+    for i, counters in enumerate(passes):
+        what = "--pmc " + " ".join(counters) if counters else "--kernel-trace"
+        cmd = [exe, *what.split(), "-d", os.path.join(tmp, f"pass{i}"), "-o", "run", "--",
+               sys.executable, os.path.abspath(__file__), "--profile-kernels", str(n)]
+        log(f"[bench] rocprofv3 {what} over --profile-kernels {n} ...")
         try:
             r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, env=env, cwd=ROOT)
         except subprocess.TimeoutExpired:
-            return {}, f"rocprofv3 --pmc {counter} timed out: traffic not measured"
+            return [], {}, f"rocprofv3 {what} timed out"
         # rocprofv3 itself may end with a segmentation fault after the program
         # finished and its results are whole; the results decide
         if r.returncode not in (0, -11, 139) or "profile-kernels:" not in (r.stdout + r.stderr):
-            return {}, f"rocprofv3 --pmc {counter} failed (rc {r.returncode}): traffic not measured"
-    _, counters = _collect([tmp])
+            return [], {}, f"rocprofv3 {what} failed (rc {r.returncode})"
+    durations, counters = _collect([tmp])
+    return durations, counters, None
+
+
+TRAFFIC_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",))
+UTIL_PASS = ("MfmaUtil", "VALUBusy")  # SQ_VALU_MFMA_BUSY_CYCLES, SQ_ACTIVE_INST_VALU, GRBM_GUI_ACTIVE
+
+
+def measure_traffic(n=16):
+    """HBM bytes per launch and MFMA / VALU busy %, measured now: rocprofv3
+    --pmc passes (FETCH_SIZE, WRITE_SIZE, MfmaUtil + VALUBusy) over the
+    --profile-kernels driver, the byte counters calibrated by the driver's
+    256 MiB device copy.  Returns ({kernel: bytes}, {kernel: (mfma %, valu %)},
+    note)."""
+    _, counters, err = rocprof_passes(TRAFFIC_PASSES + (UTIL_PASS,), n)
+    if err:
+        return {}, {}, err + ": traffic not measured"
     traffic, cal = hbm_traffic(counters)
     if not traffic:
-        return {}, "no calibrated FETCH_SIZE / WRITE_SIZE readings: traffic not measured"
-    return ({k: int(r + w) for k, (r, w) in traffic.items()},
-            f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE in this run, {n} launches per kernel, "
-            f"copy-calibrated x{cal[0]:.3f} / x{cal[1]:.3f}")
+        return {}, {}, "no calibrated FETCH_SIZE / WRITE_SIZE readings: traffic not measured"
+    util = {k: (round(v, 1), round(counters.get("VALUBusy", {}).get(k, (float("nan"),))[0], 1))
+            for k, (v, _) in counters.get("MfmaUtil", {}).items() if "tension::" in k}
+    return ({k: int(r + w) for k, (r, w) in traffic.items()}, util,
+            f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE / MfmaUtil+VALUBusy in this run, {n} launches per "
+            f"kernel, bytes copy-calibrated x{cal[0]:.3f} / x{cal[1]:.3f}")
+
+
+def kernel_counters(n=16):
+    """Markdown table per tension kernel of the --profile-kernels driver:
+    rocprofv3 kernel-trace mean duration, MFMA busy % (MfmaUtil: MFMA busy
+    cycles over all SIMDs' active cycles), VALU busy %, copy-calibrated HBM
+    traffic and GB/s over the 8 TB/s peak."""
+    import statistics
+    passes = (None,) + TRAFFIC_PASSES + (UTIL_PASS,)
+    durations, counters, err = rocprof_passes(passes, n)
+    if err:
+        print(f"kernel counters not measured: {err}")
+        return
+    dur = {}
+    for _, per in durations:
+        for _, by in per:
+            for k, d in by.items():
+                dur.setdefault(k, []).extend(d)
+    traffic, cal = hbm_traffic(counters)
+    get = lambda cn, k: counters.get(cn, {}).get(k, (float("nan"), 0))[0]  # noqa: E731
+    print(f"{n} launches per kernel; bytes calibrated x{cal[0]:.3f} (FETCH_SIZE) / x{cal[1]:.3f} "
+          "(WRITE_SIZE) against the driver's 256 MiB copy\n")
+    print("| kernel | launches | mean us | MFMA busy % | VALU busy % | HBM MB (read+write) | HBM GB/s "
+          "| of 8 TB/s |")
+    print("|---|---|---|---|---|---|---|---|")
+    for k in sorted(dur, key=lambda k: -statistics.mean(dur[k])):
+        if "tension::" not in k:
+            continue
+        us = statistics.mean(dur[k])
+        rw = traffic.get(k)
+        mb = (rw[0] + rw[1]) / 1e6 if rw else float("nan")
+        gbs = mb * 1e6 / (us * 1e-6) / 1e9
+        print(f"| {k} | {len(dur[k])} | {us:.2f} | {get('MfmaUtil', k):.1f} | {get('VALUBusy', k):.1f} "
+              f"| {mb:.2f} | {gbs:.0f} | {gbs / HBM_PEAK_GBS:.1%} |")
 
 
 def bench_global(dev, steps, warmup):
@@ -943,6 +1009,9 @@ def main():
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes that measure HBM traffic")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--kernel-counters", type=int, default=0, metavar="N",
+                    help="per-kernel table of duration, MFMA / VALU busy %%, counted MFMA TFLOP/s and HBM "
+                         "traffic from rocprofv3 passes over --profile-kernels N")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                     help="only launch each band kernel N times (counter collection)")
     ap.add_argument("--summarize", metavar="PATH", nargs="+",
@@ -967,6 +1036,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.profile_kernels:
         profile_kernels(args.profile_kernels, dev)
+        return
+    if args.kernel_counters:
+        kernel_counters(args.kernel_counters)
         return
     if args.generation_only:
         print(json.dumps(bench_generation(dev)), flush=True)
@@ -1008,8 +1080,9 @@ def main():
     result["other_configs"] = others
     if not args.no_traffic:
         log("[bench] HBM traffic: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes ...")
-        traffic, note = measure_traffic()
+        traffic, util, note = measure_traffic()
         pick = lambda key: next((v for k, v in traffic.items() if key in k), None)  # noqa: E731
+        busy = lambda key: next((v for k, v in util.items() if key in k), None)  # noqa: E731
         result["roofline"]["traffic"] = pick({"mfma_bwd_fused": "mfma_bwd_fused<1, false, false, true>",
                                               "mfma_fwd_ring": "mfma_fwd_ring<1, false, false, true>"}
                                              [result["roofline"]["kernel"]])
@@ -1017,12 +1090,14 @@ def main():
         for name, key in (("fwd", "mfma_fwd_ring<1, false, false, true>"),
                           ("bwd", "mfma_bwd_fused<1, false, false, true>")):
             result["step"]["kernels"][name]["traffic"] = pick(key)
+            result["step"]["kernels"][name]["mfma_valu_busy_pct"] = busy(key)
         for o in others:
             if o["config"].startswith("decode"):
                 o["traffic"] = pick("decode_bf16_d64")
             if o["config"].startswith("global block"):
                 o["traffic"] = {k.split("::")[-1]: v for k, v in traffic.items()
                                 if "gl_" in k or "coef_from_out" in k} or None
+                o["mfma_valu_busy_pct"] = {k.split("::")[-1]: v for k, v in util.items() if "gl_" in k} or None
         log(f"[bench] traffic: {note}; {result['roofline']['traffic']} bytes per dominant launch")
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
