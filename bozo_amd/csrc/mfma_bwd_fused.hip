@@ -23,6 +23,18 @@
 // The next step's K/V block, Q/dO tile and Q/dO fragments are loaded into
 // registers at the start of a step and stored to LDS behind the barriers.
 //
+// Runs alternate direction: even runs step t = tA .. tB-1 and then the halo
+// tB; odd runs start with the halo tB and step down to tA.  Two runs that
+// share a boundary then reach it at the same time -- at their ends (an even
+// run's halo, the next odd run's last step) or at their starts (an odd run's
+// halo, the next even run's first step) -- so the boundary tiles and blocks
+// the halo re-reads are read by both workgroups within one step (the runs
+// of one (b, h) sit on one XCD, xcd_swizzle) and the second read is an L2
+// hit instead of a second HBM read.  Ascending, the block a step completes
+// is t-1 and block t is carried to the next step; descending, block t
+// completes (it received tile t+1's part one step earlier) and block t-1 is
+// carried down.
+//
 // Exchange layout: for query group j and band slot sl (key group j + sl of
 // the 128 keys of blocks t-1, t), a [16 query][16 key] bf16 sub-tile with a
 // 32-byte row.  Phase-1 stores (lane (g,c): query c, keys 4g..4g+3) and
@@ -37,6 +49,11 @@ namespace tension {
 // Two waves per SIMD (two workgroups per CU): registers capped at 256.
 #ifndef TENSION_BWD_WAVES_PER_EU
 #define TENSION_BWD_WAVES_PER_EU 2
+#endif
+
+// Alternating run directions (see above); 0 runs every run ascending.
+#ifndef TENSION_BWD_ALTERNATE
+#define TENSION_BWD_ALTERNATE 1
 #endif
 
 // FAST (W = 64, T a multiple of 64, no bias; dTau in bf16 rows): the band of every
@@ -77,7 +94,10 @@ void mfma_bwd_fused(BandParams p) {
   const int b = bh / p.H, h = bh % p.H, T = p.T;
   const int tA = (int)((int64_t)run * p.ntiles / nch);
   const int tB = (int)((int64_t)(run + 1) * p.ntiles / nch);
-  const int tE = tB < p.ntiles ? tB : tB - 1;  // last step (the halo when tB < ntiles)
+  const int tE = tB < p.ntiles ? tB : tB - 1;  // the halo step when tB < ntiles, else tB - 1
+  // the run's direction (uniform): odd runs step down from tE to tA
+  const bool desc = TENSION_BWD_ALTERNATE && (run & 1) != 0;
+  const int t0 = desc ? tE : tA;  // first step
 
   // per-sequence buffer views: rows >= T load as zeros, stores past T drop
   const SeqBuf sq = seq_view(p.q, b, h, T), sk = seq_view(p.k, b, h, T);
@@ -133,22 +153,22 @@ void mfma_bwd_fused(BandParams p) {
     return __builtin_bit_cast(bf16x4, *(const u16x4*)(XG + (w * kXSlots + sl) * kXSub + c * 16 + 4 * g));
   };
 
-  // ---- prologue: blocks tA-1 (if any) and tA, tile tA
+  // ---- prologue: blocks t0-1 (if any) and t0, tile t0
   {
-    const uint32_t r0 = (uint32_t)(tA * kTile);
+    const uint32_t r0 = (uint32_t)(t0 * kTile);
     TileRegs k0 = seq_tile_load(sk, r0 * sk.rs2, loff(sk, lk0));
     TileRegs v0 = seq_tile_load(sv, r0 * sv.rs2, loff(sv, lv0));
     TileRegs q0 = seq_tile_load(sq, r0 * sq.rs2, loff(sq, lq0));
     TileRegs o0 = seq_tile_load(so, r0 * so.rs2, loff(so, lo0));
-    if (tA >= 1) {
+    if (t0 >= 1) {
       const uint32_t rm = r0 - kTile;
       TileRegs km = seq_tile_load(sk, rm * sk.rs2, loff(sk, lk0));
       TileRegs vm = seq_tile_load(sv, rm * sv.rs2, loff(sv, lv0));
-      tile_store_direct(km, Kt[(tA - 1) & 1], tid);
-      tile_store_direct(vm, Vt[(tA - 1) & 1], tid);
+      tile_store_direct(km, Kt[(t0 - 1) & 1], tid);
+      tile_store_direct(vm, Vt[(t0 - 1) & 1], tid);
     }
-    tile_store_direct(k0, Kt[tA & 1], tid);
-    tile_store_direct(v0, Vt[tA & 1], tid);
+    tile_store_direct(k0, Kt[t0 & 1], tid);
+    tile_store_direct(v0, Vt[t0 & 1], tid);
     tile_store_direct(q0, Qt, tid);
     tile_store_direct(o0, Ot, tid);
     if constexpr (FDT) dt_stage(seq_tile_load(sdt, r0 * sdt.rs2, loff(sdt, 0)));
@@ -161,7 +181,8 @@ void mfma_bwd_fused(BandParams p) {
   gf[0] = dt_row8(Ot, 16 * w + c, g);
   gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
 
-  // dK/dV of block t-1 (key group w), carried from step t-1 to step t
+  // dK/dV (key group w) of the block the current step completes: carried
+  // in from the previous step (ascending block t-1, descending block t)
   f32x4 dk_old[4] = {}, dv_old[4] = {};
   TileRegs dnext;  // FAST dTau: the next step's rows
   // FAST: diagonal-group masks (1 valid, 0 not) for keys 4g + r of query c
@@ -266,13 +287,18 @@ void mfma_bwd_fused(BandParams p) {
     }
   };
 
-  for (int t = tA; t <= tE; ++t) {
+  for (int t = t0; desc ? t >= tA : t <= tE; t += desc ? -1 : 1) {
     const bool halo = t >= tB;
-    const bool more = t < tE;
+    const bool more = desc ? t > tA : t < tE;
+    const int tn = desc ? t - 1 : t + 1;  // the next step's tile
+    // the K/V block the next step adds, into the slot of the block it no
+    // longer needs: t+1 ascending (replacing t-1), t-2 descending (replacing
+    // t; at t = 1 block 0 is stored again over itself)
+    const int bn = desc ? (t >= 2 ? t - 2 : 0) : t + 1;
     // ---- prefetch of step t+1 into registers
     // dTau rows of this step, loaded during the previous step's phase 2
     // (the previous phase 2 has finished reading the exchange tiles)
-    if (FDT && t > tA) {
+    if (FDT && t != t0) {
       dt_stage(dnext);
       // the writes stay here: sunk into phase 1 they would keep dnext's
       // registers live where the register file is full
@@ -280,10 +306,11 @@ void mfma_bwd_fused(BandParams p) {
     }
     TileRegs kn, vn, qn, on;
     if (more) {
-      const uint32_t r0 = (uint32_t)((t + 1) * kTile);
-      kn = seq_tile_load(sk, r0 * sk.rs2, loff(sk, lk0));
-      vn = seq_tile_load(sv, r0 * sv.rs2, loff(sv, lv0));
+      const uint32_t rb = (uint32_t)(bn * kTile);
+      kn = seq_tile_load(sk, rb * sk.rs2, loff(sk, lk0));
+      vn = seq_tile_load(sv, rb * sv.rs2, loff(sv, lv0));
       if constexpr (!FAST) {  // fast path: issued at the start of phase 2
+        const uint32_t r0 = (uint32_t)(tn * kTile);
         qn = seq_tile_load(sq, r0 * sq.rs2, loff(sq, lq0));
         on = seq_tile_load(so, r0 * so.rs2, loff(so, lo0));
       }
@@ -474,13 +501,13 @@ void mfma_bwd_fused(BandParams p) {
     }  // not all live
     __syncthreads();  // X written; every wave is done with block t-1
 
-    if (more) {  // block t+1 replaces block t-1
-      tile_store_direct(kn, Kt[(t + 1) & 1], tid);
-      tile_store_direct(vn, Vt[(t + 1) & 1], tid);
+    if (more) {  // block bn replaces block t-1 (ascending) or t (descending)
+      tile_store_direct(kn, Kt[bn & 1], tid);
+      tile_store_direct(vn, Vt[bn & 1], tid);
       if constexpr (FAST) {
         // the next Q / dO tiles (and dTau rows): loaded here rather than with
         // K / V at the step's start, which leaves phase 1 16 more registers
-        const uint32_t r1 = (uint32_t)((t + 1) * kTile);
+        const uint32_t r1 = (uint32_t)(tn * kTile);
         qn = seq_tile_load(sq, r1 * sq.rs2, loff(sq, lq0));
         on = seq_tile_load(so, r1 * so.rs2, loff(so, lo0));
         if constexpr (FDT) dnext = seq_tile_load(sdt, r1 * sdt.rs2, loff(sdt, 0));
@@ -489,33 +516,50 @@ void mfma_bwd_fused(BandParams p) {
 
     // ---- phase 2: keys 16w..16w+15 of block t-1 (key group w) and of
     // block t (key group 4+w).  Query group j covers key groups j..j+4.
-    const bool own_old = t >= 1 && t - 1 >= tA;
+    // Block t-1 is this run's when t-1 >= tA, block t when t < tB.  The
+    // accumulators hold the block the step completes (dk_old, dv_old: t-1
+    // ascending, t descending) and the block carried to the next step
+    // (dk_new, dv_new); only the exchange sub-tiles they read and the
+    // conditions depend on the direction.
+    const bool own_old = t > tA;
     const bool own_new = !halo;
+    const bool own_done = desc ? own_new : own_old, own_next = desc ? own_old : own_new;
     f32x4 dk_new[4] = {}, dv_new[4] = {};
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int j0 = 2 * kk;
-      const bool need_old = own_old && j0 <= w;
-      const bool need_new = own_new && j0 + 1 >= w;
-      if (!need_old && !need_new) continue;
+      // sub-tiles of block t-1 (key group w) and of block t (key group 4+w)
+      // for query groups j0, j0+1 (x_pair arguments)
+      const int o0 = w - j0, o1 = w - j0 - 1;
+      const bool oq0 = true, oq1 = w >= j0 + 1;
+      const int n0 = 4 + w - j0, n1 = 3 + w - j0;
+      const bool nq0 = j0 >= w, nq1 = true;
+      const bool need_old = j0 <= w, need_new = j0 + 1 >= w;
+      const bool need_done = own_done && (desc ? need_new : need_old);
+      const bool need_next = own_next && (desc ? need_old : need_new);
+      if (!need_done && !need_next) continue;
       bf16x8 aq[4], ao[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         aq[m] = dt_tr8(Qt, m, 32 * kk, g, c);
         ao[m] = dt_tr8(Ot, m, 32 * kk, g, c);
       }
-      if (need_old) {
-        const bf16x8 bp = x_pair(XP, j0, w - j0, true, w - j0 - 1, w >= j0 + 1, g, c);
-        const bf16x8 bg = x_pair(XG, j0, w - j0, true, w - j0 - 1, w >= j0 + 1, g, c);
+      if (need_done) {
+        const int s0 = desc ? n0 : o0, s1 = desc ? n1 : o1;
+        const bool q0 = desc ? nq0 : oq0, q1 = desc ? nq1 : oq1;
+        const bf16x8 bp = x_pair(XP, j0, s0, q0, s1, q1, g, c);
+        const bf16x8 bg = x_pair(XG, j0, s0, q0, s1, q1, g, c);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           dv_old[m] = mfma(ao[m], bp, dv_old[m]);
           dk_old[m] = mfma(aq[m], bg, dk_old[m]);
         }
       }
-      if (need_new) {
-        const bf16x8 bp = x_pair(XP, j0, 4 + w - j0, j0 >= w, 3 + w - j0, true, g, c);
-        const bf16x8 bg = x_pair(XG, j0, 4 + w - j0, j0 >= w, 3 + w - j0, true, g, c);
+      if (need_next) {
+        const int s0 = desc ? o0 : n0, s1 = desc ? o1 : n1;
+        const bool q0 = desc ? oq0 : nq0, q1 = desc ? oq1 : nq1;
+        const bf16x8 bp = x_pair(XP, j0, s0, q0, s1, q1, g, c);
+        const bf16x8 bg = x_pair(XG, j0, s0, q0, s1, q1, g, c);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           dv_new[m] = mfma(ao[m], bp, dv_new[m]);
@@ -523,8 +567,8 @@ void mfma_bwd_fused(BandParams p) {
         }
       }
     }
-    if (own_old) {
-      const uint32_t tk = (uint32_t)((t - 1) * kTile + 16 * w + c);
+    if (own_done) {
+      const uint32_t tk = (uint32_t)((desc ? t : t - 1) * kTile + 16 * w + c);
       STORE_ROWS(sdk, tk, dk_old, inv_scale);
       STORE_ROWS(sdv, tk, dv_old, 1.f);
     }
@@ -547,9 +591,9 @@ void mfma_bwd_fused(BandParams p) {
       gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
     }
   }
-  // the last block of the sequence has no halo step: it is complete after
-  // its own step (no query tile follows it)
-  if (tE == tB - 1) {
+  // ascending, the last block of the sequence has no halo step: it is
+  // complete after its own step (no query tile follows it)
+  if (!desc && tE == tB - 1) {
     const uint32_t tk = (uint32_t)((tB - 1) * kTile + 16 * w + c);
     STORE_ROWS(sdk, tk, dk_old, inv_scale);
     STORE_ROWS(sdv, tk, dv_old, 1.f);
