@@ -109,6 +109,23 @@ def test_compiled_rope_equals_eager(dev):
                 run(cfn, qkv(2, 100, 3, 64, torch.bfloat16, dev, 6, True)[:1]))
 
 
+def test_dynamic_shapes_equal_eager(dev):
+    """One dynamic-shape compile (symbolic T) serves several sequence lengths,
+    ragged ones included; every call equals the eager op bit for bit."""
+    W = 64
+
+    def fn(q, k, v):
+        out, tau = causal_tension(q, k, v, W, 8.0, return_tau=True, normalize="mass")
+        return out, tau, global_tension(q, k, v, 8.0)
+
+    torch._dynamo.reset()
+    cfn = torch.compile(fn, backend="aot_eager", fullgraph=True, dynamic=True)
+    for T in (130, 256, 333):
+        print(f"[compile dynamic] T={T}", flush=True)
+        assert_same(run(fn, qkv(2, T, 2, 64, torch.bfloat16, dev, T, True)),
+                    run(cfn, qkv(2, T, 2, 64, torch.bfloat16, dev, T, True)))
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("autocast,aux", [(False, False), (True, False), (True, True)])
 def test_compiled_model_step_matches_eager(dev, autocast, aux):
