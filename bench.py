@@ -606,6 +606,9 @@ def summarize(paths):
         print("|---|---|---|---|---|---|---|")
         for pname, by in per:
             tot = sum(sum(x) for x in by.values())
+            ten = sum(sum(x) for n, x in by.items() if "tension::" in n)
+            print(f"| {pname} | (all kernels: {tot / 1e3:.2f} ms; tension kernels {ten / 1e3:.2f} ms = "
+                  f"{ten / max(tot, 1e-9):.1%}) | {sum(len(x) for x in by.values())} | | | | |")
             for n, d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
                 if sum(d) < 0.01 * tot:
                     continue
@@ -827,7 +830,8 @@ def bench_model(dev, steps, warmup, aux, fast_rope=False, compiled=False):
     warm_s = time.perf_counter() - t_c
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    torch.cuda.nvtx.range_push("model:" + ("aux" if aux else "ce") + (":compiled" if compiled else ""))
+    torch.cuda.nvtx.range_push("model:" + ("aux" if aux else "ce") + (":fast_rope" if fast_rope else "")
+                               + (":compiled" if compiled else ""))
     e0.record()
     for _ in range(steps):
         loss = step()
