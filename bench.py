@@ -653,12 +653,17 @@ def rocprof_passes(passes, n=16, timeout=240):
         try:
             r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, env=env, cwd=ROOT)
         except subprocess.TimeoutExpired:
+            shutil.rmtree(tmp, ignore_errors=True)
             return [], {}, f"rocprofv3 {what} timed out"
         # rocprofv3 itself may end with a segmentation fault after the program
         # finished and its results are whole; the results decide
         if r.returncode not in (0, -11, 139) or "profile-kernels:" not in (r.stdout + r.stderr):
+            shutil.rmtree(tmp, ignore_errors=True)
             return [], {}, f"rocprofv3 {what} failed (rc {r.returncode})"
-    durations, counters = _collect([tmp])
+    try:
+        durations, counters = _collect([tmp])
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
     return durations, counters, None
 
 
@@ -678,7 +683,8 @@ def measure_traffic(n=16):
     traffic, cal = hbm_traffic(counters)
     if not traffic:
         return {}, {}, "no calibrated FETCH_SIZE / WRITE_SIZE readings: traffic not measured"
-    util = {k: (round(v, 1), round(counters.get("VALUBusy", {}).get(k, (float("nan"),))[0], 1))
+    valu = counters.get("VALUBusy", {})
+    util = {k: (round(v, 1), round(valu[k][0], 1) if k in valu else None)
             for k, (v, _) in counters.get("MfmaUtil", {}).items() if "tension::" in k}
     return ({k: int(r + w) for k, (r, w) in traffic.items()}, util,
             f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE / MfmaUtil+VALUBusy in this run, {n} launches per "
