@@ -141,7 +141,7 @@ def test_117m_geometry_tau_and_dtau(dev, normalize):
 
 
 @pytest.mark.parametrize("normalize", [None, "count", "mass"])
-@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 320), (1, 12, 1024), (8, 16, 512)])
+@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 320), (1, 12, 1024), (8, 16, 512), (2, 90, 640)])
 def test_fast_path_dtau_bf16(dev, normalize, B, H, T):
     """The W = 64, T % 64 == 0 bf16 backward with a gradient through tau
     (the model's aux-loss step): dTau rows staged per wave.  The first three
@@ -409,12 +409,15 @@ def test_errors(dev):
     (2, 48, 400, 64),   # 5 runs of 1-2 tiles, ragged last tile
     (64, 17, 65, 33),   # one run per (b,h) (no halo), W < 64
     (3, 2, 333, 17),
+    (4, 64, 512, 64),   # 2 runs of 4 tiles: run 1 steps down from the sequence end (no halo)
+    (2, 90, 640, 64),   # 3 runs of 3-4 tiles: boundaries met at the runs' ends and at their starts
 ])
 @pytest.mark.parametrize("normalize", [None, "mass", "count"])
 def test_fused_backward_runs_bf16(dev, B, H, T, W, normalize):
     """The bf16 backward for W <= 64 is one kernel that splits every (b,h)
-    sequence into runs of tiles and recomputes the tile after each run; the
-    grid size, and so the run length, depends on B*H."""
+    sequence into runs of tiles, odd runs stepping down, and recomputes the
+    tile after each run (the halo); the grid size, and so the run length and
+    count, depends on B*H."""
     inp = make_inputs(B, T, H, 64, seed=B * 1000 + T + W, std=0.5, dtype=torch.bfloat16,
                       bias_std=0.5, bias_shape=(B, T, W))
     use_bias = normalize == "mass"
