@@ -507,13 +507,14 @@ int tension_rope(const tension_buf* x, const tension_buf* y, const float* cos, c
   p.B = (int)B; p.T = (int)T; p.H = (int)H; p.D = (int)D;
   p.pos_offset = pos_offset; p.inverse = inverse;
   hipError_t e = hipSuccess;
-  // 16-byte pieces of bf16 rows and of the float tables
+  // 16-byte pieces of bf16 / float32 rows and of the float tables
   auto v16 = [](const tension_buf* b) {
-    return b->dtype == TENSION_BF16 && ((uintptr_t)b->ptr & 15) == 0 && b->s[0] % 8 == 0 && b->s[1] % 8 == 0 &&
-           b->s[2] % 8 == 0;
+    const int64_t per = b->dtype == TENSION_BF16 ? 8 : b->dtype == TENSION_F32 ? 4 : 0;
+    return per && ((uintptr_t)b->ptr & 15) == 0 && b->s[0] % per == 0 && b->s[1] % per == 0 &&
+           b->s[2] % per == 0;
   };
   if (D % 16 == 0 && v16(x) && v16(y) && ((uintptr_t)cos & 15) == 0 && ((uintptr_t)sin & 15) == 0)
-    launch_rope_vec(p, hs(stream), &e);
+    launch_rope_vec(x->dtype == TENSION_F32, y->dtype == TENSION_F32, p, hs(stream), &e);
   else
     launch_rope(is_f64(x) || is_f64(y), p, hs(stream), &e);
   return launched(e, "tension_rope");

@@ -358,11 +358,42 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
   st<A>(p.y, yo + i + half, x1 * s + x2 * c);
 }
 
-// bf16 in and out, D a multiple of 16, 16-byte aligned rows and tables: one
-// thread rotates 8 pairs (16 bytes of each half and 32 bytes of each table
-// row), so a row of D = 64 is 4 consecutive threads reading whole 16-byte
-// pieces.  Both halves are read before either is written (y may alias x).
-__global__ __launch_bounds__(256) void rope_bf16_vec(RopeParams p) {
+// bf16 / float32 in and out (the four pairs), D a multiple of 16, 16-byte
+// aligned rows and tables: one thread rotates 8 pairs (16 or 32 bytes of each
+// half, 32 bytes of each table row), so a row of D = 64 is 4 consecutive
+// threads reading whole 16-byte pieces.  float32 arithmetic, as rope_kernel;
+// both halves are read before either is written (y may alias x).
+template <typename T>
+__device__ __forceinline__ void rope_load8(const T* p, float* v) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x8 x = __builtin_bit_cast(bf16x8, *(const u16x8*)p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)x[e];
+  } else {
+    const f32x4 x0 = *(const f32x4*)p, x1 = *(const f32x4*)(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = x0[e];
+      v[4 + e] = x1[e];
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void rope_store8(T* p, const float* v) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 y;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (bf16)v[e];
+    *(u16x8*)p = __builtin_bit_cast(u16x8, y);
+  } else {
+    *(f32x4*)p = f32x4{v[0], v[1], v[2], v[3]};
+    *(f32x4*)(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+}
+
+template <typename XT, typename YT>
+__global__ __launch_bounds__(256) void rope_vec(RopeParams p) {
   const int half = p.D >> 1, nq = half >> 3;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)p.B * p.T * p.H * nq;
@@ -373,30 +404,36 @@ __global__ __launch_bounds__(256) void rope_bf16_vec(RopeParams p) {
   r /= p.H;
   const int t = (int)(r % p.T);
   const int b = (int)(r / p.T);
-  const bf16* xr = (const bf16*)p.x.p + b * p.x.s0 + (int64_t)t * p.x.s1 + h * p.x.s2 + 8 * q;
-  bf16* yr = (bf16*)p.y.p + b * p.y.s0 + (int64_t)t * p.y.s1 + h * p.y.s2 + 8 * q;
-  const bf16x8 x1 = __builtin_bit_cast(bf16x8, *(const u16x8*)xr);
-  const bf16x8 x2 = __builtin_bit_cast(bf16x8, *(const u16x8*)(xr + half));
+  const XT* xr = (const XT*)p.x.p + b * p.x.s0 + (int64_t)t * p.x.s1 + h * p.x.s2 + 8 * q;
+  YT* yr = (YT*)p.y.p + b * p.y.s0 + (int64_t)t * p.y.s1 + h * p.y.s2 + 8 * q;
+  float x1[8], x2[8], y1[8], y2[8];
+  rope_load8(xr, x1);
+  rope_load8(xr + half, x2);
   const int64_t to = (p.pos_offset + t) * half + 8 * q;
   const f32x4 c0 = *(const f32x4*)(p.cos + to), c1 = *(const f32x4*)(p.cos + to + 4);
   const f32x4 s0 = *(const f32x4*)(p.sin + to), s1 = *(const f32x4*)(p.sin + to + 4);
   const float sg = p.inverse ? -1.f : 1.f;
-  bf16x8 y1, y2;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float c = e < 4 ? c0[e & 3] : c1[e & 3];
     const float sn = sg * (e < 4 ? s0[e & 3] : s1[e & 3]);
-    const float a = (float)x1[e], bb = (float)x2[e];
-    y1[e] = (bf16)(a * c - bb * sn);
-    y2[e] = (bf16)(a * sn + bb * c);
+    y1[e] = x1[e] * c - x2[e] * sn;
+    y2[e] = x1[e] * sn + x2[e] * c;
   }
-  *(u16x8*)yr = __builtin_bit_cast(u16x8, y1);
-  *(u16x8*)(yr + half) = __builtin_bit_cast(u16x8, y2);
+  rope_store8(yr, y1);
+  rope_store8(yr + half, y2);
 }
 
-int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err) {
+int launch_rope_vec(bool x_f32, bool y_f32, const RopeParams& p, hipStream_t st, hipError_t* err) {
   const int64_t total = (int64_t)p.B * p.T * p.H * (p.D / 16);
-  hipLaunchKernelGGL(rope_bf16_vec, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (x_f32) {
+    if (y_f32) hipLaunchKernelGGL((rope_vec<float, float>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((rope_vec<float, bf16>), grid, dim3(256), 0, st, p);
+  } else {
+    if (y_f32) hipLaunchKernelGGL((rope_vec<bf16, float>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((rope_vec<bf16, bf16>), grid, dim3(256), 0, st, p);
+  }
   *err = hipGetLastError();
   return 0;
 }

@@ -84,7 +84,8 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
 // phase 0 forward, 1 dQ, 2 dK / dV
 int launch_mixed(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
-int launch_rope_vec(const RopeParams& p, hipStream_t st, hipError_t* err);
+// bf16 / float32 rows (x_f32, y_f32), D % 16 == 0, 16-byte aligned rows and tables
+int launch_rope_vec(bool x_f32, bool y_f32, const RopeParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_stats(const TauStatParams& p, hipStream_t st, hipError_t* err);
 int launch_tau_aggregate(const TauAggParams& p, hipStream_t st, hipError_t* err);
 int launch_bias_insert(const BiasTableParams& p, hipStream_t st, hipError_t* err);

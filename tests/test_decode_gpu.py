@@ -192,3 +192,31 @@ def test_rope(dev, dtype, out_dtype):
     tol = 1e-5 if dtype != torch.bfloat16 else 2e-2
     metric = max_abs if dtype != torch.bfloat16 else rel_l2
     assert metric(f64(xd.grad), dwant) <= tol
+
+
+@pytest.mark.parametrize("D,dtype,out_dtype", [(32, torch.bfloat16, torch.float32), (48, torch.float32, None),
+                                               (40, torch.bfloat16, torch.float32), (16, torch.float32, torch.bfloat16)])
+def test_rope_head_dims(dev, D, dtype, out_dtype):
+    """RoPE on the 16-byte path (D a multiple of 16: 32, 48, 16) and the
+    generic one (D = 40), each dtype pair, forward and adjoint against the
+    float64 restatement of model.py:75-81."""
+    from bozo_amd import rope
+    B, T, H = 2, 37, 3
+    cos, sin = O.rope_tables(64, D)
+    g = torch.Generator().manual_seed(D)
+    x = torch.randn(B, T, H, D, generator=g).to(dtype)
+    xd = x.to(dev).requires_grad_(True)
+    y = rope(xd, torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev), pos_offset=5, out_dtype=out_dtype)
+    dy = torch.randn(B, T, H, D, generator=g).to(y.dtype)
+    (y.double() * dy.to(dev).double()).sum().backward()
+    want = O.rope_apply(f64(x), cos, sin, pos_offset=5)
+    dwant = O.rope_apply_adjoint(f64(dy), cos, sin, pos_offset=5)
+    assert y.dtype == (out_dtype or dtype)
+    if y.dtype == torch.bfloat16:
+        assert np.max(np.abs(f64(y) - want) / np.maximum(np.abs(want), 1e-3)) <= 2 ** -8
+    else:
+        assert max_abs(f64(y), want) <= 1e-5
+    if dtype == torch.bfloat16:
+        assert rel_l2(f64(xd.grad), dwant) <= 2e-2
+    else:
+        assert max_abs(f64(xd.grad), dwant) <= 1e-5
