@@ -39,13 +39,24 @@ constexpr int kUnroll = 4;                     // passes whose loads are in flig
 // the strides multiples of 8, 16-byte aligned base): one 16-byte load, issued
 // for every lane (chunks past W read chunk 0 and are zeroed), so a pass's
 // loads carry no branch; otherwise element loads.
-template <bool VEC, bool FULL = false>
+// VEC: 0 element loads of any dtype, 1 one 16-byte load of bf16, 2 two of
+// float32 (vec_kind)
+template <int VEC, bool FULL = false>
 __device__ __forceinline__ void row8(const Buf& b, int64_t off, int ch, int W, float* v) {
-  if constexpr (VEC) {
+  if constexpr (VEC == 1) {
     const bool in = FULL || 8 * ch < W;
     const bf16x8 x = __builtin_bit_cast(bf16x8, *(const u16x8*)((const bf16*)b.p + off + (in ? 8 * ch : 0)));
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = in ? (float)x[e] : 0.f;
+  } else if constexpr (VEC == 2) {
+    const bool in = FULL || 8 * ch < W;
+    const float* q = (const float*)b.p + off + (in ? 8 * ch : 0);
+    const f32x4 x0 = *(const f32x4*)q, x1 = *(const f32x4*)(q + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = in ? x0[e] : 0.f;
+      v[4 + e] = in ? x1[e] : 0.f;
+    }
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -56,14 +67,20 @@ __device__ __forceinline__ void row8(const Buf& b, int64_t off, int ch, int W, f
 }
 
 // store counterpart of row8
-template <bool VEC, bool FULL = false>
+template <int VEC, bool FULL = false>
 __device__ __forceinline__ void row8_store(const Buf& b, int64_t off, int ch, int W, const float* v) {
-  if constexpr (VEC) {
+  if constexpr (VEC == 1) {
     if (FULL || 8 * ch < W) {
       bf16x8 x;
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = (bf16)v[e];
       *(u16x8*)((bf16*)b.p + off + 8 * ch) = __builtin_bit_cast(u16x8, x);
+    }
+  } else if constexpr (VEC == 2) {
+    if (FULL || 8 * ch < W) {
+      float* q = (float*)b.p + off + 8 * ch;
+      *(f32x4*)q = f32x4{v[0], v[1], v[2], v[3]};
+      *(f32x4*)(q + 4) = f32x4{v[4], v[5], v[6], v[7]};
     }
   } else {
 #pragma unroll
@@ -72,8 +89,13 @@ __device__ __forceinline__ void row8_store(const Buf& b, int64_t off, int ch, in
   }
 }
 
-__device__ __forceinline__ bool vec_ok(const Buf& b, int W) {
-  return b.dt == TENSION_BF16 && (W & 7) == 0 && ((b.s0 | b.s1 | b.s2) & 7) == 0 && ((uintptr_t)b.p & 15) == 0;
+// 1: bf16 rows read 16 bytes (8 slots) at a time, 2: float32 rows read 32
+// bytes at a time (W a multiple of 8, 16-byte aligned slots), 0: neither
+__device__ __forceinline__ int vec_kind(const Buf& b, int W) {
+  if ((W & 7) != 0 || ((uintptr_t)b.p & 15) != 0) return 0;
+  if (b.dt == TENSION_BF16 && ((b.s0 | b.s1 | b.s2) & 7) == 0) return 1;
+  if (b.dt == TENSION_F32 && ((b.s0 | b.s1 | b.s2) & 3) == 0) return 2;
+  return 0;
 }
 
 __device__ __forceinline__ float at(const Buf& b, int64_t off) { return ld<float>(b, off); }
@@ -135,7 +157,7 @@ struct RowWalk {
 // Forward over this workgroup's kAuxRowsPerBlock rows of one layer: the four
 // sums accumulate per lane (one lane per row contributes) and meet once at
 // the end.
-template <bool VEC, bool FULL>
+template <int VEC, bool FULL>
 __device__ __forceinline__ void fwd_rows(const AuxLossParams& p, const Buf& tb, float* sums) {
   const int ch = threadIdx.x & 7;
   const int64_t nrow = (int64_t)p.B * p.T * p.H;
@@ -193,7 +215,7 @@ __device__ __forceinline__ void fwd_rows(const AuxLossParams& p, const Buf& tb, 
   }
 }
 
-template <bool VEC, bool FULL>
+template <int VEC, bool FULL>
 __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Buf& tb, const Buf& db) {
   const int ch = threadIdx.x & 7;
   const int64_t nrow = (int64_t)p.B * p.T * p.H;
@@ -279,12 +301,17 @@ __global__ __launch_bounds__(kThreadsAux) void aux_loss_fwd_kernel(AuxLossParams
   const Buf tb = p.tau[l];
   float sums[4] = {0.f, 0.f, 0.f, 0.f};
   // W = 64 (the model's window): every lane's chunk is in the row
-  if (vec_ok(tb, p.W) && p.W == 64)
-    fwd_rows<true, true>(p, tb, sums);
-  else if (vec_ok(tb, p.W))
-    fwd_rows<true, false>(p, tb, sums);
+  const int vk = vec_kind(tb, p.W);
+  if (vk == 1 && p.W == 64)
+    fwd_rows<1, true>(p, tb, sums);
+  else if (vk == 1)
+    fwd_rows<1, false>(p, tb, sums);
+  else if (vk == 2 && p.W == 64)
+    fwd_rows<2, true>(p, tb, sums);
+  else if (vk == 2)
+    fwd_rows<2, false>(p, tb, sums);
   else
-    fwd_rows<false, false>(p, tb, sums);
+    fwd_rows<0, false>(p, tb, sums);
   // the block's sums go to its own slot of the partials buffer (summed by
   // the caller: deterministic, no atomics)
   __shared__ double red[4][kRowsPerPass];
@@ -304,13 +331,17 @@ __global__ __launch_bounds__(kThreadsAux) void aux_loss_fwd_kernel(AuxLossParams
 __global__ __launch_bounds__(kThreadsAux) void aux_loss_bwd_kernel(AuxLossParams p) {
   const int l = blockIdx.y;
   const Buf tb = p.tau[l], db = p.dtau[l];
-  const bool vec = vec_ok(tb, p.W) && vec_ok(db, p.W);
-  if (vec && p.W == 64)
-    bwd_rows<true, true>(p, l, tb, db);
-  else if (vec)
-    bwd_rows<true, false>(p, l, tb, db);
+  const int vt = vec_kind(tb, p.W), vk = vt == vec_kind(db, p.W) ? vt : 0;
+  if (vk == 1 && p.W == 64)
+    bwd_rows<1, true>(p, l, tb, db);
+  else if (vk == 1)
+    bwd_rows<1, false>(p, l, tb, db);
+  else if (vk == 2 && p.W == 64)
+    bwd_rows<2, true>(p, l, tb, db);
+  else if (vk == 2)
+    bwd_rows<2, false>(p, l, tb, db);
   else
-    bwd_rows<false, false>(p, l, tb, db);
+    bwd_rows<0, false>(p, l, tb, db);
 }
 
 int launch_aux_loss(bool bwd, const AuxLossParams& p, hipStream_t st, hipError_t* err) {
