@@ -75,6 +75,37 @@ __device__ __forceinline__ SplitRegs tile_load_split(const float* base, int64_t 
   return x;
 }
 
+// A float32 tile's two staged rows of this thread as loaded (zero outside
+// [0, T)); split_rows turns them into tile_load_split's result later.
+struct RawRows {
+  f32x4 a0, a1, b0, b1;
+};
+
+__device__ __forceinline__ RawRows tile_load_raw(const float* base, int64_t rs, int r0, int T, int tid) {
+  const int ch = tid & 7;
+  const int ra = r0 + staged_row(tid), rb = ra + 8;
+  RawRows x;
+  x.a0 = x.a1 = x.b0 = x.b1 = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (ra >= 0 && ra < T) {
+    x.a0 = *(const f32x4*)(base + (int64_t)ra * rs + 8 * ch);
+    x.a1 = *(const f32x4*)(base + (int64_t)ra * rs + 8 * ch + 4);
+  }
+  if (rb >= 0 && rb < T) {
+    x.b0 = *(const f32x4*)(base + (int64_t)rb * rs + 8 * ch);
+    x.b1 = *(const f32x4*)(base + (int64_t)rb * rs + 8 * ch + 4);
+  }
+  return x;
+}
+
+__device__ __forceinline__ SplitRegs split_rows(const RawRows& r) {
+  SplitRegs x;
+  const float a[8] = {r.a0[0], r.a0[1], r.a0[2], r.a0[3], r.a1[0], r.a1[1], r.a1[2], r.a1[3]};
+  const float b[8] = {r.b0[0], r.b0[1], r.b0[2], r.b0[3], r.b1[0], r.b1[1], r.b1[2], r.b1[3]};
+  split8(a, x.hi.a, x.lo.a);
+  split8(b, x.hi.b, x.lo.b);
+  return x;
+}
+
 // A bf16 tile's two staged rows of this thread (zero outside [0, T)).
 __device__ __forceinline__ TileRegs tile_load_staged(const bf16* base, int64_t rs, int r0, int T, int tid) {
   const int ch = tid & 7;
@@ -347,15 +378,24 @@ __global__ __launch_bounds__(kThreads) void mx_dq(BandParams p) {
 
 // ---------------------------------------------------------------- dK / dV
 
+// Query tiles k and k + 1 pass through one set of LDS tiles in turn (33 KB:
+// three workgroups per CU, register-limited) rather than side by side;
+// without bias / dTau, tile k + 1's rows are loaded into registers while
+// tile k is worked on.
+#ifndef TENSION_MX_DKV_SLOTS
+#define TENSION_MX_DKV_SLOTS 1
+#endif
+
 template <int NORM, bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
-  // query tile k in slot 0, k + 1 in slot 1: Q hi, Q lo, dO hi, dO lo
-  __shared__ __attribute__((aligned(16))) bf16 lds[8 * kDTile];
+  // query tile k + s in slot s % NS: Q hi, Q lo, dO hi, dO lo
+  constexpr int NS = TENSION_MX_DKV_SLOTS;
+  __shared__ __attribute__((aligned(16))) bf16 lds[4 * NS * kDTile];
   __shared__ float sa[2 * kTile], sc[2 * kTile];
   bf16* const Qh = lds;
-  bf16* const Ql = lds + 2 * kDTile;
-  bf16* const Oh = lds + 4 * kDTile;
-  bf16* const Ol = lds + 6 * kDTile;
+  bf16* const Ql = lds + NS * kDTile;
+  bf16* const Oh = lds + 2 * NS * kDTile;
+  bf16* const Ol = lds + 3 * NS * kDTile;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
@@ -373,16 +413,22 @@ __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
   const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const float* ob_ = (const float*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
 
+  // query tile k + s into slot s % NS
+  auto store_tile = [&](int s, const SplitRegs& qx, const SplitRegs& ox) {
+    const int sl = (s % NS) * kDTile;
+    tile_store_direct(qx.hi, Qh + sl, tid);
+    tile_store_direct(qx.lo, Ql + sl, tid);
+    tile_store_direct(ox.hi, Oh + sl, tid);
+    tile_store_direct(ox.lo, Ol + sl, tid);
+  };
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int q0 = k0 + s * kTile;
-    const SplitRegs qx = tile_load_split(qb_, p.q.s1, q0, T, tid);
-    const SplitRegs ox = tile_load_split(ob_, p.dout.s1, q0, T, tid);
-    tile_store_direct(qx.hi, Qh + s * kDTile, tid);
-    tile_store_direct(qx.lo, Ql + s * kDTile, tid);
-    tile_store_direct(ox.hi, Oh + s * kDTile, tid);
-    tile_store_direct(ox.lo, Ol + s * kDTile, tid);
-  }
+  for (int s = 0; s < NS; ++s)
+    store_tile(s, tile_load_split(qb_, p.q.s1, k0 + s * kTile, T, tid),
+               tile_load_split(ob_, p.dout.s1, k0 + s * kTile, T, tid));
+  // with one slot and no bias / dTau (whose per-pair loads need the
+  // registers): tile k + 1's rows in flight during tile k
+  constexpr bool PF = NS == 1 && !BIAS && !DTAU;
+  RawRows qn{}, on{};
   if (tid < 2 * kTile) {
     const int t = k0 + tid;
     float a = 1.f, cv = 0.f;
@@ -414,10 +460,23 @@ __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
   f32x4 dk[4] = {}, dv[4] = {};
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    const bf16* qh = Qh + s * kDTile;
-    const bf16* ql = Ql + s * kDTile;
-    const bf16* oh = Oh + s * kDTile;
-    const bf16* ol = Ol + s * kDTile;
+    if (PF && s == 0) {
+      qn = tile_load_raw(qb_, p.q.s1, k0 + kTile, T, tid);
+      on = tile_load_raw(ob_, p.dout.s1, k0 + kTile, T, tid);
+    }
+    if (s >= NS) {  // the slot of tile s - NS is free once every wave is past it
+      __syncthreads();
+      if constexpr (PF)
+        store_tile(s, split_rows(qn), split_rows(on));
+      else
+        store_tile(s, tile_load_split(qb_, p.q.s1, k0 + s * kTile, T, tid),
+                   tile_load_split(ob_, p.dout.s1, k0 + s * kTile, T, tid));
+      __syncthreads();
+    }
+    const bf16* qh = Qh + (s % NS) * kDTile;
+    const bf16* ql = Ql + (s % NS) * kDTile;
+    const bf16* oh = Oh + (s % NS) * kDTile;
+    const bf16* ol = Ol + (s % NS) * kDTile;
     float Pa[4][4], G[4][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
