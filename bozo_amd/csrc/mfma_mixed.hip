@@ -153,13 +153,24 @@ __device__ __forceinline__ void store_row_f32(float* row, const f32x4* acc, floa
 
 // ---------------------------------------------------------------- forward
 
+// Key blocks t-1 and t pass through one set of LDS tiles in turn (24 KB)
+// rather than side by side; without bias, block t's rows are loaded into
+// registers while block t-1 is worked on.
+#ifndef TENSION_MX_FWD_SLOTS
+#define TENSION_MX_FWD_SLOTS 1
+#endif
+#ifndef TENSION_MX_FWD_PREFETCH
+#define TENSION_MX_FWD_PREFETCH 1
+#endif
+
 template <int NORM, bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
-  // key block t-1 in slot 0, t in slot 1: K hi, K lo, V
-  __shared__ __attribute__((aligned(16))) bf16 lds[6 * kDTile];
+  // key block t-1+s in slot s % NS: K hi, K lo, V
+  constexpr int NS = TENSION_MX_FWD_SLOTS;
+  __shared__ __attribute__((aligned(16))) bf16 lds[3 * NS * kDTile];
   bf16* const Kh = lds;
-  bf16* const Kl = lds + 2 * kDTile;
-  bf16* const Vs = lds + 4 * kDTile;
+  bf16* const Kl = lds + NS * kDTile;
+  bf16* const Vs = lds + 2 * NS * kDTile;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
@@ -175,15 +186,23 @@ __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
   const float* kb_ = (const float*)p.k.p + b * p.k.s0 + h * p.k.s2;
   const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
 
+  // key block t-1+s into slot s % NS
+  auto store_blk = [&](int s, const SplitRegs& kx, const TileRegs& vx) {
+    const int sl = (s % NS) * kDTile;
+    tile_store_direct(kx.hi, Kh + sl, tid);
+    tile_store_direct(kx.lo, Kl + sl, tid);
+    tile_store_direct(vx, Vs + sl, tid);
+  };
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int kb0 = t0 - kTile + s * kTile;
-    const SplitRegs kx = tile_load_split(kb_, p.k.s1, kb0, T, tid);
-    const TileRegs vx = tile_load_staged(vb_, p.v.s1, kb0, T, tid);
-    tile_store_direct(kx.hi, Kh + s * kDTile, tid);
-    tile_store_direct(kx.lo, Kl + s * kDTile, tid);
-    tile_store_direct(vx, Vs + s * kDTile, tid);
+    store_blk(s, tile_load_split(kb_, p.k.s1, kb0, T, tid), tile_load_staged(vb_, p.v.s1, kb0, T, tid));
   }
+  // with one slot and no bias (whose per-pair loads need the registers):
+  // block t's rows in flight during block t-1
+  constexpr bool PF = NS == 1 && !BIAS && TENSION_MX_FWD_PREFETCH;
+  RawRows kn{};
+  TileRegs vn{};
   const SplitFrag q0 = frag_f32(qb_, p.q.s1, tq, T, g), q1 = frag_f32(qb_, p.q.s1, tq, T, 4 + g);
   __syncthreads();
 
@@ -193,8 +212,20 @@ __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int kb0 = t0 - kTile + s * kTile;
-    const bf16* kh = Kh + s * kDTile;
-    const bf16* kl = Kl + s * kDTile;
+    if (PF && s == 0) {
+      kn = tile_load_raw(kb_, p.k.s1, t0, T, tid);
+      vn = tile_load_staged(vb_, p.v.s1, t0, T, tid);
+    }
+    if (s >= NS) {  // the slot of block s - NS is free once every wave is past it
+      __syncthreads();
+      if constexpr (PF)
+        store_blk(s, split_rows(kn), vn);
+      else
+        store_blk(s, tile_load_split(kb_, p.k.s1, kb0, T, tid), tile_load_staged(vb_, p.v.s1, kb0, T, tid));
+      __syncthreads();
+    }
+    const bf16* kh = Kh + (s % NS) * kDTile;
+    const bf16* kl = Kl + (s % NS) * kDTile;
     float pr[4][4];
     int kind[4];
 #pragma unroll
@@ -231,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
       bf16x8 ph, pl;
       pack_split(pr[2 * kk], pr[2 * kk + 1], ph, pl);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc[m] = mm2(dt_tr8(Vs + s * kDTile, m, 32 * kk, g, c), ph, pl, acc[m]);
+      for (int m = 0; m < 4; ++m) acc[m] = mm2(dt_tr8(Vs + (s % NS) * kDTile, m, 32 * kk, g, c), ph, pl, acc[m]);
     }
   }
   msum = wave_sum_g(msum);

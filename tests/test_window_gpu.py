@@ -374,6 +374,18 @@ def test_mixed_dtypes_band_edges_bias(dev, T, W):
     check_mixed(hip, ref, True)
 
 
+@pytest.mark.parametrize("T,W,normalize", [(1, 4, "mass"), (70, 64, "count"), (100, 17, "mass"),
+                                           (130, 64, None), (200, 33, "mass")])
+def test_mixed_dtypes_band_edges_plain(dev, T, W, normalize):
+    """Ragged T without bias or dTau: the forward and dK/dV kernels then load
+    their second key block / query tile into registers while the first is
+    worked on."""
+    inp = mixed_inputs(2, T, 3, seed=3 * T + W, W=W)
+    hip = hip_run(inp, W, 8.0, dev, normalize=normalize)
+    ref = oracle_run(inp, W, 8.0, normalize=normalize)
+    check_mixed(hip, ref, False)
+
+
 def test_empty_batch(dev):
     from bozo_amd import causal_tension
     Q = torch.zeros(0, 16, 2, 64, device=dev, dtype=torch.bfloat16)
