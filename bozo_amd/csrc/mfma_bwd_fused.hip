@@ -141,7 +141,8 @@ void mfma_bwd_fused(BandParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int pos = 8 * ch + e + row;
-        base[(pos >> 4) * kXSub + row * 16 + (pos & 15)] = v[e];
+        const int col = pos & 15;
+        base[(pos >> 4) * kXSub + row * 16 + 4 * ((col >> 2) ^ xsw(row)) + (col & 3)] = v[e];
       }
     }
   };
@@ -150,7 +151,7 @@ void mfma_bwd_fused(BandParams p) {
   // five reads (ten live registers) into the register-bound phase 1
   auto dt_at = [&](int sl) -> bf16x4 {
     asm volatile("" ::: "memory");
-    return __builtin_bit_cast(bf16x4, *(const u16x4*)(XG + (w * kXSlots + sl) * kXSub + c * 16 + 4 * g));
+    return __builtin_bit_cast(bf16x4, *(const u16x4*)(XG + (w * kXSlots + sl) * kXSub + c * 16 + 4 * (g ^ xsw(c))));
   };
 
   // ---- prologue: blocks t0-1 (if any) and t0, tile t0
