@@ -156,6 +156,11 @@ __device__ __forceinline__ void store_row_f32(float* row, const f32x4* acc, floa
 // Key blocks t-1 and t pass through one set of LDS tiles in turn (24 KB)
 // rather than side by side; without bias, block t's rows are loaded into
 // registers while block t-1 is worked on.
+// Neighbouring tiles visit their shared block / tile in the same stage.
+#ifndef TENSION_MX_ALTERNATE
+#define TENSION_MX_ALTERNATE 1
+#endif
+
 #ifndef TENSION_MX_FWD_SLOTS
 #define TENSION_MX_FWD_SLOTS 1
 #endif
@@ -181,6 +186,10 @@ __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
   const int lo = tq - p.win > 0 ? tq - p.win : 0;
   const int hi = tq < T ? tq - 1 : -1;  // hi < lo: no key for this row
   const WaveBand wb = wave_band(p, t0 + wave * 16);
+  // odd tiles take block t first: the block two neighbouring tiles share is
+  // then read by both in the same stage (the second read an L2 hit)
+  const bool rev = TENSION_MX_ALTERNATE && (id.tile & 1) != 0;
+  auto blk0 = [&](int s) { return t0 - kTile + (rev ? 1 - s : s) * kTile; };
 
   const float* qb_ = (const float*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const float* kb_ = (const float*)p.k.p + b * p.k.s0 + h * p.k.s2;
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
   };
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    const int kb0 = t0 - kTile + s * kTile;
+    const int kb0 = blk0(s);
     store_blk(s, tile_load_split(kb_, p.k.s1, kb0, T, tid), tile_load_staged(vb_, p.v.s1, kb0, T, tid));
   }
   // with one slot and no bias (whose per-pair loads need the registers):
@@ -211,10 +220,10 @@ __global__ __launch_bounds__(kThreads) void mx_fwd(BandParams p) {
   float msum = 0.f;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    const int kb0 = t0 - kTile + s * kTile;
+    const int kb0 = blk0(s);
     if (PF && s == 0) {
-      kn = tile_load_raw(kb_, p.k.s1, t0, T, tid);
-      vn = tile_load_staged(vb_, p.v.s1, t0, T, tid);
+      kn = tile_load_raw(kb_, p.k.s1, blk0(1), T, tid);
+      vn = tile_load_staged(vb_, p.v.s1, blk0(1), T, tid);
     }
     if (s >= NS) {  // the slot of block s - NS is free once every wave is past it
       __syncthreads();
@@ -418,7 +427,7 @@ __global__ __launch_bounds__(kThreads) void mx_dq(BandParams p) {
 #endif
 
 template <int NORM, bool BIAS, bool DTAU>
-__global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) void mx_dkv(BandParams p) {
   // query tile k + s in slot s % NS: Q hi, Q lo, dO hi, dO lo
   constexpr int NS = TENSION_MX_DKV_SLOTS;
   __shared__ __attribute__((aligned(16))) bf16 lds[4 * NS * kDTile];
@@ -438,6 +447,10 @@ __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
   // queries that see this lane's key: [tk + 1, min(tk + W, T - 1)]
   const int qlo = tk + 1;
   const int qhi = !kok ? -1 : (tk + p.win > T - 1 ? T - 1 : tk + p.win);
+  // odd key tiles take query tile k + 1 first: the query tile two
+  // neighbouring key tiles share is then read by both in the same stage
+  const bool rev = TENSION_MX_ALTERNATE && (id.tile & 1) != 0;
+  auto qs = [&](int s) { return rev ? 1 - s : s; };
 
   const float* qb_ = (const float*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const float* kb_ = (const float*)p.k.p + b * p.k.s0 + h * p.k.s2;
@@ -454,8 +467,8 @@ __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
   };
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    store_tile(s, tile_load_split(qb_, p.q.s1, k0 + s * kTile, T, tid),
-               tile_load_split(ob_, p.dout.s1, k0 + s * kTile, T, tid));
+    store_tile(s, tile_load_split(qb_, p.q.s1, k0 + qs(s) * kTile, T, tid),
+               tile_load_split(ob_, p.dout.s1, k0 + qs(s) * kTile, T, tid));
   // with one slot and no bias / dTau (whose per-pair loads need the
   // registers): tile k + 1's rows in flight during tile k
   constexpr bool PF = NS == 1 && !BIAS && !DTAU;
@@ -492,16 +505,16 @@ __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (PF && s == 0) {
-      qn = tile_load_raw(qb_, p.q.s1, k0 + kTile, T, tid);
-      on = tile_load_raw(ob_, p.dout.s1, k0 + kTile, T, tid);
+      qn = tile_load_raw(qb_, p.q.s1, k0 + qs(1) * kTile, T, tid);
+      on = tile_load_raw(ob_, p.dout.s1, k0 + qs(1) * kTile, T, tid);
     }
     if (s >= NS) {  // the slot of tile s - NS is free once every wave is past it
       __syncthreads();
       if constexpr (PF)
         store_tile(s, split_rows(qn), split_rows(on));
       else
-        store_tile(s, tile_load_split(qb_, p.q.s1, k0 + s * kTile, T, tid),
-                   tile_load_split(ob_, p.dout.s1, k0 + s * kTile, T, tid));
+        store_tile(s, tile_load_split(qb_, p.q.s1, k0 + qs(s) * kTile, T, tid),
+                   tile_load_split(ob_, p.dout.s1, k0 + qs(s) * kTile, T, tid));
       __syncthreads();
     }
     const bf16* qh = Qh + (s % NS) * kDTile;
@@ -521,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void mx_dkv(BandParams p) {
       dp = mfma(dt_row8(oh, 16 * j + c, 4 + g), vf1, dp);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int ql_ = s * kTile + 16 * j + 4 * g + r;  // query - k0
+        const int ql_ = qs(s) * kTile + 16 * j + 4 * g + r;  // query - k0
         const int t = k0 + ql_;
         const bool ok = t >= qlo && t <= qhi;
         float b2 = 0.f;
