@@ -492,7 +492,7 @@ def profile_kernels(n, dev):
     torch.cuda.synchronize()
     del caches, qkv
     # config-3 global block: n forward and n backward calls (the backward runs
-    # coef_from_out, gl_dq and gl_dkv)
+    # gl_dq, which forms the tau-mass coefficients, and gl_dkv)
     Bg, Hg, Tg = 4, 12, 2048
     q, k, v, do = ((torch.randn(Bg, Tg, Hg, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
                    for _ in range(4))

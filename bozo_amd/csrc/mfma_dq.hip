@@ -279,14 +279,14 @@ void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm)
   // every query tile's band spans <= 2 key blocks iff the window is <= 64
   const bool hold = !p.glob && p.win <= kTile;
   if (norm == NORM_MASS_ && !hold && p.coef_pre) {
-    const int64_t threads = (int64_t)p.B * p.T * p.H * 8;
-    hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, p);
 #ifndef TENSION_NO_GL_BWD
-    if (p.glob) {  // bias and dtau_local included
+    if (p.glob) {  // bias and dtau_local included; the coefficients formed in-kernel
       launch_gl_dq(p, st);
       return;
     }
 #endif
+    const int64_t threads = (int64_t)p.B * p.T * p.H * 8;
+    hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, p);
   }
   switch (norm) {
     case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, dtau, hold); break;

@@ -287,8 +287,10 @@ void gl_fwd(BandParams p) {
 
 // ---------------------------------------------------------------- backward
 //
-// Both backward kernels take the per-query tau-mass coefficients a_t = 1/m_t
-// and c_t = dO_t.out_t / m_t from the workspace (coef_from_out), so
+// The dQ kernel forms the per-query tau-mass coefficients a_t = 1/m_t and
+// c_t = dO_t.out_t / m_t of its tile from the forward's saved rows and
+// writes them to the workspace, where the dK/dV kernel (launched after it)
+// reads them, so
 //   dtau = a_t dP - c_t,   G = dtau * P (1 - P)   (P recomputed in fp32),
 // and use the forward's 2 x 2 wave split (32 queries x 32 keys per wave per
 // 64 x 64 block): every fragment read from LDS feeds two MFMAs, and the two
@@ -327,6 +329,13 @@ void gl_dq(BandParams p) {
   const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const bf16* gb_ = (const bf16*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
 
+  const bf16* ob_ = (const bf16*)p.out.p + b * p.out.s0 + h * p.out.s2;
+
+  // The tau-mass coefficients of this tile's queries, from the forward's
+  // saved rows: a_t = 1 / max(m_t, eps), c_t = (dO_t . out_t) a_t (0 when
+  // m_t < eps); each lane holds 16 of a row's 64 features of dO and out, the
+  // four lanes of a row add their parts.  They go to the workspace for the
+  // dK/dV kernel (written once, by the waves of key half 0).
   bf16x8 qf[2][2], gf[2][2];
   float ca[2], cc[2];
   const int64_t nws = (int64_t)p.B * p.T * p.H;
@@ -335,9 +344,24 @@ void gl_dq(BandParams p) {
     const int tq = t0 + 32 * qh + 16 * i + c;
     load_qfrag(qb_, p.q.s1, tq, T, g, qf[i]);
     load_qfrag(gb_, p.dout.s1, tq, T, g, gf[i]);
-    const int64_t wi = ((int64_t)b * p.T + (tq < T ? tq : T - 1)) * p.H + h;
-    ca[i] = ((const float*)p.ws)[wi];
-    cc[i] = ((const float*)p.ws)[nws + wi];
+    bf16x8 of[2];
+    load_qfrag(ob_, p.out.s1, tq, T, g, of);
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      dot = fmaf((float)of[0][e], (float)gf[i][0][e], dot);
+      dot = fmaf((float)of[1][e], (float)gf[i][1][e], dot);
+    }
+    dot = wave_sum_g(dot);
+    const int tr = tq < T ? tq : T - 1;
+    const float m = ld<float>(p.mass, b * p.mass.s0 + (int64_t)tr * p.mass.s1 + h * p.mass.s2);
+    ca[i] = 1.f / (m > kMassEps ? m : kMassEps);
+    cc[i] = m >= kMassEps ? dot * ca[i] : 0.f;
+    if (kh == 0 && g == 0 && tq < T) {
+      const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
+      ((float*)p.ws)[wi] = ca[i];
+      ((float*)p.ws)[nws + wi] = cc[i];
+    }
   }
   const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
   tile_async_src(ksrc, 0, Kb[0], wave);
