@@ -60,7 +60,7 @@ bool is_f64(const tension_buf* b) { return b && b->dtype == TENSION_F64; }
 // Kernels that address one (b, h) sequence through a 32-bit buffer view need
 // every row offset up to T + 128 rows to fit in 32 bits.
 bool rows_fit_u32(const tension_buf* b, int64_t T) {
-  return b && b->s[1] > 0 && (T + 128) * b->s[1] * 2 < ((int64_t)1 << 32);
+  return b && rows_fit_view(T + 128, b->s[1]);
 }
 
 bool any_f64(const tension_buf* a, const tension_buf* b, const tension_buf* c) {
@@ -85,8 +85,9 @@ int check_shape(Shape sh, double scale, bool* empty) {
   if (sh.B < 0 || sh.T < 0 || sh.H < 0 || sh.D <= 0)
     return fail(TENSION_ERR_ARG, "bad shape B=%lld T=%lld H=%lld D=%lld", (long long)sh.B, (long long)sh.T,
                 (long long)sh.H, (long long)sh.D);
-  if (sh.T > 0x3fffffff || sh.H > 0x3fffffff || sh.B > 0x3fffffff ||
-      sh.B * sh.H * sh.T > ((int64_t)1 << 40))
+  constexpr int64_t kMaxRows = (int64_t)1 << 40;
+  if (sh.T > 0x3fffffff || sh.H > 0x3fffffff || sh.B > 0x3fffffff || sh.D > 0x3fffffff ||
+      mul_cap(mul_cap(sh.B, sh.H, kMaxRows), sh.T, kMaxRows) < 0)
     return fail(TENSION_ERR_ARG, "shape too large");
   if (!(std::isfinite(scale) && scale != 0.0)) return fail(TENSION_ERR_ARG, "scale must be finite and non-zero");
   *empty = sh.B * sh.H * sh.T == 0;
@@ -194,10 +195,13 @@ int band_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, c
 // The workspace holds the per-query coefficients a_t, c_t of the tau-mass
 // backward (dtau = a_t * dP - c_t + dTau): fp32, or f64 when any activation
 // is f64.
+// -1 for sizes that check_shape rejects (negative, or B*T*H above 2^40).
 int64_t ws_bytes(int64_t B, int64_t T, int64_t H, int32_t dtype_acc, int32_t flags) {
   if (!(flags & TENSION_NORM_MASS)) return 0;
   const int64_t el = dtype_acc == TENSION_F64 ? 8 : 4;
-  return 2 * B * T * H * el;
+  constexpr int64_t kMaxRows = (int64_t)1 << 40;
+  const int64_t rows = mul_cap(mul_cap(B, T, kMaxRows), H, kMaxRows);
+  return rows < 0 ? -1 : 2 * rows * el;
 }
 
 int check_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
@@ -436,7 +440,7 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
                         const tension_buf* k_cache, const tension_buf* v_cache, const tension_buf* out,
                         const tension_buf* tau, const int32_t* pos_in, int32_t* pos_out, int64_t N, int64_t H,
                         int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
-  if (N < 0 || H < 0 || D <= 0 || D > 256 || W < 1 || W > 0x3fffffff || N * H > 0x3fffffff)
+  if (N < 0 || H < 0 || D <= 0 || D > 256 || W < 1 || W > 0x3fffffff || mul_cap(N, H, 0x3fffffff) < 0)
     return fail(TENSION_ERR_ARG, "decode: bad sizes N=%lld H=%lld D=%lld W=%lld", (long long)N, (long long)H,
                 (long long)D, (long long)W);
   if (!(std::isfinite(scale) && scale != 0.0)) return fail(TENSION_ERR_ARG, "scale must be finite and non-zero");
@@ -469,7 +473,7 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   };
   // the fast kernel reads each (n, h) cache slab through a buffer descriptor
   // of W * row_stride * 2 bytes (31-bit range, rows of at least 64 elements)
-  auto slab_fits = [&](const tension_buf* b) { return b->s[2] >= 64 && W * b->s[2] * 2 < ((int64_t)1 << 31); };
+  auto slab_fits = [&](const tension_buf* b) { return b->s[2] >= 64 && mul_cap(W, b->s[2], (1 << 30) - 1) >= 0; };
   const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 1024 && a16(q, false) &&
                     a16(k_new, false) && a16(v_new, false) && a16(out, false) && a16(k_cache, true) &&
                     a16(v_cache, true) && slab_fits(k_cache) && slab_fits(v_cache);
@@ -481,7 +485,7 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   const bool kf32 = !fast && !(flags & TENSION_FORCE_EXACT) && !(flags & TENSION_DECODE_SELF) && D == 64 &&
                     W <= 1024 && f16b(q, false) && f16b(k_new, false) && f16b(out, false) && f16b(k_cache, true) &&
                     a16(v_new, false) && a16(v_cache, true) && k_cache->s[2] >= 64 &&
-                    W * k_cache->s[2] * 4 < ((int64_t)1 << 31) && slab_fits(v_cache);
+                    mul_cap(W, k_cache->s[2], (1 << 29) - 1) >= 0 && slab_fits(v_cache);
   hipError_t e = hipSuccess;
   launch_decode(fast || kf32, is_f64(q) || is_f64(k_cache) || is_f64(v_cache), p, hs(stream), &e, kf32);
   return launched(e, "tension_decode_step");
@@ -494,9 +498,9 @@ int tension_rope(const tension_buf* x, const tension_buf* y, const float* cos, c
   TRY(check_shape(Shape{B, T, H, D}, 1.0, &empty));
   if (D % 2) return fail(TENSION_ERR_ARG, "rope: head dim must be even");
   if (pos_offset < 0) return fail(TENSION_ERR_ARG, "rope: negative position offset");
-  if (pos_offset + T > table_rows)
-    return fail(TENSION_ERR_ARG, "rope: table has %lld rows, positions up to %lld requested",
-                (long long)table_rows, (long long)(pos_offset + T));
+  if (T > table_rows || pos_offset > table_rows - T)
+    return fail(TENSION_ERR_ARG, "rope: table has %lld rows, positions %lld + [0, %lld) requested",
+                (long long)table_rows, (long long)pos_offset, (long long)T);
   if (empty) return ok();
   TRY(check_buf(x, "x", true, 3));
   TRY(check_buf(y, "y", true, 3));
@@ -525,7 +529,8 @@ namespace {
 int check_taus(const tension_buf* taus, int32_t L, int64_t B, int64_t T, int64_t H, int64_t W, Buf* out) {
   if (!taus) return fail(TENSION_ERR_ARG, "taus is required");
   if (L < 1 || L > kMaxLayers) return fail(TENSION_ERR_ARG, "tau export: L=%d outside [1, %d]", L, kMaxLayers);
-  if (B < 1 || T < 1 || H < 1 || W < 1 || T * W > 0x3fffffff || B * T * H * W > ((int64_t)1 << 40))
+  if (B < 1 || T < 1 || H < 1 || W < 1 || mul_cap(T, W, 0x3fffffff) < 0 ||
+      mul_cap(mul_cap(mul_cap(B, T, (int64_t)1 << 40), H, (int64_t)1 << 40), W, (int64_t)1 << 40) < 0)
     return fail(TENSION_ERR_ARG, "tau export: bad sizes B=%lld T=%lld H=%lld W=%lld", (long long)B,
                 (long long)T, (long long)H, (long long)W);
   for (int l = 0; l < L; ++l) {
@@ -566,7 +571,7 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B, int64_t
 }
 
 int64_t tension_aux_loss_partials(int64_t B, int64_t T, int64_t H) {
-  const int64_t nrow = B * T * H;
+  const int64_t nrow = mul_cap(mul_cap(B, T, (int64_t)1 << 40), H, (int64_t)1 << 40);
   return nrow > 0 ? aux_loss_blocks(nrow) : 0;
 }
 
@@ -620,7 +625,10 @@ int tension_bias_table_insert(const uint64_t* keys_in, const double* vals_in, in
 int tension_bias_build(const int32_t* content_ids, int64_t B, int64_t T, int64_t W, const uint64_t* table_keys,
                        const double* table_vals, int32_t log2cap, double alpha, const tension_buf* bias,
                        double* stats, tension_stream_t stream) {
-  if (B < 1 || T < 0 || W < 0 || T > 0x7fffffff / 2 || (W == 0 && T * T > 0x3fffffffffll))
+  // the launch covers T * K (K = W, or T for the global [B, T, T] bias)
+  // elements in 256-thread blocks: at most 2^38 of them
+  if (B < 1 || T < 0 || W < 0 || B > 0x3fffffff || T > 0x7fffffff / 2 || W > 0x3fffffff ||
+      mul_cap(T, W > 0 ? W : T, 0x3fffffffffll) < 0)
     return fail(TENSION_ERR_ARG, "bias build: bad sizes B=%lld T=%lld W=%lld", (long long)B, (long long)T,
                 (long long)W);
   if (log2cap < 1 || log2cap > 40) return fail(TENSION_ERR_ARG, "bias build: log2cap=%d outside [1, 40]", log2cap);

@@ -26,6 +26,21 @@ struct Buf {
   int64_t s0, s1, s2, s3;
 };
 
+// Host-side size arithmetic on caller-supplied int64 values: a * b when both
+// are non-negative and the product is at most `lim`, else -1 (an overflowing
+// product counts as too large, never as a wrapped small value).
+inline int64_t mul_cap(int64_t a, int64_t b, int64_t lim) {
+  int64_t r;
+  if (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r) || r > lim) return -1;
+  return r;
+}
+
+// Every byte offset of `rows` rows at a row stride of `s1` two-byte elements
+// fits a 32-bit buffer view (rows * s1 * 2 < 2^32).
+inline bool rows_fit_view(int64_t rows, int64_t s1) {
+  return s1 > 0 && mul_cap(rows, s1, ((int64_t)1 << 31) - 1) >= 0;
+}
+
 inline Buf make_buf(const tension_buf* b) {
   Buf r;
   r.p = b ? b->ptr : nullptr;

@@ -615,7 +615,7 @@ static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, b
     // bf16 dTau rows of 64 slots, 16-byte aligned: staged by the fast path
     const Buf& d = p.dtau;
     const bool rows16 = d.dt == TENSION_BF16 && ((d.s0 | d.s1 | d.s2) & 7) == 0 && ((uintptr_t)d.p & 15) == 0 &&
-                        (int64_t)(p.T + 2 * kTile) * d.s1 * 2 < (int64_t)1 << 32;
+                        rows_fit_view((int64_t)p.T + 2 * kTile, d.s1);
     if (p.win == kTile && p.T % kTile == 0 && rows16)
       go<NORM, false, true, true>(p, st, nwg);
     else

@@ -91,7 +91,8 @@ int tension_window_fwd(const tension_buf* q, const tension_buf* k,
                        int64_t H, int64_t D, int64_t W, double scale,
                        int32_t flags, tension_stream_t stream);
 
-/* Bytes of device workspace tension_window_bwd needs (0 if none). */
+/* Bytes of device workspace tension_window_bwd needs (0 if none; -1 for
+ * sizes the entry points reject: negative, or B*T*H above 2^40). */
 int64_t tension_window_bwd_workspace(int64_t B, int64_t T, int64_t H,
                                      int32_t dtype_acc, int32_t flags);
 
@@ -155,6 +156,7 @@ int tension_global_fwd(const tension_buf* q, const tension_buf* k,
                        int64_t H, int64_t D, int64_t Wl, double scale,
                        int32_t flags, tension_stream_t stream);
 
+/* Bytes of device workspace tension_global_bwd needs (-1 as above). */
 int64_t tension_global_bwd_workspace(int64_t B, int64_t T, int64_t H,
                                      int32_t dtype_acc, int32_t flags);
 

@@ -162,6 +162,48 @@ def test_bias_builder_validation(lib):
     assert build(p, 1, 0, 8, p, p, 4, 0.5, b, None, None) == lib.OK                   # empty context
 
 
+def test_size_products_do_not_wrap(lib):
+    """Sizes whose products overflow int64 (or whose casts to int would
+    truncate) are rejected as too large: never taken for an empty call
+    (OK without a launch) or for a small shape that passes the range checks."""
+    big, huge = 1 << 31, 1 << 40
+    # window: B * H * T = 2^90 wraps to 0 in int64
+    assert _fwd(lib, B=(1 << 30) - 1, T=(1 << 30) - 1, H=(1 << 30) - 1) == lib.ERR_ARG
+    assert _fwd(lib, B=1 << 29, T=1 << 29, H=1 << 30, D=64) == lib.ERR_ARG
+    # head dim past int range: (int)(2^32 + 64) == 64
+    assert _fwd(lib, D=(1 << 32) + 64) == lib.ERR_ARG
+    # decode: N * H = 2^71 wraps to 0 (was reported as an empty call)
+    q = _buf(strides=(64, 16, 1, 0))
+    c = _buf()
+    pos = ctypes.c_void_p(0x2000)
+    f = lib.lib().tension_decode_step
+    assert f(q, q, q, c, c, q, None, pos, None, big, huge, 64, 12, 8.0, 0, None) == lib.ERR_ARG
+    assert f(q, q, q, c, c, q, None, pos, None, 1 << 62, 4, 64, 12, 8.0, 0, None) == lib.ERR_ARG
+    # rope: pos_offset + T overflows past the table check
+    x = _buf(strides=(4096, 64, 16, 1))
+    tab = ctypes.c_void_p(0x5000)
+    rope = lib.lib().tension_rope
+    assert rope(x, x, tab, tab, 1024, 1, 16, 1, 16, (1 << 63) - 8, 0, None) == lib.ERR_ARG
+    assert rope(x, x, tab, tab, 8, 1, 16, 1, 16, 0, 0, None) == lib.ERR_ARG          # T > rows
+    # tau export: T * W and B * T * H * W wrap
+    arr = (lib.TensionBuf * 1)(_buf().contents)
+    stats = ctypes.c_void_p(0x3000)
+    hs = lib.lib().tension_tau_head_stats
+    assert hs(arr, 1, 1, 1 << 33, 2, 1 << 31, stats, 0, None) == lib.ERR_ARG
+    assert hs(arr, 1, 1 << 40, 1 << 20, 1 << 20, 1, stats, 0, None) == lib.ERR_ARG
+    # bias builder: B and W past int range; T * W past the launch range
+    p = ctypes.c_void_p(0x4000)
+    build = lib.lib().tension_bias_build
+    b = _buf(strides=(64, 8, 1, 0))
+    assert build(p, (1 << 32) + 1, 8, 8, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG
+    assert build(p, 1, 8, (1 << 32) + 8, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG
+    assert build(p, 1, 1 << 30, 1 << 30, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG
+    # size queries: -1 / 0 instead of a wrapped byte count
+    assert lib.lib().tension_window_bwd_workspace(big, big, big, lib.F32, lib.NORM_MASS) == -1
+    assert lib.lib().tension_global_bwd_workspace(-1, 8, 2, lib.F32, 0) == -1
+    assert lib.lib().tension_aux_loss_partials(big, big, big) == 0
+
+
 def test_no_cpu_fallback():
     from bozo_amd import causal_tension, global_tension
     x = torch.zeros(1, 8, 1, 16)
