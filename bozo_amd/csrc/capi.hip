@@ -609,9 +609,9 @@ int tension_aux_loss_bwd(const tension_buf* taus, const tension_buf* dtaus, int3
 int tension_bias_table_insert(const uint64_t* keys_in, const double* vals_in, int64_t n, uint64_t* table_keys,
                               double* table_vals, int32_t log2cap, tension_stream_t stream) {
   if (log2cap < 1 || log2cap > 40) return fail(TENSION_ERR_ARG, "bias table: log2cap=%d outside [1, 40]", log2cap);
-  if (n < 0 || 2 * n > ((int64_t)1 << log2cap))
-    return fail(TENSION_ERR_ARG, "bias table: %lld keys need a capacity of at least %lld", (long long)n,
-                (long long)(2 * n));
+  if (n < 0 || n > ((int64_t)1 << log2cap) / 2)
+    return fail(TENSION_ERR_ARG, "bias table: %lld keys need a capacity of at least twice that (have 2^%d)",
+                (long long)n, log2cap);
   if (n == 0) return ok();
   if (!keys_in || !vals_in || !table_keys || !table_vals) return fail(TENSION_ERR_ARG, "bias table: null pointer");
   BiasTableParams p;

@@ -198,6 +198,9 @@ def test_size_products_do_not_wrap(lib):
     assert build(p, (1 << 32) + 1, 8, 8, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG
     assert build(p, 1, 8, (1 << 32) + 8, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG
     assert build(p, 1, 1 << 30, 1 << 30, p, p, 4, 0.5, b, None, None) == lib.ERR_ARG
+    # bias table: 2 * n wraps negative below any capacity
+    ins = lib.lib().tension_bias_table_insert
+    assert ins(p, p, (1 << 63) - 1, p, p, 40, None) == lib.ERR_ARG
     # size queries: -1 / 0 instead of a wrapped byte count
     assert lib.lib().tension_window_bwd_workspace(big, big, big, lib.F32, lib.NORM_MASS) == -1
     assert lib.lib().tension_global_bwd_workspace(-1, 8, 2, lib.F32, 0) == -1
