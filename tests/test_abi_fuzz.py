@@ -12,10 +12,10 @@ one of its sizes is 0.  A size product that wraps (B * H * T = 2^90 read as
 
 The premise needs the absence of a GPU: on a machine with one, calls that pass
 validation would launch kernels on the fake pointers used here, so the module
-skips itself there.  Built with host sanitizers
-(-Xarch_host -fsanitize=address on every hipcc line), the same calls also
-check the validation code for out-of-bounds reads and writes, and with
--fsanitize=undefined for signed overflow in the size arithmetic.
+skips itself there.  Against a library built with host sanitizers
+(`-Xarch_host -fsanitize=address`, or `=undefined`, on every hipcc line) the
+same calls also check the validation code for out-of-bounds accesses and for
+signed overflow in its size arithmetic.
 """
 import ctypes as C
 import os
