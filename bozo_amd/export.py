@@ -84,6 +84,8 @@ def _taus_arg(taus: Sequence[Tensor]):
             raise ValueError("every tau must be [B, T, H, W] of one shape")
         if not t.is_cuda:
             raise RuntimeError("tau export runs on the GPU; got a CPU tensor")
+        if t.device != taus[0].device:
+            raise ValueError(f"every tau must be on {taus[0].device}, got one on {t.device}")
     rows = [t if t.stride(-1) == 1 else t.contiguous() for t in taus]
     arr = (L.TensionBuf * len(rows))(*[L.buf(t).contents for t in rows])
     return arr, rows, shape

@@ -486,7 +486,8 @@ def tension_aux_losses(all_tensions: list, window_groups: Optional[dict] = None)
         return z, z, z
     shape = tuple(all_tensions[0].shape)
     fused = (all_tensions[0].is_cuda and len(all_tensions) <= 32 and shape[-1] <= 64
-             and all(tuple(t.shape) == shape and t.is_cuda and t.dtype in _AUX_DTYPES for t in all_tensions))
+             and all(tuple(t.shape) == shape and t.device == all_tensions[0].device and t.dtype in _AUX_DTYPES
+                     for t in all_tensions))
     if not fused:
         return (tension_diversity_loss(all_tensions, window_groups),
                 constraint_consistency_loss(all_tensions), tension_entropy_loss(all_tensions))

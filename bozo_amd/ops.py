@@ -46,6 +46,13 @@ def _on_gpu(*ts: Optional[Tensor]) -> None:
                 "the CPU reference lives in oracle/ and is test infrastructure")
 
 
+def _same_device(ref: Tensor, *ts: Optional[Tensor]) -> None:
+    """The kernels read every operand on the device of the first one."""
+    for t in ts:
+        if t is not None and t.device != ref.device:
+            raise ValueError(f"all tensors must be on {ref.device}, got one on {t.device}")
+
+
 def _rows(t: Optional[Tensor]) -> Optional[Tensor]:
     """Unit innermost stride is all the kernels need."""
     if t is None:
@@ -161,6 +168,7 @@ def causal_tension(Q: Tensor, K: Tensor, V: Tensor, window: int, scale: float,
     if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
         raise ValueError(f"Q, K, V must share one [B, T, H, HD] shape, got "
                          f"{tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
+    _same_device(Q, K, V, bias)
     if normalize not in _NORMS:
         raise ValueError(f"normalize must be one of {list(_NORMS)}")
     if int(window) < 1:
@@ -243,6 +251,7 @@ def global_tension(Q: Tensor, K: Tensor, V: Tensor, scale: float,
     _on_gpu(Q, K, V, bias)
     if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
         raise ValueError("Q, K, V must share one [B, T, H, HD] shape")
+    _same_device(Q, K, V, bias)
     if torch.compiler.is_compiling():  # the registered op, which torch.compile traces through
         B, T = Q.shape[:2]
         Bias = _side(bias, Q)
@@ -260,6 +269,30 @@ _DECODE_NORMS = {True: L.NORM_MASS, "mass": L.NORM_MASS, "count": L.NORM_COUNT,
                  False: 0, None: 0, "raw": 0}
 
 
+def _check_decode_operands(q, k_new, v_new, k_cache, v_cache, pos_in, pos_out, tau) -> None:
+    """Shapes, devices and counter dtypes of one decode step.  The library
+    sees strides only, so a cache, row or counter array smaller than q's
+    [N, H, D] implies would be read past its end on the device."""
+    if q.dim() != 3:
+        raise ValueError(f"q must be [N, H, D], got {tuple(q.shape)}")
+    N, H, D = q.shape
+    if k_new.shape != q.shape or v_new.shape != q.shape:
+        raise ValueError(f"k_new, v_new must be {tuple(q.shape)} like q, got "
+                         f"{tuple(k_new.shape)}, {tuple(v_new.shape)}")
+    if k_cache.dim() != 4 or (k_cache.shape[0], k_cache.shape[1], k_cache.shape[3]) != (N, H, D) \
+            or v_cache.shape != k_cache.shape:
+        raise ValueError(f"k_cache, v_cache must be [N, H, W, D] = [{N}, {H}, W, {D}] alike, got "
+                         f"{tuple(k_cache.shape)}, {tuple(v_cache.shape)}")
+    if pos_in.dtype != torch.int32 or (pos_out is not None and pos_out.dtype != torch.int32):
+        raise TypeError("pos tensors must be int32")
+    for name, t in (("pos_in", pos_in), ("pos_out", pos_out)):
+        if t is not None and (tuple(t.shape) != (N,) or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous [N] = [{N}] tensor, got {tuple(t.shape)}")
+    if tau is not None and tuple(tau.shape) != (N, H, k_cache.shape[2]):
+        raise ValueError(f"tau must be [N, H, W] = [{N}, {H}, {k_cache.shape[2]}], got {tuple(tau.shape)}")
+    _same_device(q, k_new, v_new, k_cache, v_cache, pos_in, pos_out, tau)
+
+
 def decode_step(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cache: Tensor,
                 pos_in: Tensor, pos_out: Optional[Tensor], scale: float,
                 normalize=True, tau: Optional[Tensor] = None, include_self: bool = False) -> Tensor:
@@ -270,11 +303,10 @@ def decode_step(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cach
     (number of keys) or False / None (raw sum).  ``include_self``: the new
     token is a key too (a global layer's step; no tau then).  Returns out
     [N,H,D] in q.dtype."""
-    _on_gpu(q, k_new, v_new, k_cache, v_cache, pos_in)
+    _on_gpu(q, k_new, v_new, k_cache, v_cache, pos_in, pos_out, tau)
+    _check_decode_operands(q, k_new, v_new, k_cache, v_cache, pos_in, pos_out, tau)
     N, H, D = q.shape
     W = k_cache.shape[2]
-    if pos_in.dtype != torch.int32 or (pos_out is not None and pos_out.dtype != torch.int32):
-        raise TypeError("pos tensors must be int32")
     if normalize not in _DECODE_NORMS:
         raise ValueError(f"normalize must be one of {list(_DECODE_NORMS)}")
     flags = _DECODE_NORMS[normalize] | (L.DECODE_SELF if include_self else 0)
@@ -359,8 +391,11 @@ def rope(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int = 0,
     _on_gpu(x, cos, sin)
     if cos.dtype != torch.float32 or sin.dtype != torch.float32:
         raise TypeError("cos/sin tables must be float32")
+    if x.dim() != 4:
+        raise ValueError(f"x must be [B, T, H, D], got {tuple(x.shape)}")
+    _same_device(x, cos, sin)
     T, half = x.shape[1], x.shape[-1] // 2
-    if cos.shape[-1] != half or cos.shape[0] < pos_offset + T or sin.shape != cos.shape:
+    if cos.dim() != 2 or cos.shape[-1] != half or cos.shape[0] < pos_offset + T or sin.shape != cos.shape:
         raise ValueError("cos/sin tables do not cover the requested positions")
     if torch.compiler.is_compiling():  # the registered op, which torch.compile traces through
         return torch.ops.bozo.rope(x, cos.contiguous(), sin.contiguous(), int(pos_offset),
