@@ -11,8 +11,8 @@ one of its sizes is 0.  A size product that wraps (B * H * T = 2^90 read as
 -1 / 0 or a non-negative byte count, never a wrapped negative one.
 
 The premise needs the absence of a GPU: on a machine with one, calls that pass
-validation would launch kernels on the fake pointers used here, so the module
-skips itself there.  Against a library built with host sanitizers
+validation would launch kernels on the fake pointers used here, so its tests
+skip themselves there.  Against a library built with host sanitizers
 (`-Xarch_host -fsanitize=address`, or `=undefined`, on every hipcc line) the
 same calls also check the validation code for out-of-bounds accesses and for
 signed overflow in its size arithmetic.
@@ -24,6 +24,7 @@ import random
 import numpy as np
 import pytest
 import torch
+
 
 @pytest.fixture(scope="module")
 def lib():
