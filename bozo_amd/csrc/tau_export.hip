@@ -38,7 +38,7 @@ constexpr int kStatVals = 128;  // values per thread of the register-resident se
 // The next order statistic after xk (xk again when more than k + 1 values
 // are <= xk, else the smallest value above it: le / gt are this thread's
 // counts), the interpolated quantile and the head's four statistics.
-__device__ void head_quantile_out(const TauStatParams& p, int l, int h, int64_t n, double g, int64_t k, float xk,
+__device__ void head_quantile_out(const TauStatParams& p, int l, int h, int64_t n, float g, int64_t k, float xk,
                                   double le, float gt, double sum, double rmax, double rarg, int T, double* red) {
   const int tid = threadIdx.x;
   le = block_sum(le, red);
@@ -50,10 +50,13 @@ __device__ void head_quantile_out(const TauStatParams& p, int l, int h, int64_t 
     float gm = gred[0];
     for (int i = 1; i < kStatThreads / 64; ++i) gm = fminf(gm, gred[i]);
     const float xk1 = (k + 1 >= n || le >= (double)(k + 2)) ? xk : gm;
-    const double frac = g - (double)k;
+    // numpy's linear interpolation in the values' dtype (float32), each step
+    // rounded on its own: a + (b - a) t, or b - (b - a) (1 - t) for t >= 0.5
+    const float t = __fsub_rn(g, (float)k);
+    const float d = __fsub_rn(xk1, xk);
     float* o = p.stats + ((int64_t)l * p.H + h) * 4;
     o[0] = (float)(sum / (double)n);
-    o[1] = (float)((double)xk + frac * ((double)xk1 - (double)xk));
+    o[1] = t >= 0.5f ? __fsub_rn(xk1, __fmul_rn(d, __fsub_rn(1.f, t))) : __fadd_rn(xk, __fmul_rn(d, t));
     o[2] = (float)(rarg / (double)T);
     o[3] = (float)(rmax / (double)T);
   }
@@ -64,7 +67,7 @@ __device__ void head_quantile_out(const TauStatParams& p, int l, int h, int64_t 
 // One workgroup per (layer, head): mean of tau over (t, w), mean over t of
 // the row maximum and of its first arg-max over w, and the 0.99 quantile of
 // all T*W values with linear interpolation between order statistics k and
-// k+1 (k = floor(0.99 (n - 1))).  The order statistics come from a radix
+// k+1 (k = floor(0.99 (n - 1)), in float32 as numpy computes it).  The order statistics come from a radix
 // select over the float bit patterns (tau >= 0, so they order as unsigned
 // integers): four 8-bit passes with an LDS histogram, then one pass for the
 // next value up.
@@ -81,7 +84,11 @@ void tau_head_stats_kernel(TauStatParams p) {
 
   double sum = 0.0, rmax = 0.0, rarg = 0.0;
   const int64_t n = (int64_t)T * W;
-  const double g = 0.99 * (double)(n - 1);
+  // The reference takes np.quantile(vals, 0.99) of float32 values
+  // (head_filter.py:108-113).  numpy >= 2 keeps a Python-float q in the
+  // array's dtype, so q, the rank (n - 1) q and the interpolation weight are
+  // float32: the rank is 2034.45007 for n = 2056, not 2034.45.
+  const float g = __fmul_rn((float)(n - 1), 0.99f);
   const int64_t k = (int64_t)g;
   if (tid == 0) {
     sel[0] = 0u;

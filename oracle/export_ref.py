@@ -7,7 +7,8 @@ product imports it.
 Follows (reference ``ts_bridge/``):
 * ``head_stats``      <- ``head_filter.py:98-130`` (``profile_heads``: batch
   mean, then per head: mean, ``np.quantile(.., 0.99)``, mean arg-max over w,
-  mean max over w) and, with ``valid_only``, ``corpus_profile.py:58-98``
+  mean max over w; the quantile restated in ``quantile99_f32``) and, with
+  ``valid_only``, ``corpus_profile.py:58-98``
   (cells with t + w < W zeroed first; no mean there, computed anyway);
 * ``classify``        <- ``head_filter.py:74-90`` (thresholds 0.40, 0.35,
   0.7 W, 0.3 W);
@@ -26,6 +27,27 @@ MAX_TAU_FLOOR = 0.40
 CONCENTRATION = 0.35
 
 
+def quantile99_f32(vals) -> float:
+    """``np.quantile(vals, 0.99)`` of float32 values as numpy >= 2 computes
+    it (the reference's call at head_filter.py:113; requirements.txt pins
+    only numpy>=1.24): a Python-float q is cast to the array's dtype, so q,
+    the rank g = (n - 1) q, its fractional part t and the linear
+    interpolation a + (b - a) t (b - (b - a)(1 - t) for t >= 0.5) are each
+    rounded to float32 -- g = 2034.45007 for n = 2056, not 2034.45.  numpy
+    1.x formed the rank in float64; the two differ by about 1e-4 of the gap
+    between the two order statistics."""
+    s = np.sort(np.asarray(vals, dtype=np.float32).ravel())
+    n = s.size
+    g = np.float32(n - 1) * np.float32(0.99)
+    k = int(np.floor(g))
+    t = np.float32(g - np.float32(k))
+    a, b = s[k], s[min(k + 1, n - 1)]
+    d = np.float32(b - a)
+    if t >= 0.5:
+        return float(np.float32(b - np.float32(d * np.float32(np.float32(1) - t))))
+    return float(np.float32(a + np.float32(d * t)))
+
+
 def head_stats(taus, valid_only: bool = False) -> np.ndarray:
     """taus: list of L arrays [B,T,H,W].  Returns [L,H,4] = mean, p99,
     peak_pos, concentration."""
@@ -39,7 +61,7 @@ def head_stats(taus, valid_only: bool = False) -> np.ndarray:
         rows = []
         for h in range(H):
             vals = t[:, h, :]
-            rows.append([float(vals.mean()), float(np.quantile(vals, 0.99)),
+            rows.append([float(vals.mean()), quantile99_f32(vals),
                          float(vals.argmax(axis=-1).mean()), float(vals.max(axis=-1).mean())])
         out.append(rows)
     return np.asarray(out, dtype=np.float64)

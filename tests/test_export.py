@@ -57,6 +57,40 @@ def test_head_stats_vs_loops(valid_only, B):
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)
 
 
+def test_quantile99_f32_rank_and_lerp():
+    """The restated quantile keeps q, the rank and the interpolation in
+    float32 (numpy >= 2 on float32 data): for n = 2056 the rank is
+    float32(2055 * 0.99f) = 2034.45007, not 2034.45, which moves the result
+    by 0.00007 of the gap between the two order statistics."""
+    v = np.concatenate([np.zeros(2034), [0.5859375, 0.62402344], np.ones(20)]).astype(np.float32)
+    g32 = np.float32(2055) * np.float32(0.99)
+    assert float(g32) == 2034.4500732421875
+    got = X.quantile99_f32(v)
+    assert got == float(np.float32(np.float32(0.5859375) + np.float32(np.float32(0.62402344 - 0.5859375) *
+                                                                       np.float32(g32 - 2034))))
+    f64_rank = 0.5859375 + 0.45 * (0.62402344 - 0.5859375)  # the float64-rank value (numpy 1.x)
+    assert abs(got - f64_rank) > 1e-6 and abs(got - f64_rank) < 1e-4 * (0.62402344 - 0.5859375)
+    # t >= 0.5 takes numpy's other form b - (b - a)(1 - t): n = 11 gives g = 9.9
+    w = np.arange(11, dtype=np.float32) / np.float32(7)
+    t = np.float32(np.float32(10) * np.float32(0.99)) - np.float32(9)
+    assert t >= 0.5
+    assert X.quantile99_f32(w) == float(np.float32(w[10] - np.float32((w[10] - w[9]) * (np.float32(1) - t))))
+
+
+@pytest.mark.skipif(int(np.__version__.split(".")[0]) < 2, reason="numpy 1.x forms the rank in float64")
+def test_quantile99_f32_is_numpy_quantile():
+    """The restatement equals the call the reference makes, np.quantile(vals,
+    0.99) on float32 values, under this numpy (>= 2): random sizes, skewed
+    values, ties."""
+    r = np.random.default_rng(7)
+    for n in list(range(1, 200)) + [2056, 4097, 65536]:
+        for rep in range(3):
+            v = (r.random(n) ** int(r.integers(1, 8))).astype(np.float32)
+            if rep == 2:
+                v = (np.round(v * 8) / 8).astype(np.float32)
+            assert X.quantile99_f32(v) == float(np.quantile(v, 0.99)), (n, rep)
+
+
 def test_gini_vs_pairwise_definition():
     r = np.random.default_rng(3)
     agg = (r.random((9, 5)) ** 3).astype(np.float32)

@@ -29,7 +29,7 @@ def test_head_stats_vs_oracle(dev, dtype, B, valid_only):
     got = E.head_stats([t.to(dev) for t in taus], valid_only).cpu().numpy()
     ref = X.head_stats([t.float().numpy() for t in taus], valid_only)
     assert np.allclose(got[..., [0, 2, 3]], ref[..., [0, 2, 3]], rtol=1e-5, atol=1e-6)
-    assert np.max(np.abs(got[..., 1] - ref[..., 1])) <= 2e-6
+    assert np.max(np.abs(got[..., 1] - ref[..., 1])) <= 1e-7
 
 
 def test_head_stats_many_ties_and_tiny(dev):
