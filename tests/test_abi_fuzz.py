@@ -38,6 +38,7 @@ def lib():
 
 
 _HOST = [np.zeros(64, np.uint8) for _ in range(16)]  # pointer targets; never launched on
+_BIG = np.zeros(4096, np.uint8)  # 256-byte aligned pointer target of the valid descriptors
 
 
 class _Gen:
@@ -139,3 +140,75 @@ def test_size_queries_never_wrap(lib):
             if min(B, T, H) < 0:
                 assert v <= 0
         assert h.tension_aux_loss_partials(B, T, H) >= 0
+
+
+def _valid_calls(L, r):
+    """Descriptors that pass validation (float dtypes, unit innermost stride,
+    one 256-byte aligned host buffer) with extreme sizes and strides, so the
+    host code behind it -- kernel selection, 32-bit view checks, launch
+    geometry -- runs on them; without a GPU each such call ends in
+    TENSION_ERR_LAUNCH."""
+    base = (_BIG.ctypes.data + 255) // 256 * 256
+    sizes = [1, 2, 3, 17, 63, 64, 65, 128, 1000, 1024, 4096, 65536, (1 << 20) + 3, (1 << 30) - 1]
+    strides = [1, 8, 64, 768, 1536, 1 << 20, 1 << 31, (1 << 40) + 8, 1 << 62]
+
+    def b(unit=3, dt=None):
+        if r.random() < 0.1:
+            return None
+        x = L.TensionBuf()
+        x.ptr = base
+        x.dtype = dt if dt is not None else r.choice([L.F32, L.BF16, L.F16, L.F64])
+        for i in range(4):
+            x.s[i] = 1 if i == unit else r.choice(strides)
+        return C.pointer(x)
+
+    def taus():
+        x = L.TensionBuf(C.c_void_p(base), L.F32, 0, (C.c_int64 * 4)(r.choice(strides), r.choice(strides),
+                                                                        r.choice(strides), 1))
+        return (L.TensionBuf * 1)(x)
+
+    d = lambda: r.choice(sizes)  # noqa: E731
+    f = lambda: r.choice([0, 1, 2, 4, 8, 16, 32, 64, 65, 66, 96])  # noqa: E731
+    p = base
+
+    def decode():
+        dk = r.choice([L.F32, L.BF16, L.F64])
+        dv = r.choice([dk, L.BF16])
+        return (b(2, dk), b(2, dk), b(2, dv), b(3, dk), b(3, dv), b(2, dk), None if r.random() < 0.5 else b(2, dk),
+                p, p + 64, r.choice([1, 3, 64, 1 << 14]), r.choice([1, 16, 1 << 10]), r.choice([32, 64, 128]),
+                r.choice([1, 64, 256, 1024, 4096, 1 << 20]), 8.0, r.choice([0, 1, 2, 16, 17]), None)
+
+    return {
+        "tension_window_fwd": lambda: (b(), b(), b(), b(), b(), b(2), b(), d(), d(), d(), r.choice([16, 32, 64, 128]),
+                                       d(), 8.0, f(), None),
+        "tension_window_bwd": lambda: (b(), b(), b(), b(), b(), b(2), b(), b(), b(), p, d(), d(), d(), r.choice([32, 64]),
+                                       d(), 8.0, f(), None),
+        "tension_global_fwd": lambda: (b(), b(), b(), b(), b(), b(2), b(2), d(), d(), d(), 64, d(), 8.0, f(), None),
+        "tension_global_bwd": lambda: (b(), b(), b(), b(), b(), b(2), b(), b(2), b(), b(), b(), p, d(), d(), d(), 64,
+                                       d(), 8.0, f(), None),
+        "tension_decode_step": decode,
+        "tension_rope": lambda: (b(), b(), p, p, r.choice([d(), 1 << 40]), d(), d(), d(), r.choice([16, 64, 128]),
+                                 r.choice([0, 5, 1 << 40]), 0, None),
+        "tension_tau_head_stats": lambda: (taus(), 1, d(), d(), d(), r.choice([1, 8, 64, 100]), p, f(), None),
+        "tension_aux_loss_fwd": lambda: (taus(), 1, d(), d(), d(), r.choice([1, 8, 64]), p, None),
+        "tension_bias_build": lambda: (p, d(), d(), r.choice([0, 8, 64, d()]), p, p, r.choice([4, 20, 40]), 0.5, b(1),
+                                       p, None),
+    }
+
+
+def test_valid_descriptors_reach_launch_cleanly(lib):
+    """Non-empty calls with valid descriptors never return OK without a GPU
+    (every one must end in an argument error or the failed launch), and a
+    share of each entry point's calls gets through validation to the
+    launch code."""
+    r = random.Random(11)
+    h = lib.lib()
+    for name, make in _valid_calls(lib, r).items():
+        fn = getattr(h, name)
+        launched = 0
+        for i in range(800):
+            res = fn(*make())
+            assert res in (lib.ERR_ARG, lib.ERR_UNSUPPORTED, lib.ERR_LAUNCH), (name, i, res)
+            assert h.tension_last_error(), (name, i)
+            launched += res == lib.ERR_LAUNCH
+        assert launched >= 40, f"{name}: only {launched} of 800 calls passed validation"
