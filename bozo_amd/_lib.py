@@ -108,6 +108,8 @@ def buf(t: torch.Tensor | None):
     code = DTYPE_CODE.get(t.dtype)
     if code is None:
         raise TypeError(f"unsupported dtype {t.dtype}")
+    if t.dim() > 4:
+        raise ValueError(f"a tension_buf describes at most 4 dimensions, got {t.dim()}")
     s = list(t.stride()) + [0] * (4 - t.dim())
     b = TensionBuf(ctypes.c_void_p(t.data_ptr()), code, 0, (ctypes.c_int64 * 4)(*s[:4]))
     return ctypes.pointer(b)

@@ -55,3 +55,12 @@ def test_same_device():
     ops._same_device(a, a, None, torch.ones(3))
     with pytest.raises(ValueError, match="all tensors must be on"):
         ops._same_device(a, a, torch.zeros(2, device="meta"))
+
+
+def test_buf_refuses_more_than_four_dimensions():
+    from bozo_amd import _lib as L
+    assert L.buf(torch.zeros(2, 2, 2, 2)) is not None
+    with pytest.raises(ValueError, match="at most 4"):
+        L.buf(torch.zeros(2, 2, 2, 2, 2))
+    with pytest.raises(TypeError, match="unsupported dtype"):
+        L.buf(torch.zeros(3, dtype=torch.int32))
