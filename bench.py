@@ -726,12 +726,14 @@ def kernel_counters(n=16):
 
 
 def bench_global(dev, steps, warmup):
-    """Config 3: global block B4 H12 T2048 d64 bf16, fwd+bwd (MFMA-bound)."""
+    """Config 3: global block B4 H12 T2048 d64 bf16, fwd+bwd (MFMA-bound),
+    over 4 rotated input sets (4 x 50 MB of Q, K, V, dO plus their
+    gradients and the forward's out: more than the 256 MB Infinity Cache)."""
     from bozo_amd import global_tension
     B, H, T, D = 4, 12, 2048, 64
     g = torch.Generator(device=dev).manual_seed(2)
     sets = []
-    for _ in range(2):
+    for _ in range(4):
         q, k, v = ((torch.randn(B, T, H, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
                    .requires_grad_(True) for _ in range(3))
         sets.append(dict(Q=q, K=k, V=v, dO=torch.randn(B, T, H, D, device=dev, generator=g)
@@ -746,7 +748,7 @@ def bench_global(dev, steps, warmup):
     ms = time_units(run, steps, warmup, "global")
     pairs = B * H * T * (T + 1) // 2
     flops = 12 * D * pairs
-    return {"config": "global block B4 H12 T2048 d64 bf16 fwd+bwd (config 3)",
+    return {"config": "global block B4 H12 T2048 d64 bf16 fwd+bwd, 4 rotated input sets (config 3)",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
             "alg_flops": flops, "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
             "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}

@@ -30,6 +30,9 @@ TAU_VALID_ONLY = 1 << 5
 # bytes of the fixed device scratch of tension_global_bwd_noalloc
 NOALLOC_SCRATCH_BYTES = 8 << 20
 
+# kernel families (tension_last_kernel)
+KERNEL_EXACT, KERNEL_MFMA, KERNEL_SPLIT_BF16, KERNEL_SPLIT_F32 = 0, 1, 2, 3
+
 # status codes
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 _STATUS = {ERR_ARG: "bad argument", ERR_UNSUPPORTED: "unsupported", ERR_LAUNCH: "launch failure"}
@@ -68,6 +71,7 @@ SIGNATURES = {
     "tension_bias_build": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _f64, BufP, _vp, _vp]),
     "tension_last_error": (ctypes.c_char_p, []),
     "tension_version": (ctypes.c_char_p, []),
+    "tension_last_kernel": (_i32, []),
 }
 
 _lib = None

@@ -17,6 +17,10 @@
 
 namespace tension {
 
+// Launcher result for a grid beyond 2^31 - 1 workgroups (0: launched, -1: no
+// kernel for the request).
+constexpr int kGridTooLarge = -2;
+
 struct BandParams {
   Buf q, k, v;
   Buf out, tau, bias, mass;

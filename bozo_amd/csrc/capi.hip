@@ -129,27 +129,48 @@ bool aligned_f32_rows(const tension_buf* b) {
   return (b->s[0] % 4 == 0) && (b->s[1] % 4 == 0) && (b->s[2] % 4 == 0);
 }
 
-// The reference's autocast flow (float32 rotated Q / K, bfloat16 V, float32
-// out and dOut) on the split-operand MFMA kernels: local windows W <= 64,
-// head dim 64.
-bool mixed_ok(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* bias,
-              int64_t D, int64_t W, int flags, bool global) {
-  if (global || (flags & TENSION_FORCE_EXACT) || D != 64 || W < 1 || W > 64) return false;
-  if (!aligned_f32_rows(q) || !aligned_f32_rows(k) || !aligned_bf16_rows(v)) return false;
-  return !bias || bias->dtype == TENSION_F32;
+// Split-operand MFMA kernels (split_band.h), head dim 32 or 64, any window,
+// local or global: float32 Q / K with a bfloat16 V -- the reference's
+// autocast flow, float32 out / dOut / dQ / dK, bf16 dV -- on three bf16
+// terms per float32 value (SPLIT_F32), or bf16 everywhere (SPLIT_BF16) for
+// what the dedicated bf16 kernels (head dim 64) do not take.
+enum { SPLIT_NONE = 0, SPLIT_BF16 = 1, SPLIT_F32 = 2 };
+
+int split_kind(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* bias,
+               int64_t D, int flags) {
+  if ((flags & TENSION_FORCE_EXACT) || (D != 32 && D != 64)) return SPLIT_NONE;
+  if (!aligned_bf16_rows(v) || (bias && bias->dtype != TENSION_F32)) return SPLIT_NONE;
+  if (aligned_f32_rows(q) && aligned_f32_rows(k)) return SPLIT_F32;
+  if (aligned_bf16_rows(q) && aligned_bf16_rows(k)) return SPLIT_BF16;
+  return SPLIT_NONE;
 }
 
-enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_MIXED = 2 };
+// A further operand of a split kernel: float32 rows with SPLIT_F32, bf16
+// rows with SPLIT_BF16 (outputs and gradients of Q / K / out).
+bool split_rows(int kind, const tension_buf* b) {
+  return kind == SPLIT_F32 ? aligned_f32_rows(b) : aligned_bf16_rows(b);
+}
+
+enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_SPLIT_BF16 = 2, KERNEL_SPLIT_F32 = 3 };
+
+thread_local int g_last_kernel = -1;
 
 int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_t stream, const char* what) {
   hipError_t e = hipSuccess;
-  int r = kind == KERNEL_MIXED ? launch_mixed(phase, p, hs(stream), &e)
-          : kind == KERNEL_MFMA ? launch_mfma(phase, p, hs(stream), &e)
-                                : launch_exact(phase, f64, p, hs(stream), &e);
+  int r = kind == KERNEL_SPLIT_F32    ? launch_split(phase, true, p, hs(stream), &e)
+          : kind == KERNEL_SPLIT_BF16 ? launch_split(phase, false, p, hs(stream), &e)
+          : kind == KERNEL_MFMA       ? launch_mfma(phase, p, hs(stream), &e)
+                                      : launch_exact(phase, f64, p, hs(stream), &e);
+  if (r == kGridTooLarge)
+    return fail(TENSION_ERR_UNSUPPORTED, "%s: B*H*T = %lld rows need a grid beyond 2^31 - 1 workgroups", what,
+                (long long)p.B * p.H * p.T);
   if (r != 0)
     return fail(TENSION_ERR_UNSUPPORTED, "%s: head dim %d not supported (exact path: 8,16,32,64,128)", what, p.D);
+  g_last_kernel = kind;
   return launched(e, what);
 }
+
+int split_kernel(int kind) { return kind == SPLIT_F32 ? KERNEL_SPLIT_F32 : KERNEL_SPLIT_BF16; }
 
 // ---------------------------------------------------------------- forward
 
@@ -186,8 +207,9 @@ int band_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, c
   p.out = make_buf(out); p.tau = make_buf(tau); p.bias = make_buf(bias); p.mass = make_buf(mass);
   const bool mf = !(flags & TENSION_FORCE_EXACT) && sh.D == 64 && aligned_bf16_rows(q) && aligned_bf16_rows(k) &&
                   aligned_bf16_rows(v) && aligned_bf16_rows(out) && (!bias || bias->dtype == TENSION_F32);
-  const bool mx = !mf && mixed_ok(q, k, v, bias, sh.D, Wparam, flags, global) && aligned_f32_rows(out);
-  return run_band(0, mx ? KERNEL_MIXED : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream, what);
+  const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, out);
+  return run_band(0, sp ? split_kernel(sk) : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream, what);
 }
 
 // ---------------------------------------------------------------- backward
@@ -262,8 +284,8 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
   BandParams p = bwd_params(q, k, v, dout, dtau, bias, ws, sh, Wparam, scale, flags, global);
   p.dq = make_buf(dq);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dq, nullptr, sh.D, flags);
-  const bool mx = !mf && mixed_ok(q, k, v, bias, sh.D, Wparam, flags, global) && aligned_f32_rows(dout) &&
-                  aligned_f32_rows(dq);
+  const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dq);
   if (mf && out && mass) {
     TRY(check_buf(out, "out", true, 3));
     TRY(check_buf(mass, "mass", true, -1));
@@ -273,7 +295,7 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
       p.coef_pre = 1;
     }
   }
-  return run_band(1, mx ? KERNEL_MIXED : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
+  return run_band(1, sp ? split_kernel(sk) : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
                   global ? "tension_global_bwd(dq)" : "tension_window_bwd_dq");
 }
 
@@ -290,9 +312,9 @@ int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* 
   p.dk = make_buf(dk);
   p.dv = make_buf(dv);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dk, dv, sh.D, flags);
-  const bool mx = !mf && mixed_ok(q, k, v, bias, sh.D, Wparam, flags, global) && aligned_f32_rows(dout) &&
-                  aligned_f32_rows(dk) && aligned_bf16_rows(dv);
-  return run_band(2, mx ? KERNEL_MIXED : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
+  const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dk) && aligned_bf16_rows(dv);
+  return run_band(2, sp ? split_kernel(sk) : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
                   global ? "tension_global_bwd(dkv)" : "tension_window_bwd_dkv");
 }
 
@@ -337,6 +359,8 @@ int scratch_ptr(void** out) {
 extern "C" {
 
 const char* tension_last_error(void) { return g_err.c_str(); }
+
+int tension_last_kernel(void) { return g_last_kernel; }
 
 const char* tension_version(void) { return "tension_hip 0.1 (gfx950)"; }
 

@@ -10,6 +10,7 @@ static void launch_d(const BandParams& p, hipStream_t st, unsigned grid) {
 
 int launch_exact_dq_f64(const BandParams& p, hipStream_t st, hipError_t* err) {
   const int64_t total = (int64_t)p.B * p.H * p.T;
+  if ((total + 127) / 128 > 0x7fffffff) return kGridTooLarge;
   const unsigned grid = (unsigned)((total + 127) / 128);
   switch (p.D) {
     case 8: launch_d<8>(p, st, grid); break;

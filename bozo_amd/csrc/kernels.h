@@ -75,14 +75,16 @@ struct AuxLossParams {
 };
 
 // phase: 0 forward, 1 dQ, 2 dK/dV.  Return 0 when launched (HIP status in
-// *err), -1 when no kernel exists for the request.
+// *err), -1 when no kernel exists for the request, kGridTooLarge when the
+// grid would exceed 2^31 - 1 workgroups (band.h).
 int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
 // kf32 (with fast): float32 q / k_new / K cache / out and a bf16 V
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32 = false);
-// float32 Q / K / dOut with a bfloat16 V (local windows W <= 64, head dim 64);
-// phase 0 forward, 1 dQ, 2 dK / dV
-int launch_mixed(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
+// split-operand kernels (split_band.h): f32 = float32 Q / K / dOut with a
+// bfloat16 V, else bf16 throughout; head dim 32 or 64; phase 0 forward,
+// 1 dQ, 2 dK / dV
+int launch_split(int phase, bool f32, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
 // bf16 / float32 rows (x_f32, y_f32), D % 16 == 0, 16-byte aligned rows and tables
 int launch_rope_vec(bool x_f32, bool y_f32, const RopeParams& p, hipStream_t st, hipError_t* err);

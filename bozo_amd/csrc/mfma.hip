@@ -49,7 +49,8 @@ int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* e
   while (p.chunk < 4 && (int64_t)p.B * p.H * ((p.ntiles + 2 * p.chunk - 1) / (2 * p.chunk)) >= 3 * cus)
     p.chunk *= 2;
 #endif
-  if (nwg <= 0 || nwg > 0x7fffffff) return -1;
+  if (nwg <= 0) return -1;
+  if (nwg > 0x7fffffff) return kGridTooLarge;
   const int norm = (p.flags & TENSION_NORM_MASS)    ? NORM_MASS_
                    : (p.flags & TENSION_NORM_COUNT) ? NORM_COUNT_
                                                     : NORM_RAW;
@@ -59,7 +60,7 @@ int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* e
     int64_t runs = (TENSION_BWD_WG_PER_CU * cus + bh / 2) / bh;
     if (runs < 1) runs = 1;
     if (runs > p.ntiles) runs = p.ntiles;
-    if (bh * runs > 0x7fffffff) return -1;
+    if (bh * runs > 0x7fffffff) return kGridTooLarge;
     p.chunk = (int)runs;
     launch_mfma_bwd_fused(p, st, (unsigned)(bh * runs), norm);
     *err = hipGetLastError();

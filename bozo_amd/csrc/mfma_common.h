@@ -559,7 +559,7 @@ __device__ __forceinline__ TrRead tr8_issue_at(uint32_t lo, uint32_t hi) {
 // Per-lane source offsets of a direct-tile copy: lane L of wave w copies the
 // chunks q_n = (4n + w) * 64 + L (n = 0, 1) of the tile, i.e. row q_n / 8 and
 // logical chunk (q_n & 7) ^ dsw(row), at byte offset off[n] from the tile's
-// first row (the host keeps 64 rows of a tensor within 32-bit offsets).
+// first row (the host takes this path only when rows_fit_view(64, rs)).
 struct TileLane {
   uint32_t off[2];
 };

@@ -525,7 +525,9 @@ void launch_gl_fwd(const BandParams& p, hipStream_t st);
 void launch_mfma_fwd(const BandParams& p, hipStream_t st, unsigned nwg, int norm) {
   const bool bias = p.bias.p != nullptr, tau = p.tau.p != nullptr;
 #ifndef TENSION_NO_GL_FWD
-  if (p.glob && norm == NORM_MASS_) {  // bias and tau_local included
+  // gl_fwd keeps each lane's offset within a 64-row K / V tile in 32 bits
+  // (tile_lane); larger row strides take the band kernel's 64-bit sources
+  if (p.glob && norm == NORM_MASS_ && rows_fit_view(kTile, p.k.s1) && rows_fit_view(kTile, p.v.s1)) {
     launch_gl_fwd(p, st);
     return;
   }

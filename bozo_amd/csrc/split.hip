@@ -1,0 +1,32 @@
+// Dispatch of the split-operand band kernels (split_band.h): grid size and
+// the per-phase, per-precision instantiation units.
+#include "kernels.h"
+
+namespace tension {
+
+void launch_split_fwd_bf16(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dq_bf16(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dkv_bf16(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_fwd_f32(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dq_f32(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dkv_f32(const BandParams& p, hipStream_t st, unsigned n);
+
+int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hipError_t* err) {
+  BandParams p = p_in;
+  if (p.D != 32 && p.D != 64) return -1;
+  p.ntiles = (p.T + 63) / 64;
+  const int64_t nwg = (int64_t)p.B * p.H * p.ntiles;
+  if (nwg <= 0) return -1;
+  if (nwg > 0x7fffffff) return kGridTooLarge;
+  const unsigned n = (unsigned)nwg;
+  switch (phase) {
+    case 0: (f32 ? launch_split_fwd_f32 : launch_split_fwd_bf16)(p, st, n); break;
+    case 1: (f32 ? launch_split_dq_f32 : launch_split_dq_bf16)(p, st, n); break;
+    case 2: (f32 ? launch_split_dkv_f32 : launch_split_dkv_bf16)(p, st, n); break;
+    default: return -1;
+  }
+  *err = hipGetLastError();
+  return 0;
+}
+
+}  // namespace tension

@@ -1,0 +1,761 @@
+// Split-operand MFMA band kernels (gfx950): every operand enters
+// v_mfma_f32_16x16x32_bf16 as a sum of NT bf16 terms.
+//
+//   NT = 1  bf16 tensors, taken as stored;
+//   NT = 3  float32 tensors, split on their way into registers or LDS as
+//           x = t0 + t1 + t2 + r with t0 = bf16(x), t1 = bf16(x - t0),
+//           t2 = bf16(x - t0 - t1) (both differences are exact in float32)
+//           and |r| <= 2^-24 |x|, the size of float32 rounding itself.
+//
+// A product of two split operands keeps the terms t_i u_j with i + j <= L,
+// smallest first into the float32 accumulator: L = 2 (six MFMAs for
+// NT = 3) where the result is float32, L = 1 (three) where it is rounded to
+// bf16 (dV); a product with the exact bf16 V takes the three t_i v.  The
+// dropped terms are below 3 * 2^-24 of each product term, so sums agree
+// with a float32 evaluation to its own rounding level.  The float32 flow is
+// the reference's autocast one: RoPE hands the op float32 Q / K
+// (model.py:75-81), V stays bf16, and the Triton kernel computes the call in
+// float32 (kernel.py:71-98); out, tau, dOut, dQ, dK are float32, dV bf16.
+// With NT = 1 the same kernels are the bf16 MFMA path of the head dims and
+// windows the dedicated bf16 kernels do not take.
+//
+// Head dim D = 32 or 64: LDS tiles are 64 rows x 64 bf16 (direct tiles,
+// mfma_common.h); D = 32 fills the first four 16-byte chunks of each row
+// and runs half the feature chunks.  Any band (local window of any width,
+// or the global block): the forward and dQ kernels stream the key blocks
+// of one 64-query tile's band through LDS, the dK / dV kernel the query
+// tiles that see one 64-key tile.  Each kernel: 256 threads (4 waves), a
+// wave owns 16 rows of the tile.
+#pragma once
+
+#include <type_traits>
+
+#include "mfma_common.h"
+
+namespace tension {
+namespace split {
+
+template <int NT>
+using Elem = typename std::conditional<NT == 1, bf16, float>::type;
+
+// ----------------------------------------------------------------- terms
+
+// 8 float32 values -> NT bf16 bit patterns per value.
+template <int NT>
+__device__ __forceinline__ void split8(const float* x, u16x8* t) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bf16 h = (bf16)x[e];
+    t[0][e] = bf16_bits(h);
+    if constexpr (NT == 3) {
+      const float r = x[e] - (float)h;
+      const bf16 m = (bf16)r;
+      t[1][e] = bf16_bits(m);
+      t[2][e] = bf16_bits((bf16)(r - (float)m));
+    }
+  }
+}
+
+// C += sum of A_i B_j over i < NA, j < NB, i + j <= L, largest i + j first.
+template <int NA, int NB, int L>
+__device__ __forceinline__ f32x4 mmx(const bf16x8* a, const bf16x8* b, f32x4 c) {
+#pragma unroll
+  for (int s = L; s >= 0; --s)
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int j = s - i;
+      if (j >= 0 && j < NB) c = mfma(a[i], b[j], c);
+    }
+  return c;
+}
+
+// B operand of a product over 32 tile rows from two 16-row groups of
+// float32 C-layout values (the pairing dt_tr8 uses), as NT terms.
+template <int NT>
+__device__ __forceinline__ void pack_terms(const float* lo4, const float* hi4, bf16x8* t) {
+  const float x[8] = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+  u16x8 u[NT];
+  split8<NT>(x, u);
+#pragma unroll
+  for (int i = 0; i < NT; ++i) t[i] = __builtin_bit_cast(bf16x8, u[i]);
+}
+
+// Operand fragment from global memory: features 8 chunk .. +7 of row `row`
+// of a tensor of Elem<NT> (zero outside [0, T)).
+template <int NT>
+__device__ __forceinline__ void frag_row(const Elem<NT>* base, int64_t rs, int row, int T, int chunk,
+                                         bf16x8* t) {
+  u16x8 u[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) u[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  if (row >= 0 && row < T) {
+    const Elem<NT>* src = base + (int64_t)row * rs + 8 * chunk;
+    if constexpr (NT == 1) {
+      u[0] = *(const u16x8*)src;
+    } else {
+      const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
+      const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      split8<NT>(x, u);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NT; ++i) t[i] = __builtin_bit_cast(bf16x8, u[i]);
+}
+
+// ----------------------------------------------------------------- staging
+
+// A thread's two staged rows (staged_row(tid), +8; chunk tid % 8) of a
+// 64-row tile as loaded: bf16 (NT = 1) or float32 (NT = 3).
+template <int NT>
+struct Raw;
+template <>
+struct Raw<1> {
+  u16x8 a, b;
+};
+template <>
+struct Raw<3> {
+  f32x4 a0, a1, b0, b1;
+};
+
+// Rows outside [0, T) and chunks past the head dim read as zero.
+template <int NT, int D>
+__device__ __forceinline__ Raw<NT> load_raw(const Elem<NT>* base, int64_t rs, int r0, int T, int tid) {
+  const int ch = tid & 7;
+  const int ra = r0 + staged_row(tid), rb = ra + 8;
+  const bool okc = ch < D / 8;
+  const bool oka = okc && ra >= 0 && ra < T, okb = okc && rb >= 0 && rb < T;
+  Raw<NT> x;
+  if constexpr (NT == 1) {
+    x.a = x.b = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (oka) x.a = *(const u16x8*)(base + (int64_t)ra * rs + 8 * ch);
+    if (okb) x.b = *(const u16x8*)(base + (int64_t)rb * rs + 8 * ch);
+  } else {
+    x.a0 = x.a1 = x.b0 = x.b1 = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (oka) {
+      x.a0 = *(const f32x4*)(base + (int64_t)ra * rs + 8 * ch);
+      x.a1 = *(const f32x4*)(base + (int64_t)ra * rs + 8 * ch + 4);
+    }
+    if (okb) {
+      x.b0 = *(const f32x4*)(base + (int64_t)rb * rs + 8 * ch);
+      x.b1 = *(const f32x4*)(base + (int64_t)rb * rs + 8 * ch + 4);
+    }
+  }
+  return x;
+}
+
+// The rows into NT consecutive direct tiles (term i at tile0 + i kDTile).
+template <int NT>
+__device__ __forceinline__ void store_raw(const Raw<NT>& x, bf16* tile0, int tid) {
+  if constexpr (NT == 1) {
+    tile_store_direct(TileRegs{x.a, x.b}, tile0, tid);
+  } else {
+    const float a[8] = {x.a0[0], x.a0[1], x.a0[2], x.a0[3], x.a1[0], x.a1[1], x.a1[2], x.a1[3]};
+    const float b[8] = {x.b0[0], x.b0[1], x.b0[2], x.b0[3], x.b1[0], x.b1[1], x.b1[2], x.b1[3]};
+    u16x8 ta[NT], tb[NT];
+    split8<NT>(a, ta);
+    split8<NT>(b, tb);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) tile_store_direct(TileRegs{ta[i], tb[i]}, tile0 + i * kDTile, tid);
+  }
+}
+
+// One output row's C-layout values (features 16 m + 4 g .. +3), times f.
+template <typename O, int D>
+__device__ __forceinline__ void store_acc(O* row, const f32x4* acc, float f, int g) {
+#pragma unroll
+  for (int m = 0; m < D / 16; ++m) {
+    if constexpr (std::is_same<O, float>::value) {
+      *(f32x4*)(row + 16 * m + 4 * g) = acc[m] * f;
+    } else {
+      u16x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+      *(u16x4*)(row + 16 * m + 4 * g) = o;
+    }
+  }
+}
+
+// --------------------------------------------------------------- geometry
+
+// The key blocks of a query tile's band: [kb_first, kb_first + 64 nblk).
+struct Blocks {
+  int first, n;
+};
+
+__device__ __forceinline__ Blocks band_blocks(const BandParams& p, int t0) {
+  int s_lo = t0 - p.win;
+  if (s_lo < 0) s_lo = 0;
+  int s_hi = t0 + kTile - 2 + p.diag;
+  if (s_hi > p.T - 1) s_hi = p.T - 1;
+  Blocks r;
+  r.first = s_lo & ~(kTile - 1);
+  r.n = s_hi < r.first ? 0 : (s_hi - r.first) / kTile + 1;
+  return r;
+}
+
+// Keys go through LDS: buffer `buf` holds block terms K_0 .. K_{NT-1}, V.
+template <int NT>
+__device__ __forceinline__ bf16* key_buf(bf16* lds, int buf) {
+  return lds + buf * (NT + 1) * kDTile;
+}
+
+// Stream the key blocks of a band through NBUF LDS buffers: block i is
+// staged (from registers loaded during block i - 1) while the waves work on
+// block i - 1 (NBUF = 2) or after they leave it (NBUF = 1);
+// body(tiles, first key) runs once per block with its buffer filled.
+template <int NT, int D, int NBUF, typename Body>
+__device__ __forceinline__ void stream_keys(bf16* lds, const Elem<NT>* kb_, int64_t ks, const bf16* vb_,
+                                            int64_t vs, const Blocks& bl, int T, int tid, Body body) {
+  if (bl.n <= 0) return;
+  store_raw<NT>(load_raw<NT, D>(kb_, ks, bl.first, T, tid), key_buf<NT>(lds, 0), tid);
+  store_raw<1>(load_raw<1, D>(vb_, vs, bl.first, T, tid), key_buf<NT>(lds, 0) + NT * kDTile, tid);
+  __syncthreads();
+  for (int i = 0; i < bl.n; ++i) {
+    const int kb0 = bl.first + i * kTile;
+    const int buf = NBUF == 2 ? (i & 1) : 0;
+    const bool more = i + 1 < bl.n;
+    Raw<NT> kn;
+    Raw<1> vn;
+    if (more) {
+      kn = load_raw<NT, D>(kb_, ks, kb0 + kTile, T, tid);
+      vn = load_raw<1, D>(vb_, vs, kb0 + kTile, T, tid);
+    }
+    body((const bf16*)key_buf<NT>(lds, buf), kb0);
+    if (more) {
+      if (NBUF == 1) __syncthreads();  // every wave is done with the buffer
+      bf16* nb = key_buf<NT>(lds, NBUF == 2 ? (buf ^ 1) : 0);
+      store_raw<NT>(kn, nb, tid);
+      store_raw<1>(vn, nb + NT * kDTile, tid);
+    }
+    __syncthreads();
+  }
+}
+
+// S^T (keys 16 j + 4 g + r, query c) of one 16-key group against this
+// lane's query fragments.
+template <int NT, int D>
+__device__ __forceinline__ f32x4 scores_t(const bf16* kt, const bf16x8 (*qf)[NT], int j, int g, int c) {
+  f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    bf16x8 ka[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) ka[i] = dt_row8(kt + i * kDTile, 16 * j + c, 4 * ch + g);
+    sc = mmx<NT, NT, 2>(ka, qf[ch], sc);
+  }
+  return sc;
+}
+
+// ----------------------------------------------------------------- forward
+
+template <int NT, int D, int NORM, bool BIAS, bool TAU>
+__global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
+  constexpr int NBUF = NT == 1 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const TileId id = tile_id(p, p.glob != 0);
+  const int b = id.b, h = id.h, T = p.T;
+  const int t0 = id.tile * kTile;
+  const int tq = t0 + wave * 16 + c;
+  const int lo = tq - p.win > 0 ? tq - p.win : 0;
+  const int hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
+  const WaveBand wb = wave_band(p, t0 + wave * 16);
+  const Blocks bl = band_blocks(p, t0);
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  bf16x8 qf[D / 32][NT];
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) frag_row<NT>(qb_, p.q.s1, tq, T, 4 * ch + g, qf[ch]);
+
+  const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float msum = 0.f;
+  stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, [&](const bf16* kt, int kb0) {
+    float pr[4][4];
+    int kind[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kind[j] = sub_kind(wb, kb0 + 16 * j);
+      if (kind[j] == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[j][r] = 0.f;
+        continue;
+      }
+      const f32x4 sc = scores_t<NT, D>(kt, qf, j, g, c);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * j + 4 * g + r;
+        const bool ok = (key >= lo) & (key <= hi);
+        float b2 = 0.f;
+        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+        const float pv = ok ? sigmoid_scaled(sc[r], k2, b2) : 0.f;
+        if (TAU && ok) {
+          const int col = tau_col(p, tq, key);
+          if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), pv);
+        }
+        msum += pv;
+        pr[j][r] = pv;
+      }
+    }
+    // O^T += V^T P^T over 32-key pairs (A = V^T read transposed)
+    const bf16* vt = kt + NT * kDTile;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kind[2 * kk] == 0 && kind[2 * kk + 1] == 0) continue;
+      bf16x8 ps[NT];
+      pack_terms<NT>(pr[2 * kk], pr[2 * kk + 1], ps);
+#pragma unroll
+      for (int m = 0; m < D / 16; ++m) {
+        const bf16x8 va = dt_tr8(vt, m, 32 * kk, g, c);
+        acc[m] = mmx<1, NT, 2>(&va, ps, acc[m]);
+      }
+    }
+  });
+  msum = wave_sum_g(msum);
+  if (tq >= T) return;
+  store_acc<E, D>((E*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2, acc,
+                  out_factor<NORM>(msum, tq, p.W), g);
+  if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, msum);
+  if (TAU) {
+    const int e = tau_empty_bound(p, tq);
+    for (int col = g; col < e; col += 4) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------- dQ
+
+// MODE 0: raw / valid-count (the coefficients are known): one pass.
+// MODE 1: tau-mass with the band within two key blocks (W <= 64): P and dP
+//         of the band stay in registers while the coefficients form.
+// MODE 2: tau-mass over a wider band: a first pass forms the coefficients,
+//         a second recomputes S and dP.
+// The tau-mass coefficients of each query (dtau = a dP - c + dTau,
+// a = 1 / m, c = sum_s P dP / m^2, model.py:257-258 differentiated) go to
+// the workspace for the dK / dV kernel.
+template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
+__global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
+  constexpr int NBUF = (NT == 1 || MODE == 1) ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const TileId id = tile_id(p, p.glob != 0);
+  const int b = id.b, h = id.h, T = p.T;
+  const int t0 = id.tile * kTile;
+  const int tq = t0 + wave * 16 + c;
+  const bool qok = tq < T;
+  const int lo = tq - p.win > 0 ? tq - p.win : 0;
+  const int hi = qok ? tq - 1 + p.diag : -1;
+  const WaveBand wb = wave_band(p, t0 + wave * 16);
+  const Blocks bl = band_blocks(p, t0);
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  bf16x8 qf[D / 32][NT], of[D / 32][NT];
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    frag_row<NT>(qb_, p.q.s1, tq, T, 4 * ch + g, qf[ch]);
+    frag_row<NT>(ob_, p.dout.s1, tq, T, 4 * ch + g, of[ch]);
+  }
+
+  const float inv_scale = (float)(1.0 / p.scale);
+  const float k2 = -kLog2e * inv_scale;
+  float ca = 1.f, cc = 0.f;
+  if (NORM == NORM_COUNT_) {
+    const int cnt = tq < p.W ? tq : p.W;
+    ca = 1.f / (float)(cnt > 1 ? cnt : 1);
+  }
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // S^T and dP^T (keys 16 j + 4 g + r, query c) of one 16-key group
+  auto sdp = [&](const bf16* kt, int j, f32x4& sc, f32x4& dp) {
+    sc = scores_t<NT, D>(kt, qf, j, g, c);
+    dp = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bf16* vt = kt + NT * kDTile;
+#pragma unroll
+    for (int ch = 0; ch < D / 32; ++ch) {
+      const bf16x8 va = dt_row8(vt, 16 * j + c, 4 * ch + g);
+      dp = mmx<1, NT, 2>(&va, of[ch], dp);
+    }
+  };
+  // tau (masked) of one element
+  auto tau_of = [&](float s, int key, bool ok) {
+    float b2 = 0.f;
+    if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+    return ok ? sigmoid_scaled(s, k2, b2) : 0.f;
+  };
+  // G = tau (1 - tau) (a dP - c + dTau), zero off the band
+  auto g_of = [&](float pv, float dpv, int key, bool ok) {
+    float dt = fmaf(dpv, ca, -cc);
+    if (DTAU && ok) {
+      const int col = tau_col(p, tq, key);
+      if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, tq, h, col));
+    }
+    return ok ? dt * (pv - pv * pv) : 0.f;
+  };
+  // dQ^T += K^T G^T over 32-key pairs (A = K^T read transposed)
+  auto dq_product = [&](const bf16* kt, const int* kind, float (*G)[4]) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kind[2 * kk] == 0 && kind[2 * kk + 1] == 0) continue;
+      bf16x8 gs[NT];
+      pack_terms<NT>(G[2 * kk], G[2 * kk + 1], gs);
+#pragma unroll
+      for (int m = 0; m < D / 16; ++m) {
+        bf16x8 ka[NT];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) ka[i] = dt_tr8(kt + i * kDTile, m, 32 * kk, g, c);
+        acc[m] = mmx<NT, NT, 2>(ka, gs, acc[m]);
+      }
+    }
+  };
+  // one block's S, dP -> G -> dQ with the coefficients known
+  auto g_pass = [&](const bf16* kt, int kb0) {
+    float G[4][4];
+    int kind[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kind[j] = sub_kind(wb, kb0 + 16 * j);
+      if (kind[j] == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) G[j][r] = 0.f;
+        continue;
+      }
+      f32x4 sc, dp;
+      sdp(kt, j, sc, dp);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * j + 4 * g + r;
+        const bool ok = (key >= lo) & (key <= hi);
+        G[j][r] = g_of(tau_of(sc[r], key, ok), dp[r], key, ok);
+      }
+    }
+    dq_product(kt, kind, G);
+  };
+  float msum = 0.f, dsum = 0.f;
+  auto coefficients = [&]() {
+    msum = wave_sum_g(msum);
+    dsum = wave_sum_g(dsum);
+    const float m = msum > kMassEps ? msum : kMassEps;
+    ca = 1.f / m;
+    cc = msum >= kMassEps ? dsum * ca * ca : 0.f;
+    if (p.ws && qok && g == 0) {
+      const int64_t nws = (int64_t)p.B * p.T * p.H;
+      const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
+      ((float*)p.ws)[wi] = ca;
+      ((float*)p.ws)[nws + wi] = cc;
+    }
+  };
+
+  if constexpr (MODE == 0) {
+    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+  } else if constexpr (MODE == 1) {
+    // both blocks stay resident (buffers 0 and 1)
+    float P[2][4][4], Dp[2][4][4];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) P[s][j][r] = Dp[s][j][r] = 0.f;
+    if (bl.n > 0) {
+      store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first, T, tid), key_buf<NT>(lds, 0), tid);
+      store_raw<1>(load_raw<1, D>(vb_, p.v.s1, bl.first, T, tid), key_buf<NT>(lds, 0) + NT * kDTile, tid);
+    }
+    if (bl.n > 1) {
+      store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first + kTile, T, tid), key_buf<NT>(lds, 1), tid);
+      store_raw<1>(load_raw<1, D>(vb_, p.v.s1, bl.first + kTile, T, tid), key_buf<NT>(lds, 1) + NT * kDTile,
+                   tid);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s >= bl.n) break;
+      const int kb0 = bl.first + s * kTile;
+      const bf16* kt = key_buf<NT>(lds, s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
+        f32x4 sc, dp;
+        sdp(kt, j, sc, dp);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * j + 4 * g + r;
+          const bool ok = (key >= lo) & (key <= hi);
+          const float pv = tau_of(sc[r], key, ok);
+          P[s][j][r] = pv;
+          Dp[s][j][r] = ok ? dp[r] : 0.f;
+          msum += pv;
+          dsum = fmaf(pv, Dp[s][j][r], dsum);
+        }
+      }
+    }
+    coefficients();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s >= bl.n) break;
+      const int kb0 = bl.first + s * kTile;
+      float G[4][4];
+      int kind[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kind[j] = sub_kind(wb, kb0 + 16 * j);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * j + 4 * g + r;
+          const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
+          G[j][r] = g_of(P[s][j][r], Dp[s][j][r], key, ok);
+        }
+      }
+      dq_product(key_buf<NT>(lds, s), kind, G);
+    }
+  } else {
+    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, [&](const bf16* kt, int kb0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
+        f32x4 sc, dp;
+        sdp(kt, j, sc, dp);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * j + 4 * g + r;
+          const bool ok = (key >= lo) & (key <= hi);
+          const float pv = tau_of(sc[r], key, ok);
+          msum += pv;
+          dsum = fmaf(pv, ok ? dp[r] : 0.f, dsum);
+        }
+      }
+    });
+    coefficients();
+    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+  }
+  if (!qok) return;
+  store_acc<E, D>((E*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2, acc, inv_scale, g);
+}
+
+// ----------------------------------------------------------------- dK / dV
+
+// Key tile k: the query tiles whose band reaches it pass through LDS in
+// turn (Q and dOut as NT terms each, plus their rows' coefficients a, c).
+template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+__global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
+  constexpr int NBUF = NT == 1 ? 2 : 1;
+  constexpr int TPB = 2 * NT;  // tiles per buffer: Q terms, then dOut terms
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * TPB * kDTile];
+  __shared__ float sa[NBUF][kTile], scf[NBUF][kTile];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const TileId id = tile_id(p, false);
+  const int b = id.b, h = id.h, T = p.T;
+  const int k0 = id.tile * kTile;
+  const int tk = k0 + wave * 16 + c;
+  const bool kok = tk < T;
+  // queries that see this lane's key: [tk + 1 - diag, min(tk + win, T - 1)]
+  const int qlo = tk + 1 - p.diag;
+  const int qhi = !kok ? -1 : (tk > T - 1 - p.win ? T - 1 : tk + p.win);
+  // queries that see any key of this wave (a 16-query group outside is skipped)
+  const int ka = k0 + wave * 16;
+  const int kz = ka + 15 < T - 1 ? ka + 15 : T - 1;
+  const int wq_lo = ka + 1 - p.diag;
+  const int wq_hi = kz < ka ? -1 : (kz > T - 1 - p.win ? T - 1 : kz + p.win);
+  // query tiles k .. k + nqt - 1
+  const int last_q = k0 + kTile - 1 > T - 1 - p.win ? T - 1 : k0 + kTile - 1 + p.win;
+  const int nqt = last_q < k0 ? 0 : (last_q >> 6) - id.tile + 1;
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+
+  // this lane's key row as B operands: K as terms, V exact
+  bf16x8 kf[D / 32][NT], vf[D / 32];
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    frag_row<NT>(kb_, p.k.s1, tk, T, 4 * ch + g, kf[ch]);
+    frag_row<1>(vb_, p.v.s1, tk, T, 4 * ch + g, &vf[ch]);
+  }
+
+  auto stage = [&](int buf, int q0, const Raw<NT>& qx, const Raw<NT>& ox) {
+    bf16* base = lds + buf * TPB * kDTile;
+    store_raw<NT>(qx, base, tid);
+    store_raw<NT>(ox, base + NT * kDTile, tid);
+    if (tid < kTile) {
+      const int t = q0 + tid;
+      float a = 1.f, cv = 0.f;
+      if (t < T) {
+        if (NORM == NORM_MASS_) {
+          const int64_t nws = (int64_t)p.B * p.T * p.H;
+          const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
+          a = ((const float*)p.ws)[wi];
+          cv = ((const float*)p.ws)[nws + wi];
+        } else if (NORM == NORM_COUNT_) {
+          const int cnt = t < p.W ? t : p.W;
+          a = 1.f / (float)(cnt > 1 ? cnt : 1);
+        }
+      }
+      sa[buf][tid] = a;
+      scf[buf][tid] = cv;
+    }
+  };
+
+  const float inv_scale = (float)(1.0 / p.scale);
+  const float k2 = -kLog2e * inv_scale;
+  f32x4 dk[D / 16], dv[D / 16];
+#pragma unroll
+  for (int m = 0; m < D / 16; ++m) dk[m] = dv[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nqt > 0) {
+    stage(0, k0, load_raw<NT, D>(qb_, p.q.s1, k0, T, tid), load_raw<NT, D>(ob_, p.dout.s1, k0, T, tid));
+    __syncthreads();
+  }
+  for (int i = 0; i < nqt; ++i) {
+    const int q0 = k0 + i * kTile;
+    const int buf = NBUF == 2 ? (i & 1) : 0;
+    const bool more = i + 1 < nqt;
+    Raw<NT> qn, on;
+    if (more) {
+      qn = load_raw<NT, D>(qb_, p.q.s1, q0 + kTile, T, tid);
+      on = load_raw<NT, D>(ob_, p.dout.s1, q0 + kTile, T, tid);
+    }
+    const bf16* qt = lds + buf * TPB * kDTile;
+    const bf16* ot = qt + NT * kDTile;
+    float Pa[4][4], G[4][4];
+    bool live[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int qa = q0 + 16 * j;
+      live[j] = qa + 15 >= wq_lo && qa <= wq_hi;
+      if (!live[j]) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Pa[j][r] = G[j][r] = 0.f;
+        continue;
+      }
+      // S = Q K^T, dP = dO V^T: queries 16 j + 4 g + r (rows), key c (column)
+      f32x4 sv = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) {
+        bf16x8 qa_[NT], oa_[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          qa_[t] = dt_row8(qt + t * kDTile, 16 * j + c, 4 * ch + g);
+          oa_[t] = dt_row8(ot + t * kDTile, 16 * j + c, 4 * ch + g);
+        }
+        sv = mmx<NT, NT, 2>(qa_, kf[ch], sv);
+        dp = mmx<NT, 1, 2>(oa_, &vf[ch], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ql = 16 * j + 4 * g + r;  // query - q0
+        const int t = q0 + ql;
+        const bool ok = t >= qlo && t <= qhi;
+        float b2 = 0.f;
+        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, t, tk));
+        const float pv = sigmoid_scaled(sv[r], k2, b2);
+        const float a = sa[buf][ql];
+        float dt = fmaf(dp[r], a, -scf[buf][ql]);
+        if (DTAU && ok) {
+          const int col = tau_col(p, t, tk);
+          if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, t, h, col));
+        }
+        Pa[j][r] = ok ? pv * a : 0.f;
+        G[j][r] = ok ? dt * (pv - pv * pv) : 0.f;
+      }
+    }
+    // dV^T += dO^T (a P),  dK^T += Q^T G over 32-query pairs
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (!live[2 * kk] && !live[2 * kk + 1]) continue;
+      bf16x8 ps[NT], gs[NT];
+      pack_terms<NT>(Pa[2 * kk], Pa[2 * kk + 1], ps);
+      pack_terms<NT>(G[2 * kk], G[2 * kk + 1], gs);
+#pragma unroll
+      for (int m = 0; m < D / 16; ++m) {
+        bf16x8 oa_[NT], qa_[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          oa_[t] = dt_tr8(ot + t * kDTile, m, 32 * kk, g, c);
+          qa_[t] = dt_tr8(qt + t * kDTile, m, 32 * kk, g, c);
+        }
+        dv[m] = mmx<NT, NT, 1>(oa_, ps, dv[m]);
+        dk[m] = mmx<NT, NT, 2>(qa_, gs, dk[m]);
+      }
+    }
+    if (more) {
+      if (NBUF == 1) __syncthreads();  // every wave is done with the buffer
+      stage(NBUF == 2 ? (buf ^ 1) : 0, q0 + kTile, qn, on);
+      __syncthreads();
+    }
+  }
+  if (!kok) return;
+  store_acc<E, D>((E*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2, dk, inv_scale, g);
+  store_acc<bf16, D>((bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2, dv, 1.f, g);
+}
+
+// ----------------------------------------------------------------- launch
+
+template <int NT, int D, int NORM, int PHASE>
+void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
+  const bool bias = p.bias.p != nullptr;
+  const dim3 grid(n), block(kThreads);
+#define XB_BT(K, ...)                                                                                \
+  do {                                                                                               \
+    if (bias) {                                                                                      \
+      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, true, true __VA_ARGS__>), grid, block, 0, st, p);  \
+      else hipLaunchKernelGGL((K<NT, D, NORM, true, false __VA_ARGS__>), grid, block, 0, st, p);     \
+    } else {                                                                                         \
+      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, false, true __VA_ARGS__>), grid, block, 0, st, p); \
+      else hipLaunchKernelGGL((K<NT, D, NORM, false, false __VA_ARGS__>), grid, block, 0, st, p);    \
+    }                                                                                                \
+  } while (0)
+  if constexpr (PHASE == 0) {
+    const bool opt = p.tau.p != nullptr;
+    XB_BT(xb_fwd);
+  } else if constexpr (PHASE == 1) {
+    const bool opt = p.dtau.p != nullptr;
+    if constexpr (NORM != NORM_MASS_) {
+      XB_BT(xb_dq, , 0);
+    } else {
+      if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
+      else XB_BT(xb_dq, , 2);
+    }
+  } else {
+    const bool opt = p.dtau.p != nullptr;
+    XB_BT(xb_dkv);
+  }
+#undef XB_BT
+}
+
+// PHASE 0: forward, 1: dQ (+ coefficients), 2: dK / dV; one workgroup per
+// 64-row tile (n of them)
+template <int NT, int PHASE>
+void launch(const BandParams& p, hipStream_t st, unsigned n) {
+  const int norm = (p.flags & TENSION_NORM_MASS)    ? NORM_MASS_
+                   : (p.flags & TENSION_NORM_COUNT) ? NORM_COUNT_
+                                                    : NORM_RAW;
+  if (p.D == 32) {
+    if (norm == NORM_MASS_) launch_norm<NT, 32, NORM_MASS_, PHASE>(p, st, n);
+    else if (norm == NORM_COUNT_) launch_norm<NT, 32, NORM_COUNT_, PHASE>(p, st, n);
+    else launch_norm<NT, 32, NORM_RAW, PHASE>(p, st, n);
+  } else {
+    if (norm == NORM_MASS_) launch_norm<NT, 64, NORM_MASS_, PHASE>(p, st, n);
+    else if (norm == NORM_COUNT_) launch_norm<NT, 64, NORM_COUNT_, PHASE>(p, st, n);
+    else launch_norm<NT, 64, NORM_RAW, PHASE>(p, st, n);
+  }
+}
+
+}  // namespace split
+}  // namespace tension

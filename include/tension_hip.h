@@ -333,6 +333,18 @@ const char* tension_last_error(void);
 /* Library version string. */
 const char* tension_version(void);
 
+/* Kernel family of the last band launch (window / global forward, dq, dkv)
+ * on the calling thread: TENSION_KERNEL_* below, or -1 before the first.
+ * No counterpart in the reference (its router picks Triton or PyTorch,
+ * ops.py:217-219); it lets callers and tests see which path ran. */
+enum {
+  TENSION_KERNEL_EXACT = 0,      /* one thread per row, any dtype / head dim */
+  TENSION_KERNEL_MFMA = 1,       /* dedicated bf16 kernels, head dim 64 */
+  TENSION_KERNEL_SPLIT_BF16 = 2, /* split-operand kernels, bf16, head dim 32 / 64 */
+  TENSION_KERNEL_SPLIT_F32 = 3   /* split-operand kernels, float32 Q / K with bf16 V */
+};
+int tension_last_kernel(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -357,10 +357,17 @@ def window_forward_loops(Q, K, V, W, scale, bias=None):
     return msg, tau
 
 
-def global_forward_loops(Q, K, V, scale, bias=None):
+def global_forward_loops(Q, K, V, scale, bias=None, W_local=None):
+    """Loops over (b, t, h, s) from the definitions of model.py:217-238.
+    With W_local, also returns tau_local from its index definition
+    (model.py:235-236: tau[..., :T].flip(-1)[..., :min(W_local, T)]): slot j
+    of every query row holds the weight of key s = T-1-j, zero where that key
+    lies after the query (s > t)."""
     Q, K, V = np.asarray(Q, np.float64), np.asarray(K, np.float64), np.asarray(V, np.float64)
     B, T, H, D = Q.shape
     out = np.zeros((B, T, H, D))
+    Wl = None if W_local is None else min(W_local, T)
+    tl = None if Wl is None else np.zeros((B, T, H, Wl))
     for b in range(B):
         for h in range(H):
             for t in range(T):
@@ -374,7 +381,15 @@ def global_forward_loops(Q, K, V, scale, bias=None):
                     mass += p
                     acc += p * V[b, s, h]
                 out[b, t, h] = acc / max(mass, MASS_EPS)
-    return out
+                if tl is not None:
+                    for j in range(Wl):
+                        s = T - 1 - j
+                        if s <= t:
+                            x = float(Q[b, t, h] @ K[b, s, h]) / scale
+                            if bias is not None:
+                                x += float(bias[b, t, s])
+                            tl[b, t, h, j] = _sig1(x)
+    return out if tl is None else (out, tl)
 
 
 # Which check pins each function (all in tests/test_oracle.py).
@@ -385,7 +400,8 @@ PINS = {
                        "central finite differences; V-linearity of dV",
     "window_backward_normalized": "torch autograd through unfold + tau-mass; finite differences",
     "normalize_mass/normalize_count": "K=0 closed form (window mean of V); valid_count formula",
-    "global_forward": "brute-force loops; diag-masked global == window W=T; torch einsum restatement",
+    "global_forward": "brute-force loops (tau_local from its index definition); diag-masked global == "
+                      "window W=T; torch einsum restatement",
     "global_backward": "torch autograd through the einsum restatement; finite differences",
     "decode_step": "equals last rows of window_forward + tau-mass / valid-count normalisation over "
                    "a sequence; with self_kv, the rows of global_forward",

@@ -52,20 +52,33 @@ def scale_of(D):
     return math.sqrt(D)
 
 
-def fused_geometry(B, H, T, tile=64, wg_target=512):
+def device_cus(dev=0):
+    """Compute units of the GPU the kernels run on (the host launch code
+    queries the same attribute); 256 on MI355X, also assumed without a GPU."""
+    if torch.cuda.is_available():
+        return int(torch.cuda.get_device_properties(dev).multi_processor_count)
+    return 256
+
+
+def fused_geometry(B, H, T, tile=64, cus=None):
     """Launch geometry of the bf16 W <= 64 band kernels, restated from their
-    host dispatch (bozo_amd/csrc/mfma.hip ``launch_mfma``; the fast forward
-    with tau caps its tiles per workgroup at 2, mfma_fwd.hip ``go``).
+    host dispatch (bozo_amd/csrc/mfma.hip ``launch_mfma``: forward chunks while
+    the grid keeps >= 3 workgroups per CU, backward runs aimed at 2 per CU;
+    the fast forward with tau caps its tiles per workgroup at 2,
+    mfma_fwd.hip ``go``), for a device with ``cus`` compute units (default:
+    the current GPU's).
 
     Returns (fwd_tiles_per_workgroup, bwd_runs_per_sequence,
     longest_bwd_run_in_tiles).  A backward run of r tiles takes r own steps
     plus one recomputed halo step; runs longer than one tile hand dTau rows
     and the previous key block's partial dK/dV from step to step."""
+    if cus is None:
+        cus = device_cus()
     ntiles = -(-T // tile)
     bh = B * H
     chunk = 1
-    while chunk < 4 and bh * (-(-ntiles // (2 * chunk))) >= 768:
+    while chunk < 4 and bh * (-(-ntiles // (2 * chunk))) >= 3 * cus:
         chunk *= 2
-    runs = min(max(1, (wg_target + bh // 2) // bh), ntiles)
+    runs = min(max(1, (2 * cus + bh // 2) // bh), ntiles)
     longest = max((r + 1) * ntiles // runs - r * ntiles // runs for r in range(runs))
     return chunk, runs, longest

@@ -207,6 +207,18 @@ def test_size_products_do_not_wrap(lib):
     assert lib.lib().tension_aux_loss_partials(big, big, big) == 0
 
 
+def test_noalloc_refuses_requests_beyond_the_scratch(lib):
+    """tension_global_bwd_noalloc checks the coefficient scratch it needs
+    (2 * B*T*H floats) against its fixed size before it looks up the scratch
+    or launches anything: one query past the limit is an argument error,
+    with fake host pointers that are never read."""
+    n = lib.NOALLOC_SCRATCH_BYTES // 8 + 1
+    fake = _buf(strides=(n * 64, 64, 64, 1))
+    r = lib.lib().tension_global_bwd_noalloc(*([fake] * 11), 1, n, 1, 64, 0, ctypes.c_double(8.0), 0, None)
+    assert r == lib.ERR_ARG
+    assert b"fixed scratch" in lib.lib().tension_last_error()
+
+
 def test_no_cpu_fallback():
     from bozo_amd import causal_tension, global_tension
     x = torch.zeros(1, 8, 1, 16)

@@ -220,3 +220,70 @@ def test_rope_head_dims(dev, D, dtype, out_dtype):
         assert rel_l2(f64(xd.grad), dwant) <= 2e-2
     else:
         assert max_abs(f64(xd.grad), dwant) <= 1e-5
+
+
+def test_decode_config4_graph_replay_wraps(dev):
+    """Config 4 through the path bench.py times: ``TensionDecodeCache.step``
+    (position counters double-buffered on the device) captured 320 times in
+    one HIP graph over a cache pre-filled with W = 256 tokens, then replayed.
+    The ring wraps past its 256 slots; eight sequences are checked at every
+    step against the oracle's decode_step over its decode_append ring, and
+    the whole cache and counters after the replay against the known appends.
+    The graph is replayed a second time from a restored state: same bits."""
+    from bozo_amd import TensionDecodeCache
+    N, H, D, W, S = 64, 16, 64, 256, 320
+    sel = [0, 9, 17, 30, 41, 50, 58, 63]
+    g = torch.Generator().manual_seed(3)
+    kc = (torch.randn(N, H, W, D, generator=g) * 0.5).to(torch.bfloat16)
+    vc = (torch.randn(N, H, W, D, generator=g) * 0.5).to(torch.bfloat16)
+    q, k, v = ((torch.randn(S, N, H, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3))
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    cache = TensionDecodeCache(N, H, D, W, dtype=torch.bfloat16, device=dev)
+
+    def reset():
+        cache.k.copy_(kc.to(dev))
+        cache.v.copy_(vc.to(dev))
+        cache.pos[0].fill_(W)
+        cache.pos[1].fill_(-1)
+        cache.cur = 0
+
+    # one eager step on a scratch cache loads the library before capture
+    scratch = TensionDecodeCache(N, H, D, W, dtype=torch.bfloat16, device=dev)
+    scratch.step(qd[0], kd[0], vd[0])
+    reset()
+    torch.cuda.synchronize()
+    print(f"[decode graph] capturing {S} steps", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    outs = []
+    with torch.cuda.graph(graph):
+        for i in range(S):
+            outs.append(cache.step(qd[i], kd[i], vd[i]))
+    assert cache.cur == 0  # an even number of steps: the counters end in pos[0]
+    reset()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    first = [o.clone() for o in outs]
+
+    kc_s, vc_s = kc[sel].float().numpy(), vc[sel].float().numpy()
+    pos = np.full(len(sel), W, dtype=np.int64)
+    worst = 0.0
+    for i in range(S):
+        ro, _ = O.decode_step(q[i, sel].float().numpy(), kc_s, vc_s, pos, W, 8.0)
+        worst = max(worst, rel_l2(f64(first[i][sel]), ro))
+        assert rel_l2(f64(first[i][sel]), ro) <= 2e-2, (i, rel_l2(f64(first[i][sel]), ro))
+        kc_s, vc_s, pos = O.decode_append(kc_s, vc_s, pos, k[i, sel].float().numpy(),
+                                          v[i, sel].float().numpy(), W)
+    print(f"  worst per-step rel L2 over {S} steps: {worst:.3e}", flush=True)
+    # the ring after S appends: slot (W + i) % W holds step i's row for the last W steps
+    want_k, want_v = kc.clone(), vc.clone()
+    for i in range(S):
+        want_k[:, :, (W + i) % W] = k[i]
+        want_v[:, :, (W + i) % W] = v[i]
+    assert torch.equal(cache.k.cpu(), want_k) and torch.equal(cache.v.cpu(), want_v)
+    assert torch.equal(cache.pos[0].cpu(), torch.full((N,), W + S, dtype=torch.int32))
+    reset()
+    graph.replay()
+    torch.cuda.synchronize()
+    for i in range(S):
+        assert torch.equal(outs[i], first[i]), i

@@ -136,3 +136,58 @@ def test_backward_saved_rows_match_band_recompute(dev):
         assert rel_l2(f64(grads["saved"][i]), f64(grads["band"][i])) <= 1e-2, n
     mo, _, _ = O.global_forward(f64(inp["Q"]), f64(inp["K"]), f64(inp["V"]), 8.0, None, None)
     assert rel_l2(f64(out), mo) <= 2e-2
+
+
+def test_global_row_stride_beyond_32bit_offsets(dev):
+    """K / V rows 33,554,496 elements apart (64 rows span more than 2^32
+    bytes): the dedicated forward keeps per-lane tile offsets in 32 bits, so
+    the host sends such calls to the band kernel's 64-bit sources.  The views
+    sit in 6.6 GB allocations of which only the rows are written."""
+    B, H, T, D = 1, 1, 100, 64
+    s1 = (1 << 25) + 64
+    inp = make_inputs(B, T, H, D, seed=31, std=0.5, dtype=torch.bfloat16, rope=False)
+
+    def spread(x):
+        base = torch.empty((T - 1) * s1 + D, dtype=x.dtype, device=dev)
+        view = base.as_strided((B, T, H, D), (T * s1, s1, D, 1))
+        view.copy_(x.to(dev))
+        return view
+
+    from bozo_amd import global_tension
+    Q = inp["Q"].to(dev).requires_grad_(True)
+    K = spread(inp["K"]).requires_grad_(True)
+    V = spread(inp["V"]).requires_grad_(True)
+    print(f"[global stride] s1={s1} K stride {K.stride()}", flush=True)
+    out = global_tension(Q, K, V, 8.0)
+    (out.float() * inp["dO"].to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    ref = oracle_run(inp, 8.0)
+    check((out, None, (Q.grad, K.grad, V.grad)), ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("flow,D,T", [("bf16", 32, 200), ("bf16", 32, 64), ("f32qk", 64, 130), ("f32qk", 32, 97)])
+def test_global_split_kernels(dev, flow, D, T):
+    """The global block on the split-operand kernels: bf16 at head dim 32
+    (the reference's default model under autocast, model.py:33-36,219) and
+    float32 Q / K with a bf16 V (three bf16 terms per float32 value: the
+    fp32 bound, max-abs 1e-5, on out, dQ, dK and tau_local), with bias,
+    tau_local and its gradient."""
+    from bozo_amd import _lib as L
+    B, H, Wl = 2, 3, 16
+    dt = torch.bfloat16 if flow == "bf16" else torch.float32
+    inp = make_inputs(B, T, H, D, seed=40 + D + T, std=0.5, dtype=dt, W=Wl, dtau_std=0.1,
+                      bias_std=0.5, bias_shape=(B, T, T))
+    inp["V"] = inp["V"].to(torch.bfloat16)
+    scale = math.sqrt(D)
+    hip = hip_run(inp, scale, dev, W_local=Wl, use_bias=True, use_dtl=True)
+    assert int(L.lib().tension_last_kernel()) == (L.KERNEL_SPLIT_BF16 if flow == "bf16" else L.KERNEL_SPLIT_F32)
+    ref = oracle_run(inp, scale, W_local=Wl, use_bias=True, use_dtl=True)
+    if flow == "bf16":
+        check(hip, ref, torch.bfloat16, True)
+        return
+    for name, g, r in zip(("out", "dQ", "dK"), (hip[0], hip[2][0], hip[2][1]), (ref[0], ref[2][0], ref[2][1])):
+        err = max_abs(f64(g), r)
+        print(f"  {name}: max abs err {err:.3e}", flush=True)
+        assert err <= 1e-5, f"{name}: {err:.3e}"
+    assert rel_l2(f64(hip[2][2]), ref[2][2]) <= 2e-2
+    assert max_abs(f64(hip[1]), ref[1]) <= 1e-5

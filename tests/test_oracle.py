@@ -207,6 +207,31 @@ def test_global_forward_matches_loops_and_torch(with_bias):
     close(tl, tl2.numpy(), 1e-12)
 
 
+@pytest.mark.parametrize("T,Wl", [(12, 5), (9, 9), (7, 20)])
+def test_tau_local_matches_index_loops(T, Wl):
+    """tau_local (model.py:235-236) from a loop over its index definition,
+    slot j = key T-1-j for every query row: not the flip / slice expression
+    the oracle uses.  A query-relative reading (slot j = key t-j) differs."""
+    B, H, D = 2, 2, 4
+    Q, K, V = rnd(160 + T, B, T, H, D), rnd(161 + T, B, T, H, D), rnd(162 + T, B, T, H, D)
+    bias = rnd(163 + T, B, T, T) * 0.5
+    _, _, tl = O.global_forward(Q, K, V, 2.0, bias, W_local=Wl)
+    out_l, tl_l = O.global_forward_loops(Q, K, V, 2.0, bias, W_local=Wl)
+    assert tl.shape == (B, T, H, min(Wl, T))
+    close(tl, tl_l, 1e-12)
+    # the last query sees every key: its row is the full tau row reversed
+    x = np.einsum("bhd,bshd->bhs", Q[:, -1], K) / 2.0 + bias[:, -1][:, None, :]
+    close(tl[:, -1], (1 / (1 + np.exp(-x)))[..., ::-1][..., :min(Wl, T)], 1e-12)
+    # query-relative slots (key t-j) are a different quantity
+    rel = np.zeros_like(tl)
+    for t in range(T):
+        for j in range(min(Wl, T)):
+            if t - j >= 0:
+                xx = np.einsum("bhd,bhd->bh", Q[:, t], K[:, t - j]) / 2.0 + bias[:, t, t - j][:, None]
+                rel[:, t, :, j] = 1 / (1 + np.exp(-xx))
+    assert np.max(np.abs(rel - tl)) > 1e-3
+
+
 def test_global_without_diagonal_equals_full_window():
     B, T, H, D = 2, 16, 2, 8
     Q, K, V = rnd(64, B, T, H, D), rnd(65, B, T, H, D), rnd(66, B, T, H, D)
