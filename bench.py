@@ -446,6 +446,63 @@ def bench_window(args, dev):
     return result
 
 
+def bench_window_variants(dev, steps, warmup):
+    """The local-window op at the reference's other shipped shapes, fwd+bwd
+    per step over 4 rotated input sets, tau-mass normalised:
+      * the 350M preset's local layer (train.py:246-256: B4, 16 heads of 64,
+        T1024, W256) in the reference's autocast flow -- RoPE'd float32 Q / K,
+        bf16 V, float32 out / dOut (the split kernels, three bf16 terms per
+        float32 value) -- with and without tau + dTau (the aux-loss step),
+        and in bf16 (the dedicated bf16 kernels, W > 64 split backward);
+      * head dim 32 in bf16 (the reference's default model, model.py:33-36):
+        BASELINE config 1's shape (B4 H4 T256 W32) and a 32-sequence batch
+        at T1024."""
+    def sets_for(B, H, T, D, W, flow, n=4, seed=11):
+        raw = make_window_sets(n, B, T, H, D, dev, seed=seed)
+        g = torch.Generator(device=dev).manual_seed(seed + 1)
+        out = []
+        for s in raw:
+            if flow == "f32qk":
+                s = dict(Q=s["Q"].detach().float().requires_grad_(True),
+                         K=s["K"].detach().float().requires_grad_(True), V=s["V"], dO=s["dO"].float())
+            dt = torch.float32 if flow == "f32qk" else torch.bfloat16
+            s["dTau"] = (torch.randn(B, T, H, W, device=dev, generator=g) * 0.1).to(dt)
+            out.append(s)
+        return out
+
+    from bozo_amd import _lib as L
+    rows = []
+    for name, (B, H, T, D, W), flow, tau in (
+            ("350m_local_autocast", (4, 16, 1024, 64, 256), "f32qk", False),
+            ("350m_local_autocast_tau", (4, 16, 1024, 64, 256), "f32qk", True),
+            ("350m_local_bf16", (4, 16, 1024, 64, 256), "bf16", False),
+            ("117m_local_autocast", (8, 12, 1024, 64, 64), "f32qk", False),
+            ("d32_bf16_config1", (4, 4, 256, 32, 32), "bf16", False),
+            ("d32_bf16_b32_t1024", (32, 4, 1024, 32, 32), "bf16", False),
+            ("d32_autocast_b32_t1024", (32, 4, 1024, 32, 32), "f32qk", False)):
+        sets = sets_for(B, H, T, D, W, flow)
+        run = Runner([window_step_fn(s, W, math.sqrt(D), "mass", return_tau=tau) for s in sets])
+        ms = time_units(run, max(steps, 40), warmup, f"variant:{name}")
+        kernel = int(L.lib().tension_last_kernel())
+        del run, sets
+        el_qk = 4 if flow == "f32qk" else 2
+        # compulsory bytes: fwd reads Q, K, V, writes out; bwd reads Q, K, V, dO,
+        # writes dQ, dK, dV (out / dO / dQ / dK in Q's dtype, V / dV bf16)
+        nel = B * T * H * D
+        step_bytes = nel * (el_qk * 2 + 2 + el_qk) + nel * (el_qk * 2 + 2 + el_qk + el_qk * 2 + 2)
+        if tau:
+            step_bytes += 2 * B * T * H * W * el_qk
+        rows.append({"name": name, "B": B, "H": H, "T": T, "head_dim": D, "window": W,
+                     "dtype_flow": "fp32 Q/K/out/dOut, bf16 V/dV" if flow == "f32qk" else "bf16",
+                     "tau_and_dtau": tau, "ms_per_step": round(ms, 5),
+                     "tokens_per_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": step_bytes,
+                     "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "kernel_family": {0: "exact", 1: "mfma_bf16", 2: "split_bf16", 3: "split_f32"}.get(kernel)})
+        log(f"[bench] variant {rows[-1]}")
+    return {"config": "window op at the reference's other shipped shapes (350M preset W256, head dim 32)",
+            "rows": rows}
+
+
 def profile_kernels(n, dev):
     """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
     of each band kernel on rotated config-2 sets (bf16, then fp32 Q / K with
@@ -1031,6 +1088,8 @@ def main():
                          "dirs or .db files and exit")
     ap.add_argument("--model-only", action="store_true",
                     help="only the TensionLM-117M training step (config 5), one JSON line per variant")
+    ap.add_argument("--window-only", action="store_true",
+                    help="only the config-2 step (with its variants) and the other window shapes")
     ap.add_argument("--generation-only", action="store_true",
                     help="only the cached-generation, tau-export and graph-bias timings")
     args = ap.parse_args()
@@ -1068,8 +1127,14 @@ def main():
             print(json.dumps({"cpu_model_baselines": cpu_model_baselines(args.cpu_seconds)}), flush=True)
         return
     result = bench_window(args, dev)
+    log("[bench] window op at the other shipped shapes ...")
+    variants = bench_window_variants(dev, 40, 5)
+    if args.window_only:
+        result["other_configs"] = [variants]
+        print(json.dumps(result), flush=True)
+        return
     log("[bench] global block (config 3) ...")
-    others = [bench_global(dev, 20, 3)]
+    others = [variants, bench_global(dev, 20, 3)]
     log(f"[bench] {others[-1]}")
     log("[bench] decode (config 4) ...")
     others.append(bench_decode(dev, 4))
