@@ -47,6 +47,11 @@ __device__ __forceinline__ int64_t bias_off(const BandParams& p, int b, int t, i
   return (int64_t)b * p.bias.s0 + (int64_t)t * p.bias.s1 + (int64_t)col * p.bias.s2;
 }
 
+// Column of (t, s) in the bias (local [B,T,W]: s - t + W; global [B,T,T]: s).
+__device__ __forceinline__ int bias_col(const BandParams& p, int t, int s) {
+  return p.glob ? s : s - t + p.W;
+}
+
 // Column of (t, s) in tau / dtau, or -1 if the pair has no slot there.
 __device__ __forceinline__ int tau_col(const BandParams& p, int t, int s) {
   if (p.glob) {

@@ -151,6 +151,12 @@ bool split_rows(int kind, const tension_buf* b) {
   return kind == SPLIT_F32 ? aligned_f32_rows(b) : aligned_bf16_rows(b);
 }
 
+// tau / dtau of a split kernel: absent, or in Q's dtype (the kernels index
+// them as typed rows).
+bool split_side(int kind, const tension_buf* b) {
+  return !b || b->dtype == (kind == SPLIT_F32 ? TENSION_F32 : TENSION_BF16);
+}
+
 enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_SPLIT_BF16 = 2, KERNEL_SPLIT_F32 = 3 };
 
 thread_local int g_last_kernel = -1;
@@ -208,7 +214,7 @@ int band_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, c
   const bool mf = !(flags & TENSION_FORCE_EXACT) && sh.D == 64 && aligned_bf16_rows(q) && aligned_bf16_rows(k) &&
                   aligned_bf16_rows(v) && aligned_bf16_rows(out) && (!bias || bias->dtype == TENSION_F32);
   const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
-  const bool sp = sk != SPLIT_NONE && split_rows(sk, out);
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, out) && split_side(sk, tau);
   return run_band(0, sp ? split_kernel(sk) : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream, what);
 }
 
@@ -285,7 +291,7 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
   p.dq = make_buf(dq);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dq, nullptr, sh.D, flags);
   const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
-  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dq);
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dq) && split_side(sk, dtau);
   if (mf && out && mass) {
     TRY(check_buf(out, "out", true, 3));
     TRY(check_buf(mass, "mass", true, -1));
@@ -313,7 +319,8 @@ int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* 
   p.dv = make_buf(dv);
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dk, dv, sh.D, flags);
   const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
-  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dk) && aligned_bf16_rows(dv);
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dk) && aligned_bf16_rows(dv) &&
+                  split_side(sk, dtau);
   return run_band(2, sp ? split_kernel(sk) : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
                   global ? "tension_global_bwd(dkv)" : "tension_window_bwd_dkv");
 }

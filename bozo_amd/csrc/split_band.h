@@ -273,6 +273,11 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
   for (int ch = 0; ch < D / 32; ++ch) frag_row<NT>(qb_, p.q.s1, tq, T, 4 * ch + g, qf[ch]);
 
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  // this lane's query row of tau (dtype of Q, host-checked) and of the bias
+  // (float32, unit column stride); rows past T are never touched
+  const int tr = tq < T ? tq : T - 1;
+  E* const trow = TAU ? (E*)p.tau.p + b * p.tau.s0 + (int64_t)tr * p.tau.s1 + h * p.tau.s2 : nullptr;
+  const float* const brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
   f32x4 acc[D / 16];
 #pragma unroll
   for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -294,11 +299,11 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = (key >= lo) & (key <= hi);
         float b2 = 0.f;
-        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+        if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
         const float pv = ok ? sigmoid_scaled(sc[r], k2, b2) : 0.f;
         if (TAU && ok) {
           const int col = tau_col(p, tq, key);
-          if (col >= 0) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), pv);
+          if (col >= 0) trow[col] = (E)pv;
         }
         msum += pv;
         pr[j][r] = pv;
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
   if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, msum);
   if (TAU) {
     const int e = tau_empty_bound(p, tq);
-    for (int col = g; col < e; col += 4) st<float>(p.tau, tau_off(p.tau, b, tq, h, col), 0.f);
+    for (int col = g; col < e; col += 4) trow[col] = (E)0.f;
   }
 }
 
@@ -375,6 +380,11 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
     const int cnt = tq < p.W ? tq : p.W;
     ca = 1.f / (float)(cnt > 1 ? cnt : 1);
   }
+  // this lane's query row of dTau (dtype of Q, host-checked) and of the bias
+  const int tr = qok ? tq : T - 1;
+  const E* const drow = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + (int64_t)tr * p.dtau.s1 + h * p.dtau.s2
+                             : nullptr;
+  const float* const brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
   f32x4 acc[D / 16];
 #pragma unroll
   for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -393,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
   // tau (masked) of one element
   auto tau_of = [&](float s, int key, bool ok) {
     float b2 = 0.f;
-    if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+    if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
     return ok ? sigmoid_scaled(s, k2, b2) : 0.f;
   };
   // G = tau (1 - tau) (a dP - c + dTau), zero off the band
@@ -401,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
     float dt = fmaf(dpv, ca, -cc);
     if (DTAU && ok) {
       const int col = tau_col(p, tq, key);
-      if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, tq, h, col));
+      if (col >= 0) dt += (float)drow[col];
     }
     return ok ? dt * (pv - pv * pv) : 0.f;
   };
@@ -614,6 +624,9 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
 
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
+  // dTau (dtype of Q, host-checked) and bias (float32) of this (b, h)
+  const E* const dtb = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;
+  const float* const bb = BIAS ? (const float*)p.bias.p + b * p.bias.s0 : nullptr;
   f32x4 dk[D / 16], dv[D / 16];
 #pragma unroll
   for (int m = 0; m < D / 16; ++m) dk[m] = dv[m] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -663,13 +676,13 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
         const int t = q0 + ql;
         const bool ok = t >= qlo && t <= qhi;
         float b2 = 0.f;
-        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, t, tk));
+        if (BIAS && ok) b2 = -kLog2e * bb[(int64_t)t * p.bias.s1 + bias_col(p, t, tk)];
         const float pv = sigmoid_scaled(sv[r], k2, b2);
         const float a = sa[buf][ql];
         float dt = fmaf(dp[r], a, -scf[buf][ql]);
         if (DTAU && ok) {
           const int col = tau_col(p, t, tk);
-          if (col >= 0) dt += ld<float>(p.dtau, tau_off(p.dtau, b, t, h, col));
+          if (col >= 0) dt += (float)dtb[(int64_t)t * p.dtau.s1 + col];
         }
         Pa[j][r] = ok ? pv * a : 0.f;
         G[j][r] = ok ? dt * (pv - pv * pv) : 0.f;
