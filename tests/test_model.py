@@ -8,6 +8,7 @@ model.py independently of the module code.  The aux losses are compared with
 pure-Python loops written from their definitions (model.py:489-611).
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -313,3 +314,54 @@ def test_sample_next_matches_reference_loop(seed):
     assert a == b
     # the penalty only touches the last 32 tokens, by sign
     assert sample_next(logits, [], 1e-7, 0.9) == int(torch.argmax(logits))
+
+
+GOLDEN_MODEL = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "model_ref_cpu.npz")
+
+
+@pytest.mark.parametrize("case", ["rope", "rope_osc_bias", "learned_pos", "learned_pos_bias"])
+def test_model_ref_matches_reference_fixture(case):
+    """oracle/model_ref.py against the reference TensionLM itself: vectors
+    written by tests/golden/make_model_golden.py, which ran the reference's
+    model.py on the CPU in float64 (its unfold and einsum paths,
+    model.py:181-287,436-480).  Same seeded parameters (RoPE on / off,
+    oscillation on / off, a global layer every 2nd block, graph biases on
+    both layer kinds): logits, hidden state and every layer's tau to 1e-10;
+    this build's four aux losses (bozo_amd/model.py) on model_ref's taus to
+    1e-10; the gradient of sum(logits * g) + aux terms with respect to every
+    parameter to 1e-5 relative (stored in float32)."""
+    from tests.golden.make_model_golden import weights
+    d = np.load(GOLDEN_MODEL)
+    pre = case + "/"
+    use_rope, use_osc, biases = (bool(x) for x in d[pre + "cfg"])
+    cfg = M.TensionConfig(vocab_size=53, dim=16, num_layers=4, num_heads=2, window=3, ffn_mult=3,
+                          max_seq_len=16, dropout=0.0, use_rope=use_rope, use_oscillation=use_osc,
+                          use_triton=False, global_every=2)
+    shapes = []
+    for item in d[pre + "params"]:
+        name, sh = str(item).rsplit(":", 1)
+        shapes.append((name, tuple(int(x) for x in sh.split("x"))))
+    sd = {k: torch.from_numpy(v).requires_grad_(True) for k, v in weights(shapes, int(d[pre + "seed"])).items()}
+    ids = torch.from_numpy(d[pre + "ids"])
+    bias = torch.from_numpy(d[pre + "bias"]) if biases else None
+    bias_g = torch.from_numpy(d[pre + "bias_global"]) if biases else None
+    logits, hidden, taus = model_ref.forward(sd, cfg, ids, True, bias, bias_g)
+    close = lambda a, b, tol: float((a.detach() - torch.from_numpy(b)).abs().max()) <= tol  # noqa: E731
+    assert close(logits, d[pre + "logits"], 1e-10)
+    assert close(hidden, d[pre + "hidden"], 1e-10)
+    for i, t in enumerate(taus):
+        assert close(t, d[pre + f"tau/{i}"], 1e-10), i
+    groups = M.TensionLM(cfg).window_groups
+    div = M.tension_diversity_loss(taus, groups)
+    cons = M.constraint_consistency_loss(taus)
+    ent = M.tension_entropy_loss(taus)
+    clo = M.manifold_closure_loss(hidden)
+    got = torch.stack([div, cons, ent, clo]).detach().numpy()
+    assert np.max(np.abs(got - d[pre + "aux"])) <= 1e-10, (got, d[pre + "aux"])
+    upstream = torch.from_numpy(d[pre + "upstream"])
+    loss = (logits * upstream).sum() + 0.3 * div + 0.2 * cons + 0.1 * ent + 0.05 * clo
+    loss.backward()
+    for name, _ in shapes:
+        want = d[pre + "grad/" + name].astype(np.float64)
+        err = float(np.max(np.abs(sd[name].grad.numpy() - want)) / max(np.max(np.abs(want)), 1e-30))
+        assert err <= 1e-5, (name, err)
