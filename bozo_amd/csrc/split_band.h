@@ -246,12 +246,94 @@ __device__ __forceinline__ f32x4 scores_t(const bf16* kt, const bf16x8 (*qf)[NT]
   return sc;
 }
 
+// ----------------------------------------------------------- tau staging
+// tau / dTau cross the kernels as whole row segments: a wave's 16 query rows
+// x 64 keys of one key block sit in LDS, and each row's segment moves
+// between LDS and memory as one coalesced 64-lane access (column =
+// key - t + W, local; T - 1 - key, global).  Rows of 64 elements; the
+// 4-element chunk k of row r sits at chunk k ^ (r & 15), so the C-layout
+// accesses (16 rows at one chunk) and the row accesses (one row, 64 lanes)
+// both spread over distinct banks.
+constexpr int kStageRows = 16 * 64;  // elements per wave
+
+__device__ __forceinline__ int stage_at(int row, int col) {
+  return row * 64 + ((((col >> 2) ^ (row & 15))) << 2) + (col & 3);
+}
+
+// This lane's four C-layout values (keys 16 j + 4 g .. +3, query c) <-> LDS.
+template <typename E>
+__device__ __forceinline__ void stage_put4(E* st, int c, int j, int g, const float* v) {
+  E* at = st + stage_at(c, 16 * j + 4 * g);
+  if constexpr (std::is_same<E, float>::value) {
+    *(f32x4*)at = f32x4{v[0], v[1], v[2], v[3]};
+  } else {
+    u16x4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)v[r]);
+    *(u16x4*)at = o;
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ void stage_get4(const E* st, int c, int j, int g, float* v) {
+  const E* at = st + stage_at(c, 16 * j + 4 * g);
+  if constexpr (std::is_same<E, float>::value) {
+    const f32x4 x = *(const f32x4*)at;
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+  } else {
+    // bit-cast the whole vector (a bit_cast of one subscripted element has
+    // compiled to element 0 for every index on this toolchain)
+    const bf16x4 x = __builtin_bit_cast(bf16x4, *(const u16x4*)at);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = (float)x[r];
+  }
+}
+
+// Column of key `key` in query row t's tau, or -1 outside its band / slots.
+__device__ __forceinline__ int band_tau_col(const BandParams& p, int t, int key) {
+  const int lo = t - p.win > 0 ? t - p.win : 0;
+  if (key < lo || key > t - 1 + p.diag) return -1;
+  return tau_col(p, t, key);
+}
+
+// Rows t0w .. t0w + 15 (the wave's queries) of a [B,T,H,Wtau] tau / dTau of
+// this (b, h): lane l moves key kb0 + l of each row.
+template <typename E>
+__device__ __forceinline__ void tau_rows_store(const BandParams& p, E* base, const E* st, int t0w, int kb0,
+                                               int lane) {
+#pragma unroll 4
+  for (int rr = 0; rr < 16; ++rr) {
+    const int t = t0w + rr;
+    if (t >= p.T) break;
+    const int col = band_tau_col(p, t, kb0 + lane);
+    if (col >= 0) base[(int64_t)t * p.tau.s1 + col] = st[stage_at(rr, lane)];
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ void dtau_rows_load(const BandParams& p, const E* base, E* v, int t0w, int kb0,
+                                               int lane) {
+#pragma unroll
+  for (int rr = 0; rr < 16; ++rr) {
+    const int t = t0w + rr;
+    const int col = t < p.T ? band_tau_col(p, t, kb0 + lane) : -1;
+    v[rr] = col >= 0 ? base[(int64_t)t * p.dtau.s1 + col] : (E)0.f;
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ void dtau_rows_put(E* st, const E* v, int lane) {
+#pragma unroll
+  for (int rr = 0; rr < 16; ++rr) st[stage_at(rr, lane)] = v[rr];
+}
+
 // ----------------------------------------------------------------- forward
 
 template <int NT, int D, int NORM, bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
   constexpr int NBUF = NT == 1 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
@@ -276,7 +358,9 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
   // this lane's query row of tau (dtype of Q, host-checked) and of the bias
   // (float32, unit column stride); rows past T are never touched
   const int tr = tq < T ? tq : T - 1;
-  E* const trow = TAU ? (E*)p.tau.p + b * p.tau.s0 + (int64_t)tr * p.tau.s1 + h * p.tau.s2 : nullptr;
+  E* const tbh = TAU ? (E*)p.tau.p + b * p.tau.s0 + h * p.tau.s2 : nullptr;  // tau of this (b, h)
+  E* const trow = TAU ? tbh + (int64_t)tr * p.tau.s1 : nullptr;
+  E* const tst = tstage + (TAU ? wave * kStageRows : 0);
   const float* const brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
   f32x4 acc[D / 16];
 #pragma unroll
@@ -301,13 +385,16 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
         float b2 = 0.f;
         if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
         const float pv = ok ? sigmoid_scaled(sc[r], k2, b2) : 0.f;
-        if (TAU && ok) {
-          const int col = tau_col(p, tq, key);
-          if (col >= 0) trow[col] = (E)pv;
-        }
         msum += pv;
         pr[j][r] = pv;
       }
+    }
+    // whole row segments out (keys outside each row's band are not stored;
+    // a global block holds tau_local keys only from T - Wtau on)
+    if (TAU && !(p.glob && kb0 + kTile <= T - p.Wtau)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) stage_put4(tst, c, j, g, pr[j]);
+      tau_rows_store(p, tbh, tst, t0 + wave * 16, kb0, lane);
     }
     // O^T += V^T P^T over 32-key pairs (A = V^T read transposed)
     const bf16* vt = kt + NT * kDTile;
@@ -348,6 +435,7 @@ template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
 __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
   constexpr int NBUF = (NT == 1 || MODE == 1) ? 2 : 1;
   __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
@@ -381,9 +469,10 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
     ca = 1.f / (float)(cnt > 1 ? cnt : 1);
   }
   // this lane's query row of dTau (dtype of Q, host-checked) and of the bias
+  const E* const dbh = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;  // this (b, h)
+  E* const dst = dstage + (DTAU ? wave * kStageRows : 0);
+  const int t0w = t0 + wave * 16;
   const int tr = qok ? tq : T - 1;
-  const E* const drow = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + (int64_t)tr * p.dtau.s1 + h * p.dtau.s2
-                             : nullptr;
   const float* const brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
   f32x4 acc[D / 16];
 #pragma unroll
@@ -406,13 +495,10 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
     if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
     return ok ? sigmoid_scaled(s, k2, b2) : 0.f;
   };
-  // G = tau (1 - tau) (a dP - c + dTau), zero off the band
-  auto g_of = [&](float pv, float dpv, int key, bool ok) {
-    float dt = fmaf(dpv, ca, -cc);
-    if (DTAU && ok) {
-      const int col = tau_col(p, tq, key);
-      if (col >= 0) dt += (float)drow[col];
-    }
+  // G = tau (1 - tau) (a dP - c + dTau), zero off the band (dtv: the
+  // staged dTau of the pair, zero where it has no slot)
+  auto g_of = [&](float pv, float dpv, float dtv, bool ok) {
+    const float dt = fmaf(dpv, ca, -cc) + dtv;
     return ok ? dt * (pv - pv * pv) : 0.f;
   };
   // dQ^T += K^T G^T over 32-key pairs (A = K^T read transposed)
@@ -431,25 +517,29 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
       }
     }
   };
-  // one block's S, dP -> G -> dQ with the coefficients known
+  // one block's S, dP -> G -> dQ with the coefficients known; with dTau its
+  // rows are loaded before the products and staged through LDS after them
   auto g_pass = [&](const bf16* kt, int kb0) {
-    float G[4][4];
+    E dv[DTAU ? 16 : 1];
+    if constexpr (DTAU) dtau_rows_load(p, dbh, dv, t0w, kb0, lane);
+    f32x4 sc[4], dp[4];
     int kind[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       kind[j] = sub_kind(wb, kb0 + 16 * j);
-      if (kind[j] == 0) {
+      if (kind[j] != 0) sdp(kt, j, sc[j], dp[j]);
+    }
+    if constexpr (DTAU) dtau_rows_put(dst, dv, lane);
+    float G[4][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) G[j][r] = 0.f;
-        continue;
-      }
-      f32x4 sc, dp;
-      sdp(kt, j, sc, dp);
+    for (int j = 0; j < 4; ++j) {
+      float dtv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (DTAU && kind[j] != 0) stage_get4(dst, c, j, g, dtv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
-        const bool ok = (key >= lo) & (key <= hi);
-        G[j][r] = g_of(tau_of(sc[r], key, ok), dp[r], key, ok);
+        const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
+        G[j][r] = kind[j] != 0 ? g_of(tau_of(sc[j][r], key, ok), dp[j][r], dtv[r], ok) : 0.f;
       }
     }
     dq_product(kt, kind, G);
@@ -474,6 +564,11 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
   } else if constexpr (MODE == 1) {
     // both blocks stay resident (buffers 0 and 1)
     float P[2][4][4], Dp[2][4][4];
+    E dv[2][DTAU ? 16 : 1];
+    if constexpr (DTAU) {
+      dtau_rows_load(p, dbh, dv[0], t0w, bl.first, lane);
+      dtau_rows_load(p, dbh, dv[1], t0w, bl.first + kTile, lane);
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -517,16 +612,21 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
     for (int s = 0; s < 2; ++s) {
       if (s >= bl.n) break;
       const int kb0 = bl.first + s * kTile;
+      if constexpr (DTAU) {
+        dtau_rows_put(dst, dv[s], lane);
+      }
       float G[4][4];
       int kind[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         kind[j] = sub_kind(wb, kb0 + 16 * j);
+        float dtv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (DTAU && kind[j] != 0) stage_get4(dst, c, j, g, dtv);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = kb0 + 16 * j + 4 * g + r;
           const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
-          G[j][r] = g_of(P[s][j][r], Dp[s][j][r], key, ok);
+          G[j][r] = g_of(P[s][j][r], Dp[s][j][r], dtv[r], ok);
         }
       }
       dq_product(key_buf<NT>(lds, s), kind, G);

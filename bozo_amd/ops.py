@@ -94,6 +94,27 @@ def _grads_like(*ts: Tensor):
 
 # ----------------------------------------------------------------- local window
 
+_EXACT_WARNED = set()
+
+
+def _note_exact_path(what: str, Q: Tensor, K: Tensor, V: Tensor, pairs: int) -> None:
+    """Warn once per dtype / head-dim combination when a large call ran on the
+    exact kernels (one thread per row, no MFMA): float16, float32 V, head
+    dims other than 32 / 64 or unaligned rows.  float64 is exact on purpose."""
+    if pairs < (1 << 20) or Q.dtype == torch.float64:
+        return
+    if int(L.lib().tension_last_kernel()) != L.KERNEL_EXACT:
+        return
+    key = (what, Q.dtype, K.dtype, V.dtype, Q.shape[-1])
+    if key in _EXACT_WARNED:
+        return
+    _EXACT_WARNED.add(key)
+    import warnings
+    warnings.warn(f"{what}: Q/K/V {Q.dtype}/{K.dtype}/{V.dtype} with head dim {Q.shape[-1]} ran on the exact "
+                  "(non-MFMA) kernels, one thread per row; the MFMA kernels take bf16, or float32 Q/K with "
+                  "a bf16 V, at head dim 32 or 64 with 16-byte aligned rows", RuntimeWarning, stacklevel=3)
+
+
 def _window_fwd(Q, K, V, W, scale, tau, bias, flags, mass):
     B, T, H, D = Q.shape
     out = torch.empty(B, T, H, D, dtype=Q.dtype, device=Q.device)
@@ -101,6 +122,7 @@ def _window_fwd(Q, K, V, W, scale, tau, bias, flags, mass):
         L.check(L.lib().tension_window_fwd(
             L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tau), L.buf(bias), L.buf(mass),
             B, T, H, D, W, float(scale), flags, _stream(Q)), "tension_window_fwd")
+    _note_exact_path("causal_tension", Q, K, V, B * T * H * min(int(W), T))
     return out
 
 
@@ -222,6 +244,7 @@ def _global_fwd(Q, K, V, scale, Bias, Wl):
         L.check(L.lib().tension_global_fwd(
             L.buf(Q), L.buf(K), L.buf(V), L.buf(out), L.buf(tl), L.buf(Bias), L.buf(mass),
             B, T, H, D, Wl, float(scale), 0, _stream(Q)), "tension_global_fwd")
+    _note_exact_path("global_tension", Q, K, V, B * H * T * (T + 1) // 2)
     return out, tl, mass
 
 
