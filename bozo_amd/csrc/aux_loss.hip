@@ -10,9 +10,10 @@
 //               for w1 = 1..n with w1 + 1 <= r <= w1 + T_out:
 //               relu(tau[r, w1-1] * tau[r-1, 0] - tau[r, w1])  (acc 1)
 //   entropy   : m = mean tau, relu(0.05 - m) (acc 2), relu(m - 0.8) (acc 3)
-// Eight lanes share a row (16 bytes of bf16 each, W <= 64), so a wave load
-// instruction reads eight whole 128-byte rows; row sums fold through DPP.
-// A workgroup walks 1024 consecutive rows of one layer, four rows per lane
+// Eight lanes share a row: lane ch holds the 8-slot chunks ch, ch + 8, ..
+// (NCH = ceil(W / 64) of them, W <= 256), so a wave load instruction reads
+// eight whole 128-byte row pieces (bf16); row sums fold through DPP.  A
+// workgroup walks 1024 consecutive rows of one layer, 4 / NCH rows per lane
 // in flight at a time, and (forward) reduces its sums once at the end.
 //
 // Backward, with per-layer coefficients k = (k_div, k_cons, k_ent):
@@ -33,7 +34,7 @@ constexpr float kDivEps = 1e-8f;  // model.py:527-528
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kThreadsAux = 256;
 constexpr int kRowsPerPass = kThreadsAux / 8;  // one row per 8 lanes
-constexpr int kUnroll = 4;                     // passes whose loads are in flight together
+constexpr int kUnrollVals = 4;                 // row chunks per lane whose loads are in flight together
 
 // the eight values of lane chunk ch of a row (0 past W).  VEC (bf16, W and
 // the strides multiples of 8, 16-byte aligned base): one 16-byte load, issued
@@ -87,6 +88,19 @@ __device__ __forceinline__ void row8_store(const Buf& b, int64_t off, int ch, in
     for (int e = 0; e < 8; ++e)
       if (8 * ch + e < W) st<float>(b, off + 8 * ch + e, v[e]);
   }
+}
+
+// The NCH chunks ch + 8 k of a row (slots 8 (ch + 8 k) .. +7) into v[8 k ..].
+template <int VEC, bool FULL, int NCH>
+__device__ __forceinline__ void rowN(const Buf& b, int64_t off, int ch, int W, float* v) {
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) row8<VEC, FULL>(b, off, ch + 8 * k, W, v + 8 * k);
+}
+
+template <int VEC, bool FULL, int NCH>
+__device__ __forceinline__ void rowN_store(const Buf& b, int64_t off, int ch, int W, const float* v) {
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) row8_store<VEC, FULL>(b, off, ch + 8 * k, W, v + 8 * k);
 }
 
 // 1: bf16 rows read 16 bytes (8 slots) at a time, 2: float32 rows read 32
@@ -157,15 +171,16 @@ struct RowWalk {
 // Forward over this workgroup's kAuxRowsPerBlock rows of one layer: the four
 // sums accumulate per lane (one lane per row contributes) and meet once at
 // the end.
-template <int VEC, bool FULL>
+template <int VEC, bool FULL, int NCH>
 __device__ __forceinline__ void fwd_rows(const AuxLossParams& p, const Buf& tb, float* sums) {
+  constexpr int kUnroll = kUnrollVals / NCH, NV = 8 * NCH;
   const int ch = threadIdx.x & 7;
   const int64_t nrow = (int64_t)p.B * p.T * p.H;
   const int n = cons_n(p.W, p.T), T_out = p.T - (n + 1);
   RowWalk rw;
   rw.init((int64_t)blockIdx.x * kAuxRowsPerBlock + (threadIdx.x >> 3), p.T, p.H, tb, tb);
   for (int it = 0; it < kAuxRowsPerBlock / kRowsPerPass; it += kUnroll) {
-    float v[kUnroll][8], prev0[kUnroll];
+    float v[kUnroll][NV], prev0[kUnroll];
     int ts[kUnroll];
     bool live[kUnroll];
 #pragma unroll
@@ -175,7 +190,7 @@ __device__ __forceinline__ void fwd_rows(const AuxLossParams& p, const Buf& tb, 
       live[u] = rw.row < nrow;
       ts[u] = rw.t;
       const int64_t off = live[u] ? rw.off : 0;
-      row8<VEC, FULL>(tb, off, ch, p.W, v[u]);
+      rowN<VEC, FULL, NCH>(tb, off, ch, p.W, v[u]);
       // tau[t-1, 0] (a clamped row for t = 0); slots 0..4 of row t are in
       // lane 0's v[]
       prev0[u] = at(tb, live[u] && rw.t >= 1 ? off - tb.s1 : off);
@@ -185,14 +200,14 @@ __device__ __forceinline__ void fwd_rows(const AuxLossParams& p, const Buf& tb, 
     for (int u = 0; u < kUnroll; ++u) {
       float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += v[u][e];
+      for (int e = 0; e < NV; ++e) s += v[u][e];
       s = row_sum8(s);
       const float inv = __builtin_amdgcn_rcpf(s + kDivEps);
       // -sum p ln(p + eps) = -(inv ln 2) sum tau log2(tau inv + eps); slots
       // past W hold tau = 0 and add nothing
       float acc = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = fmaf(v[u][e], __builtin_amdgcn_logf(fmaf(v[u][e], inv, kDivEps)), acc);
+      for (int e = 0; e < NV; ++e) acc = fmaf(v[u][e], __builtin_amdgcn_logf(fmaf(v[u][e], inv, kDivEps)), acc);
       const float ent = -kLn2 * inv * row_sum8(acc);
       const float m = s / (float)p.W;
       float cons = 0.f;
@@ -215,8 +230,9 @@ __device__ __forceinline__ void fwd_rows(const AuxLossParams& p, const Buf& tb, 
   }
 }
 
-template <int VEC, bool FULL>
+template <int VEC, bool FULL, int NCH>
 __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Buf& tb, const Buf& db) {
+  constexpr int kUnroll = kUnrollVals / NCH, NV = 8 * NCH;
   const int ch = threadIdx.x & 7;
   const int64_t nrow = (int64_t)p.B * p.T * p.H;
   const int n = cons_n(p.W, p.T), T_out = p.T - (n + 1);
@@ -224,7 +240,7 @@ __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Bu
   RowWalk rw;
   rw.init((int64_t)blockIdx.x * kAuxRowsPerBlock + (threadIdx.x >> 3), p.T, p.H, tb, db);
   for (int it = 0; it < kAuxRowsPerBlock / kRowsPerPass; it += kUnroll) {
-    float v[kUnroll][8], vn[kUnroll][8], bprev[kUnroll];
+    float v[kUnroll][NV], vn[kUnroll][8], bprev[kUnroll];
     int ts[kUnroll];
     bool live[kUnroll];
     int64_t doffs[kUnroll];
@@ -236,7 +252,7 @@ __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Bu
       doffs[u] = rw.doff;
       const int64_t off = live[u] ? rw.off : 0;
       const int t = live[u] ? rw.t : 0;
-      row8<VEC, FULL>(tb, off, ch, p.W, v[u]);
+      rowN<VEC, FULL, NCH>(tb, off, ch, p.W, v[u]);
       // the consistency neighbours (clamped rows at the ends): tau[t-1, 0]
       // and slots 0..7 of row t+1
       bprev[u] = at(tb, t >= 1 ? off - tb.s1 : off);
@@ -247,14 +263,14 @@ __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Bu
     for (int u = 0; u < kUnroll; ++u) {
       float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += v[u][e];
+      for (int e = 0; e < NV; ++e) s += v[u][e];
       s = row_sum8(s);
       const float inv = __builtin_amdgcn_rcpf(s + kDivEps);
       // e_w = -(ln(p + eps) + p / (p + eps)); slots past W hold p = 0, so
       // they add nothing to sum e p
-      float ee[8], dot = 0.f;
+      float ee[NV], dot = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < NV; ++e) {
         const float pe = v[u][e] * inv, x = pe + kDivEps;
         ee[e] = -fmaf(__builtin_amdgcn_logf(x), kLn2, pe * __builtin_amdgcn_rcpf(x));
         dot = fmaf(ee[e], pe, dot);
@@ -264,9 +280,9 @@ __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Bu
       const float gent = kent * ((m > 0.8f ? 1.f : 0.f) - (m < 0.05f ? 1.f : 0.f)) / (float)p.W;
       // g = k_div (e - dot) / (S + eps) + gent = kd e + (gent - kd dot)
       const float kd = kdiv * inv, g0 = fmaf(-kd, dot, gent);
-      float g[8];
+      float g[NV];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) g[e] = fmaf(kd, ee[e], g0);
+      for (int e = 0; e < NV; ++e) g[e] = fmaf(kd, ee[e], g0);
       // consistency: slots 0..n live in lane chunk 0 (n <= 4 < 8)
       const int t = ts[u];
       if (ch == 0 && n > 0 && kcons != 0.f) {
@@ -289,7 +305,7 @@ __device__ __forceinline__ void bwd_rows(const AuxLossParams& p, int l, const Bu
           }
         }
       }
-      if (live[u]) row8_store<VEC, FULL>(db, doffs[u], ch, p.W, g);
+      if (live[u]) rowN_store<VEC, FULL, NCH>(db, doffs[u], ch, p.W, g);
     }
   }
 }
@@ -300,18 +316,24 @@ __global__ __launch_bounds__(kThreadsAux) void aux_loss_fwd_kernel(AuxLossParams
   const int l = blockIdx.y;
   const Buf tb = p.tau[l];
   float sums[4] = {0.f, 0.f, 0.f, 0.f};
-  // W = 64 (the model's window): every lane's chunk is in the row
+  // W = 64 NCH (e.g. the model's 64): every lane's chunks are in the row
   const int vk = vec_kind(tb, p.W);
-  if (vk == 1 && p.W == 64)
-    fwd_rows<1, true>(p, tb, sums);
-  else if (vk == 1)
-    fwd_rows<1, false>(p, tb, sums);
-  else if (vk == 2 && p.W == 64)
-    fwd_rows<2, true>(p, tb, sums);
-  else if (vk == 2)
-    fwd_rows<2, false>(p, tb, sums);
-  else
-    fwd_rows<0, false>(p, tb, sums);
+  const int nch = p.W <= 64 ? 1 : p.W <= 128 ? 2 : 4;
+  const bool full = p.W == 64 * nch;
+#define AUX_FWD(N)                                             \
+  if (vk == 1 && full) fwd_rows<1, true, N>(p, tb, sums);      \
+  else if (vk == 1) fwd_rows<1, false, N>(p, tb, sums);        \
+  else if (vk == 2 && full) fwd_rows<2, true, N>(p, tb, sums); \
+  else if (vk == 2) fwd_rows<2, false, N>(p, tb, sums);        \
+  else fwd_rows<0, false, N>(p, tb, sums);
+  if (nch == 1) {
+    AUX_FWD(1)
+  } else if (nch == 2) {
+    AUX_FWD(2)
+  } else {
+    AUX_FWD(4)
+  }
+#undef AUX_FWD
   // the block's sums go to its own slot of the partials buffer (summed by
   // the caller: deterministic, no atomics)
   __shared__ double red[4][kRowsPerPass];
@@ -332,16 +354,22 @@ __global__ __launch_bounds__(kThreadsAux) void aux_loss_bwd_kernel(AuxLossParams
   const int l = blockIdx.y;
   const Buf tb = p.tau[l], db = p.dtau[l];
   const int vt = vec_kind(tb, p.W), vk = vt == vec_kind(db, p.W) ? vt : 0;
-  if (vk == 1 && p.W == 64)
-    bwd_rows<1, true>(p, l, tb, db);
-  else if (vk == 1)
-    bwd_rows<1, false>(p, l, tb, db);
-  else if (vk == 2 && p.W == 64)
-    bwd_rows<2, true>(p, l, tb, db);
-  else if (vk == 2)
-    bwd_rows<2, false>(p, l, tb, db);
-  else
-    bwd_rows<0, false>(p, l, tb, db);
+  const int nch = p.W <= 64 ? 1 : p.W <= 128 ? 2 : 4;
+  const bool full = p.W == 64 * nch;
+#define AUX_BWD(N)                                                   \
+  if (vk == 1 && full) bwd_rows<1, true, N>(p, l, tb, db);           \
+  else if (vk == 1) bwd_rows<1, false, N>(p, l, tb, db);             \
+  else if (vk == 2 && full) bwd_rows<2, true, N>(p, l, tb, db);      \
+  else if (vk == 2) bwd_rows<2, false, N>(p, l, tb, db);             \
+  else bwd_rows<0, false, N>(p, l, tb, db);
+  if (nch == 1) {
+    AUX_BWD(1)
+  } else if (nch == 2) {
+    AUX_BWD(2)
+  } else {
+    AUX_BWD(4)
+  }
+#undef AUX_BWD
 }
 
 int launch_aux_loss(bool bwd, const AuxLossParams& p, hipStream_t st, hipError_t* err) {

@@ -611,7 +611,7 @@ int tension_aux_loss_fwd(const tension_buf* taus, int32_t L, int64_t B, int64_t 
   AuxLossParams p;
   memset(&p, 0, sizeof p);
   TRY(check_taus(taus, L, B, T, H, W, p.tau));
-  if (W > 64) return fail(TENSION_ERR_UNSUPPORTED, "aux loss: W=%lld > 64", (long long)W);
+  if (W > 256) return fail(TENSION_ERR_UNSUPPORTED, "aux loss: W=%lld > 256", (long long)W);
   if (!partials) return fail(TENSION_ERR_ARG, "partials is required");
   if (B * T * H * 8 > 0x7fffffffll * 256) return fail(TENSION_ERR_ARG, "aux loss: too many rows");
   p.acc = partials;
@@ -627,7 +627,7 @@ int tension_aux_loss_bwd(const tension_buf* taus, const tension_buf* dtaus, int3
   memset(&p, 0, sizeof p);
   TRY(check_taus(taus, L, B, T, H, W, p.tau));
   TRY(check_taus(dtaus, L, B, T, H, W, p.dtau));
-  if (W > 64) return fail(TENSION_ERR_UNSUPPORTED, "aux loss: W=%lld > 64", (long long)W);
+  if (W > 256) return fail(TENSION_ERR_UNSUPPORTED, "aux loss: W=%lld > 256", (long long)W);
   if (!coef) return fail(TENSION_ERR_ARG, "coef is required");
   if (B * T * H * 8 > 0x7fffffffll * 256) return fail(TENSION_ERR_ARG, "aux loss: too many rows");
   p.coef = coef;

@@ -477,15 +477,15 @@ class _AuxLossFn(torch.autograd.Function):
 def tension_aux_losses(all_tensions: list, window_groups: Optional[dict] = None):
     """(tension_diversity_loss, constraint_consistency_loss,
     tension_entropy_loss) of the same taus, in one fused pass on the GPU
-    when every tau has one [B, T, H, W] shape with W <= 64 (the model's
-    layers; each layer in its own float dtype, e.g. the float32 tau of the
+    when every tau has one [B, T, H, W] shape with W <= 256 (the model's
+    layers, e.g. the 350M preset's W = 256; each layer in its own float dtype, e.g. the float32 tau of the
     local layers beside the global layers' bf16 tau_local under autocast,
     all read into float32); otherwise the three functions above."""
     if not all_tensions:
         z = torch.tensor(0.0)
         return z, z, z
     shape = tuple(all_tensions[0].shape)
-    fused = (all_tensions[0].is_cuda and len(all_tensions) <= 32 and shape[-1] <= 64
+    fused = (all_tensions[0].is_cuda and len(all_tensions) <= 32 and shape[-1] <= 256
              and all(tuple(t.shape) == shape and t.device == all_tensions[0].device and t.dtype in _AUX_DTYPES
                      for t in all_tensions))
     if not fused:

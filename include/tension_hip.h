@@ -274,7 +274,7 @@ int tension_tau_aggregate(const tension_buf* taus, int32_t L, int64_t B,
 /* ---------------------------------------------------------------------------
  * The model's tau regularisers (model.py:498-611: tension_diversity_loss,
  * constraint_consistency_loss, tension_entropy_loss) over the tau of L <= 32
- * layers, each [B,T,H,W] (W <= 64, s[3] == 1), computed in fp32.
+ * layers, each [B,T,H,W] (W <= 256, s[3] == 1), computed in fp32.
  *
  * tension_aux_loss_fwd: partials (device double [L, P, 4], P =
  *   tension_aux_loss_partials(B,T,H)) receives, per layer and workgroup, the

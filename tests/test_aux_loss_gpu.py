@@ -43,6 +43,14 @@ def reference(taus, groups):
     # host sum of the partials; T = 1000 is not a multiple of the block
     (12, 2, 1024, 12, 64, torch.bfloat16, True),
     (3, 2, 1000, 12, 64, torch.float32, True),
+    # wider windows: two and four 8-slot chunks per lane (the 350M preset's
+    # W = 256, train.py:246-256), ragged widths and float32 / bf16 rows
+    (8, 2, 1024, 16, 256, torch.float32, True),
+    (8, 1, 700, 16, 256, torch.bfloat16, True),
+    (3, 2, 129, 3, 200, torch.float32, False),
+    (3, 2, 65, 2, 128, torch.bfloat16, False),
+    (2, 2, 100, 3, 100, torch.float32, False),
+    (2, 1, 40, 2, 77, torch.bfloat16, False),   # element loads (W not a multiple of 8)
 ])
 def test_fused_aux_losses_match_reference(dev, L, B, T, H, W, dtype, grouped):
     taus = taus_of(L * 100 + W, L, B, T, H, W, dtype, dev)
