@@ -54,6 +54,7 @@ SIGNATURES = {
     "tension_window_fwd": (_i32, [BufP] * 7 + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_window_bwd_workspace": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "tension_window_bwd": (_i32, [BufP] * 9 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
+    "tension_window_bwd_saved": (_i32, [BufP] * 11 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_window_bwd_dq": (_i32, [BufP] * 7 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_window_bwd_dkv": (_i32, [BufP] * 8 + [_vp] + [_i64] * 5 + [_f64, _i32, _vp]),
     "tension_global_fwd": (_i32, [BufP] * 7 + [_i64] * 5 + [_f64, _i32, _vp]),

@@ -292,10 +292,18 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
   const bool mf = mfma_ok_bwd(q, k, v, dout, bias, dq, nullptr, sh.D, flags);
   const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
   const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dq) && split_side(sk, dtau);
-  if (mf && out && mass) {
+  // the forward's saved output rows and tau mass (the tau-mass coefficients
+  // come from them instead of a pass over the band): the global bf16
+  // kernels, and the split kernels with float32 rows (whose dO . out does
+  // not cancel the way a bf16 out would); every other kernel ignores them
+  if (out && mass) {
     TRY(check_buf(out, "out", true, 3));
     TRY(check_buf(mass, "mass", true, -1));
-    if (aligned_bf16_rows(out) && mass->dtype == TENSION_F32) {
+    const bool f32_mass = mass->dtype == TENSION_F32;
+    const bool rows_mf = mf && global && aligned_bf16_rows(out) && f32_mass;
+    const bool rows_sp = sp && sk == SPLIT_F32 && ((flags & TENSION_NORM_MASS) || global) &&
+                         aligned_f32_rows(out) && f32_mass;
+    if (rows_mf || rows_sp) {
       p.out = make_buf(out);
       p.mass = make_buf(mass);
       p.coef_pre = 1;
@@ -397,10 +405,16 @@ int tension_window_bwd_dkv(const tension_buf* q, const tension_buf* k, const ten
   return band_bwd_dkv(q, k, v, dout, dtau, bias, dk, dv, ws, Shape{B, T, H, D}, W, scale, flags, stream, false);
 }
 
-int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
-                       const tension_buf* dtau, const tension_buf* bias, const tension_buf* dq,
-                       const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H,
-                       int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// tension_window_bwd with, optionally, the forward's output rows and tau
+// mass (see band_bwd_dq).
+int window_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
+               const tension_buf* dtau, const tension_buf* bias, const tension_buf* out, const tension_buf* mass,
+               const tension_buf* dq, const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B,
+               int64_t T, int64_t H, int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
   const Shape sh{B, T, H, D};
   if (W >= 1 && W <= 64) {
     // one fused kernel (no workspace traffic) when the MFMA path applies
@@ -420,8 +434,30 @@ int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension
       return run_band(3, KERNEL_MFMA, false, p, stream, "tension_window_bwd");
     }
   }
-  TRY(band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, sh, W, scale, flags, stream, false));
+  TRY(band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, sh, W, scale, flags, stream, false, out, mass));
   return band_bwd_dkv(q, k, v, dout, dtau, bias, dk, dv, ws, sh, W, scale, flags, stream, false);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tension_window_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* dout,
+                       const tension_buf* dtau, const tension_buf* bias, const tension_buf* dq,
+                       const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T, int64_t H,
+                       int64_t D, int64_t W, double scale, int32_t flags, tension_stream_t stream) {
+  return window_bwd(q, k, v, dout, dtau, bias, nullptr, nullptr, dq, dk, dv, ws, B, T, H, D, W, scale, flags,
+                    stream);
+}
+
+int tension_window_bwd_saved(const tension_buf* q, const tension_buf* k, const tension_buf* v,
+                             const tension_buf* dout, const tension_buf* dtau, const tension_buf* bias,
+                             const tension_buf* out, const tension_buf* mass, const tension_buf* dq,
+                             const tension_buf* dk, const tension_buf* dv, void* ws, int64_t B, int64_t T,
+                             int64_t H, int64_t D, int64_t W, double scale, int32_t flags,
+                             tension_stream_t stream) {
+  if (!out || !mass) return fail(TENSION_ERR_ARG, "tension_window_bwd_saved: out and mass are required");
+  return window_bwd(q, k, v, dout, dtau, bias, out, mass, dq, dk, dv, ws, B, T, H, D, W, scale, flags, stream);
 }
 
 int tension_global_fwd(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* out,

@@ -428,6 +428,11 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
 //         of the band stay in registers while the coefficients form.
 // MODE 2: tau-mass over a wider band: a first pass forms the coefficients,
 //         a second recomputes S and dP.
+// MODE 3: tau-mass with the forward's float32 output rows and tau mass
+//         (p.out, p.mass): a = 1 / max(m, 1e-6), c = (dO . out) a (zero
+//         where m < 1e-6, the clamp branch), then one pass.  out = msg a,
+//         so c = (dO . msg) a^2 = sum_s P dP / m^2; out is float32 (NT = 3),
+//         so dO . out does not cancel the way a bf16 out would.
 // The tau-mass coefficients of each query (dtau = a dP - c + dTau,
 // a = 1 / m, c = sum_s P dP / m^2, model.py:257-258 differentiated) go to
 // the workspace for the dK / dV kernel.
@@ -560,6 +565,34 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
   };
 
   if constexpr (MODE == 0) {
+    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+  } else if constexpr (MODE == 3) {
+    // dO . out over this lane's features (its dO terms summed back to the
+    // float32 value: t0 + t1 + t2 is exact in float32), then over the row
+    static_assert(NT == 3, "saved rows are float32 (the autocast flow)");
+    float dot = 0.f;
+    if (qok) {
+      const float* orow = (const float*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) {
+        const float* src = orow + 8 * (4 * ch + g);
+        const f32x4 o0 = *(const f32x4*)src, o1 = *(const f32x4*)(src + 4);
+        const float ov[8] = {o0[0], o0[1], o0[2], o0[3], o1[0], o1[1], o1[2], o1[3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          dot = fmaf((float)of[ch][0][e] + (float)of[ch][1][e] + (float)of[ch][2][e], ov[e], dot);
+      }
+    }
+    dot = wave_sum_g(dot);
+    const float m = qok ? ld<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2) : 1.f;
+    ca = 1.f / (m > kMassEps ? m : kMassEps);
+    cc = m >= kMassEps ? dot * ca : 0.f;
+    if (p.ws && qok && g == 0) {
+      const int64_t nws = (int64_t)p.B * p.T * p.H;
+      const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
+      ((float*)p.ws)[wi] = ca;
+      ((float*)p.ws)[nws + wi] = cc;
+    }
     stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
   } else if constexpr (MODE == 1) {
     // both blocks stay resident (buffers 0 and 1)
@@ -841,6 +874,12 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
     const bool opt = p.dtau.p != nullptr;
     if constexpr (NORM != NORM_MASS_) {
       XB_BT(xb_dq, , 0);
+    } else if constexpr (NT == 3) {
+      // a band within two blocks keeps P and dP in registers (faster than
+      // one pass from saved rows at W = 64: 42 against 48 us at config 2)
+      if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
+      else if (p.coef_pre) XB_BT(xb_dq, , 3);
+      else XB_BT(xb_dq, , 2);
     } else {
       if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
       else XB_BT(xb_dq, , 2);

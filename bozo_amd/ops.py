@@ -137,9 +137,18 @@ class _CausalTensionFn(torch.autograd.Function):
         if Bias is not None and tuple(Bias.shape) != (B, T, W):
             raise ValueError(f"bias must be [B, T, W]=[{B}, {T}, {W}], got {tuple(Bias.shape)}")
         tau = torch.empty(B, T, H, W, dtype=Q.dtype, device=Q.device) if return_tau else None
-        out = _window_fwd(Q, K, V, W, scale, tau, Bias, flags, None)
-        # the backward recomputes tau (and the tau mass) from the inputs
-        ctx.save_for_backward(Q, K, V, Bias)
+        # the backward recomputes tau from the inputs; in the autocast flow
+        # (float32 Q / K, bf16 V) under tau-mass it takes the per-query
+        # coefficients from the forward's float32 rows and tau mass
+        # (tension_window_bwd_saved: one pass over the band instead of two)
+        rows = _saved_rows_flow(Q, K, V, W, flags)
+        mass = torch.empty(B, T, H, dtype=torch.float32, device=Q.device) if rows else None
+        out = _window_fwd(Q, K, V, W, scale, tau, Bias, flags, mass)
+        if rows:
+            ctx.save_for_backward(Q, K, V, Bias, out, mass)
+        else:
+            ctx.save_for_backward(Q, K, V, Bias)
+        ctx.rows = rows
         ctx.W, ctx.scale, ctx.flags = W, scale, flags
         ctx.return_tau = return_tau
         if return_tau:
@@ -148,13 +157,25 @@ class _CausalTensionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        Q, K, V, Bias = ctx.saved_tensors
+        if ctx.rows:
+            Q, K, V, Bias, out, mass = ctx.saved_tensors
+        else:
+            (Q, K, V, Bias), out, mass = ctx.saved_tensors, None, None
         dTau = grads[1] if ctx.return_tau else None
-        dQ, dK, dV = _window_bwd(Q, K, V, grads[0], dTau, Bias, ctx.W, ctx.scale, ctx.flags)
+        dQ, dK, dV = _window_bwd(Q, K, V, grads[0], dTau, Bias, ctx.W, ctx.scale, ctx.flags, out, mass)
         return dQ, dK, dV, None, None, None, None, None
 
 
-def _window_bwd(Q, K, V, dOut, dTau, Bias, W, scale, flags):
+def _saved_rows_flow(Q: Tensor, K: Tensor, V: Tensor, W: int, flags: int) -> bool:
+    """Tau-mass in the reference's autocast flow (float32 Q / K, bf16 V, head
+    dim 32 / 64) with a window wider than 64: the backward takes its
+    coefficients from the forward's rows (narrower bands form them in
+    registers, which is faster)."""
+    return bool(flags & L.NORM_MASS) and W > 64 and Q.dtype == torch.float32 and K.dtype == torch.float32 \
+        and V.dtype == torch.bfloat16 and Q.shape[-1] in (32, 64)
+
+
+def _window_bwd(Q, K, V, dOut, dTau, Bias, W, scale, flags, out=None, mass=None):
     B, T, H, D = Q.shape
     dOut = _rows(dOut) if dOut is not None else torch.zeros_like(Q)
     dTau = _rows(dTau)
@@ -162,10 +183,16 @@ def _window_bwd(Q, K, V, dOut, dTau, Bias, W, scale, flags):
     lib = L.lib()
     ws = _ws(lib.tension_window_bwd_workspace(B, T, H, _acc_code(Q, K, V), flags), Q.device)
     with torch.cuda.device(Q.device):
-        L.check(lib.tension_window_bwd(
-            L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias),
-            L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, W,
-            float(scale), flags, _stream(Q)), "tension_window_bwd")
+        if out is not None:
+            L.check(lib.tension_window_bwd_saved(
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias), L.buf(out),
+                L.buf(mass), L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, W,
+                float(scale), flags, _stream(Q)), "tension_window_bwd_saved")
+        else:
+            L.check(lib.tension_window_bwd(
+                L.buf(Q), L.buf(K), L.buf(V), L.buf(dOut), L.buf(dTau), L.buf(Bias),
+                L.buf(dQ), L.buf(dK), L.buf(dV), _ptr(ws), B, T, H, D, W,
+                float(scale), flags, _stream(Q)), "tension_window_bwd")
     return dQ, dK, dV
 
 

@@ -123,6 +123,24 @@ int tension_window_bwd(const tension_buf* q, const tension_buf* k,
                        int64_t T, int64_t H, int64_t D, int64_t W,
                        double scale, int32_t flags, tension_stream_t stream);
 
+/* tension_window_bwd with the forward's output rows `out` ([B,T,H,D], as
+ * written by tension_window_fwd) and tau mass `mass` ([B,T,H] f32, the
+ * forward's `mass` output), both required.  No counterpart in the reference
+ * (its backward recomputes everything, ops.py:126-187): with
+ * TENSION_NORM_MASS on the float32-Q/K split kernels and a window wider
+ * than 64 the per-query coefficients then come from these rows --
+ * a = 1/max(m, 1e-6), c = dout.out * a (0 where m < 1e-6) -- in one pass
+ * over the band instead of two; every other case computes them as
+ * tension_window_bwd does.  Same results to float32 rounding. */
+int tension_window_bwd_saved(const tension_buf* q, const tension_buf* k,
+                             const tension_buf* v, const tension_buf* dout,
+                             const tension_buf* dtau, const tension_buf* bias,
+                             const tension_buf* out, const tension_buf* mass,
+                             const tension_buf* dq, const tension_buf* dk,
+                             const tension_buf* dv, void* workspace, int64_t B,
+                             int64_t T, int64_t H, int64_t D, int64_t W,
+                             double scale, int32_t flags, tension_stream_t stream);
+
 /* The two halves of tension_window_bwd, one kernel each.  _dq fills the
  * workspace that _dkv reads, so on one stream _dq must precede _dkv.
  * Counterparts: kernel.py:130-227 (dQ) and kernel.py:232-341 (dK/dV). */

@@ -219,6 +219,18 @@ def test_noalloc_refuses_requests_beyond_the_scratch(lib):
     assert b"fixed scratch" in lib.lib().tension_last_error()
 
 
+def test_window_bwd_saved_requires_rows(lib):
+    """tension_window_bwd_saved takes the forward's rows: a call without out or
+    mass is an argument error before any HIP call."""
+    b = _buf()
+    f = lib.lib().tension_window_bwd_saved
+    args = lambda out, mass: (b, b, b, b, None, None, out, mass, b, b, b, None,  # noqa: E731
+                              1, 16, 1, 16, 4, ctypes.c_double(4.0), 0, None)
+    assert f(*args(None, b)) == lib.ERR_ARG
+    assert f(*args(b, None)) == lib.ERR_ARG
+    assert b"out and mass are required" in lib.lib().tension_last_error()
+
+
 def test_no_cpu_fallback():
     from bozo_amd import causal_tension, global_tension
     x = torch.zeros(1, 8, 1, 16)

@@ -535,3 +535,48 @@ def test_tau_dtau_row_layouts_abi(dev, pad):
     assert torch.isnan(taup[..., W:]).all()  # the padding is not written
     for a, b in ((dq, qq.grad), (dk, kk.grad), (dv, vv.grad)):
         assert (a.float() - b.float()).abs().max().item() <= 2e-2 * b.float().abs().max().item()
+
+
+@pytest.mark.parametrize("W,D,tau", [(256, 64, False), (256, 64, True), (65, 32, True), (100, 64, True)])
+def test_window_bwd_saved_rows_match_recompute(dev, W, D, tau):
+    """tension_window_bwd_saved (coefficients from the forward's float32 rows
+    and tau mass, one pass) against tension_window_bwd (coefficients from a
+    pass over the band) through the C ABI, autocast flow, tau-mass: equal to
+    float32 rounding (max-abs 2e-7 on dQ, dK; dV bf16 to one rounding), and
+    both against the float64 oracle at the fp32 bound."""
+    import ctypes
+    from bozo_amd import _lib as L
+    B, T, H = 2, 300, 3
+    inp = mixed_inputs(B, T, H, seed=70 + W + D, W=W, dtau_std=0.1 if tau else None, D=D)
+    q, k, dO = (inp[n].to(dev) for n in ("Q", "K", "dO"))
+    v = inp["V"].to(dev)
+    dtau = inp["dTau"].to(dev) if tau else None
+    scale = math.sqrt(D)
+    lib, st = L.lib(), L.stream_handle(dev)
+    out = torch.empty_like(q)
+    mass = torch.empty(B, T, H, device=dev)
+    L.check(lib.tension_window_fwd(L.buf(q), L.buf(k), L.buf(v), L.buf(out), None, None, L.buf(mass),
+                                   B, T, H, D, W, ctypes.c_double(scale), L.NORM_MASS, st), "fwd")
+    res = []
+    for saved in (False, True):
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        ws = torch.empty(lib.tension_window_bwd_workspace(B, T, H, L.F32, L.NORM_MASS), dtype=torch.uint8,
+                         device=dev)
+        common = (L.buf(q), L.buf(k), L.buf(v), L.buf(dO), L.buf(dtau), None)
+        tail = (L.buf(dq), L.buf(dk), L.buf(dv), ctypes.c_void_p(ws.data_ptr()), B, T, H, D, W,
+                ctypes.c_double(scale), L.NORM_MASS, st)
+        if saved:
+            L.check(lib.tension_window_bwd_saved(*common, L.buf(out), L.buf(mass), *tail), "saved")
+        else:
+            L.check(lib.tension_window_bwd(*common, *tail), "recompute")
+        assert int(lib.tension_last_kernel()) == L.KERNEL_SPLIT_F32
+        res.append((dq, dk, dv))
+    torch.cuda.synchronize()
+    for name, a, b_ in zip(("dQ", "dK"), res[0], res[1]):
+        err = float((a - b_).abs().max())
+        print(f"  {name}: saved vs recompute max abs {err:.2e}", flush=True)
+        assert err <= 2e-7, (name, err)
+    assert float((res[0][2].float() - res[1][2].float()).abs().max()) <= 2 ** -8 * float(res[0][2].float().abs().max())
+    _, _, grads = oracle_run(inp, W, scale, normalize="mass", use_dtau=tau)
+    for got, want, name in zip(res[1][:2], grads[:2], ("dQ", "dK")):
+        check_fp32(got, want, name)
