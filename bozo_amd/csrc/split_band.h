@@ -428,11 +428,12 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
 //         of the band stay in registers while the coefficients form.
 // MODE 2: tau-mass over a wider band: a first pass forms the coefficients,
 //         a second recomputes S and dP.
-// MODE 3: tau-mass with the forward's float32 output rows and tau mass
-//         (p.out, p.mass): a = 1 / max(m, 1e-6), c = (dO . out) a (zero
-//         where m < 1e-6, the clamp branch), then one pass.  out = msg a,
-//         so c = (dO . msg) a^2 = sum_s P dP / m^2; out is float32 (NT = 3),
-//         so dO . out does not cancel the way a bf16 out would.
+// MODE 3: tau-mass with the forward's output rows and tau mass (p.out,
+//         p.mass): a = 1 / max(m, 1e-6), c = (dO . out) a (zero where
+//         m < 1e-6, the clamp branch), then one pass.  out = msg a, so
+//         c = (dO . msg) a^2 = sum_s P dP / m^2.  The host passes the rows
+//         for float32 out (NT = 3: dO . out does not cancel the way a bf16
+//         out does).
 // The tau-mass coefficients of each query (dtau = a dP - c + dTau,
 // a = 1 / m, c = sum_s P dP / m^2, model.py:257-258 differentiated) go to
 // the workspace for the dK / dV kernel.
@@ -569,18 +570,23 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
   } else if constexpr (MODE == 3) {
     // dO . out over this lane's features (its dO terms summed back to the
     // float32 value: t0 + t1 + t2 is exact in float32), then over the row
-    static_assert(NT == 3, "saved rows are float32 (the autocast flow)");
     float dot = 0.f;
     if (qok) {
-      const float* orow = (const float*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
+      const E* orow = (const E*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
 #pragma unroll
       for (int ch = 0; ch < D / 32; ++ch) {
-        const float* src = orow + 8 * (4 * ch + g);
-        const f32x4 o0 = *(const f32x4*)src, o1 = *(const f32x4*)(src + 4);
-        const float ov[8] = {o0[0], o0[1], o0[2], o0[3], o1[0], o1[1], o1[2], o1[3]};
+        bf16x8 ot[NT];
+        frag_row<NT>(orow, 0, 0, 1, 4 * ch + g, ot);  // the row's features 8 (4 ch + g) ..
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          dot = fmaf((float)of[ch][0][e] + (float)of[ch][1][e] + (float)of[ch][2][e], ov[e], dot);
+        for (int e = 0; e < 8; ++e) {
+          float ov = 0.f, dv_ = 0.f;
+#pragma unroll
+          for (int i = 0; i < NT; ++i) {
+            ov += (float)ot[i][e];
+            dv_ += (float)of[ch][i][e];
+          }
+          dot = fmaf(dv_, ov, dot);
+        }
       }
     }
     dot = wave_sum_g(dot);
@@ -880,7 +886,7 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
       if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
       else if (p.coef_pre) XB_BT(xb_dq, , 3);
       else XB_BT(xb_dq, , 2);
-    } else {
+    } else {  // bf16 rows: the coefficients from the band (a bf16 out would cancel)
       if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
       else XB_BT(xb_dq, , 2);
     }
