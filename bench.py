@@ -506,7 +506,8 @@ def bench_window_variants(dev, steps, warmup):
 def profile_kernels(n, dev):
     """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
     of each band kernel on rotated config-2 sets (bf16, then fp32 Q / K with
-    bf16 V), n config-4 decode steps
+    bf16 V), of the split kernels at the 350M preset's W = 256 shape (bf16
+    and fp32 Q / K), n config-4 decode steps
     over 4 rotated caches and n config-3 global forward + backward calls, then
     a plain device copy of
     known size (256 MiB read + 256 MiB written) whose FETCH_SIZE/WRITE_SIZE
@@ -521,7 +522,7 @@ def profile_kernels(n, dev):
         torch.cuda.synchronize()
     del fns
     # the reference's autocast dtype flow: fp32 (RoPE'd) Q / K, bf16 V, fp32
-    # out / dOut (the split-operand kernels mx_fwd / mx_dq / mx_dkv)
+    # out / dOut (the split-operand kernels xb_fwd / xb_dq / xb_dkv)
     mixed = [dict(Q=s["Q"].detach().float(), K=s["K"].detach().float(), V=s["V"].detach(),
                   dO=s["dO"].float()) for s in sets[:2]]
     del sets
@@ -531,6 +532,19 @@ def profile_kernels(n, dev):
             fns[i % 2][0][name]()
         torch.cuda.synchronize()
     del fns, mixed
+    # the 350M preset's local layer (B4 H16 T1024 W256) on the split kernels,
+    # bf16 and in the autocast flow, valid-count normalised (its CE-only step;
+    # distinct kernel instances from the tau-mass config-2 ones above)
+    wide = make_window_sets(2, 4, T, 16, D, dev, seed=11)
+    wide += [dict(Q=s["Q"].detach().float(), K=s["K"].detach().float(), V=s["V"].detach(),
+                  dO=s["dO"].float()) for s in wide]
+    fns = [kernel_fns(s, 256, math.sqrt(D), L.NORM_COUNT) for s in wide]
+    for name in ("fwd", "dq", "dkv"):
+        for i in range(n):
+            fns[i % 2][0][name]()       # bf16
+            fns[2 + i % 2][0][name]()   # fp32 Q / K, bf16 V
+        torch.cuda.synchronize()
+    del fns, wide
     # config-4 decode steps over 4 rotated caches, fresh q / k / v per step
     from bozo_amd import TensionDecodeCache
     N, Hd, Wd, NC = 64, 16, 256, 4
