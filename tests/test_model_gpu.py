@@ -175,21 +175,22 @@ def test_bf16_autocast_model_vs_reference_ops(dev, use_triton, return_all):
     assert e_grads[worst] < 4e-2, (worst, e_grads[worst])
 
 
-@pytest.mark.parametrize("return_all", [False, True])
-def test_117m_shape_step_vs_reference_ops(dev, return_all):
+@pytest.mark.parametrize("B,return_all", [(1, False), (1, True), (8, True)])
+def test_117m_shape_step_vs_reference_ops(dev, B, return_all):
     """Config 5's model (12 layers, dim 768, 12 heads, head_dim 64, vocab
-    32768, W = 64, global layers 3, 7, 11, RoPE) on one 1024-token sequence
-    under bf16 autocast: the kernels' logits, loss and every parameter
-    gradient against the same model with its tension ops swapped for the
-    reference's float32 math.  ``return_all`` is the reference-default step
-    (tau from every layer, the aux losses through dTau); without it, the
-    cross-entropy step (valid-count local layers)."""
+    32768, W = 64, global layers 3, 7, 11, RoPE) on B 1024-token sequences
+    under bf16 autocast (B = 8: the benchmark's batch, so every kernel runs at
+    its config-5 launch geometry): the kernels' logits, loss and every
+    parameter gradient against the same model with its tension ops swapped
+    for the reference's float32 math.  ``return_all`` is the
+    reference-default step (tau from every layer, the aux losses through
+    dTau); without it, the cross-entropy step (valid-count local layers)."""
     cfg = M.config_117m(dropout=0.0, use_triton=True)
     torch.manual_seed(4)
     m = M.TensionLM(cfg).to(dev).train()
     g = torch.Generator().manual_seed(14)
-    ids = torch.randint(0, cfg.vocab_size, (1, 1025), generator=g).to(dev)
-    print(f"[model 117m] return_all={return_all} params={m.num_params}", flush=True)
+    ids = torch.randint(0, cfg.vocab_size, (B, 1025), generator=g).to(dev)
+    print(f"[model 117m] B={B} return_all={return_all} params={m.num_params}", flush=True)
     lg, loss, grads = _run_bf16(m, ids[:, :-1], ids[:, 1:], return_all)
     with reference_ops():
         lr, loss_r, grads_r = _run_bf16(m, ids[:, :-1], ids[:, 1:], return_all)
