@@ -85,6 +85,8 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
 // bfloat16 V, else bf16 throughout; head dim 32 or 64; phase 0 forward,
 // 1 dQ, 2 dK / dV
 int launch_split(int phase, bool f32, const BandParams& p, hipStream_t st, hipError_t* err);
+// Compute units of the current device (queried once per device).
+int device_cus();
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);
 // bf16 / float32 rows (x_f32, y_f32), D % 16 == 0, 16-byte aligned rows and tables
 int launch_rope_vec(bool x_f32, bool y_f32, const RopeParams& p, hipStream_t st, hipError_t* err);

@@ -17,10 +17,9 @@ void launch_mfma_bwd_fused(const BandParams& p, hipStream_t st, unsigned nwg, in
 #define TENSION_BWD_WG_PER_CU 2
 #endif
 
-namespace {
-
 // Compute units of the current device (256 on MI355X), queried once per
-// device: the grids below are sized to whole rounds of resident workgroups.
+// device: the band kernels' grids are sized to whole rounds of resident
+// workgroups.
 int device_cus() {
   static std::atomic<int> cus[64];
   int dev = 0;
@@ -32,8 +31,6 @@ int device_cus() {
   }
   return n;
 }
-
-}  // namespace
 
 int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* err) {
   BandParams p = p_in;

@@ -15,9 +15,22 @@ int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hi
   BandParams p = p_in;
   if (p.D != 32 && p.D != 64) return -1;
   p.ntiles = (p.T + 63) / 64;
-  const int64_t nwg = (int64_t)p.B * p.H * p.ntiles;
+  int64_t nwg = (int64_t)p.B * p.H * p.ntiles;
   if (nwg <= 0) return -1;
   if (nwg > 0x7fffffff) return kGridTooLarge;
+  // p.chunk > 0: runs of consecutive key tiles per workgroup (p.chunk runs
+  // per (b, h)) for the dK / dV kernel of a local window W <= 64, sized for
+  // about two resident workgroups per CU; 0: one tile per workgroup
+  p.chunk = 0;
+  if (phase == 2 && !p.glob && p.win >= 1 && p.win <= 64) {
+    const int64_t bh = (int64_t)p.B * p.H;
+    int64_t runs = (2 * (int64_t)device_cus() + bh / 2) / bh;
+    if (runs < 1) runs = 1;
+    if (runs < p.ntiles) {
+      p.chunk = (int)runs;
+      nwg = bh * runs;
+    }
+  }
   const unsigned n = (unsigned)nwg;
   switch (phase) {
     case 0: (f32 ? launch_split_fwd_f32 : launch_split_fwd_bf16)(p, st, n); break;

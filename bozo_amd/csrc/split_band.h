@@ -81,25 +81,55 @@ __device__ __forceinline__ void pack_terms(const float* lo4, const float* hi4, b
 }
 
 // Operand fragment from global memory: features 8 chunk .. +7 of row `row`
-// of a tensor of Elem<NT> (zero outside [0, T)).
+// of a tensor of Elem<NT> (zero outside [0, T)), loaded as stored
+// (frag_load) and then as NT terms (frag_terms), so a load can run ahead of
+// its use; frag_row does both.
+template <int NT>
+struct RawFrag;
+template <>
+struct RawFrag<1> {
+  u16x8 a;
+};
+template <>
+struct RawFrag<3> {
+  f32x4 a, b;
+};
+
+template <int NT>
+__device__ __forceinline__ RawFrag<NT> frag_load(const Elem<NT>* base, int64_t rs, int row, int T, int chunk) {
+  RawFrag<NT> x;
+  const bool ok = row >= 0 && row < T;
+  const Elem<NT>* src = base + (int64_t)row * rs + 8 * chunk;
+  if constexpr (NT == 1) {
+    x.a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (ok) x.a = *(const u16x8*)src;
+  } else {
+    x.a = x.b = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (ok) {
+      x.a = *(const f32x4*)src;
+      x.b = *(const f32x4*)(src + 4);
+    }
+  }
+  return x;
+}
+
+template <int NT>
+__device__ __forceinline__ void frag_terms(const RawFrag<NT>& x, bf16x8* t) {
+  if constexpr (NT == 1) {
+    t[0] = __builtin_bit_cast(bf16x8, x.a);
+  } else {
+    const float v[8] = {x.a[0], x.a[1], x.a[2], x.a[3], x.b[0], x.b[1], x.b[2], x.b[3]};
+    u16x8 u[NT];
+    split8<NT>(v, u);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) t[i] = __builtin_bit_cast(bf16x8, u[i]);
+  }
+}
+
 template <int NT>
 __device__ __forceinline__ void frag_row(const Elem<NT>* base, int64_t rs, int row, int T, int chunk,
                                          bf16x8* t) {
-  u16x8 u[NT];
-#pragma unroll
-  for (int i = 0; i < NT; ++i) u[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-  if (row >= 0 && row < T) {
-    const Elem<NT>* src = base + (int64_t)row * rs + 8 * chunk;
-    if constexpr (NT == 1) {
-      u[0] = *(const u16x8*)src;
-    } else {
-      const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
-      const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-      split8<NT>(x, u);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < NT; ++i) t[i] = __builtin_bit_cast(bf16x8, u[i]);
+  frag_terms<NT>(frag_load<NT>(base, rs, row, T, chunk), t);
 }
 
 // ----------------------------------------------------------------- staging
@@ -696,6 +726,172 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
 
 // ----------------------------------------------------------------- dK / dV
 
+// One key tile's lane state in the dK / dV kernels: the lane's key row as B
+// operands (K as terms, V exact), the queries that see it, its dK / dV
+// accumulators, and the number of query tiles whose band reaches the tile.
+template <int NT, int D>
+struct KeyTile {
+  bf16x8 kf[D / 32][NT], vf[D / 32];
+  f32x4 dk[D / 16], dv[D / 16];
+  int tk, qlo, qhi, wq_lo, wq_hi, nqt;
+};
+
+// Key tile k0's geometry for lane (wave, c); accumulators cleared.
+template <int NT, int D>
+__device__ __forceinline__ void key_tile_init(const BandParams& p, int k0, int wave, int c, KeyTile<NT, D>& kt) {
+  const int T = p.T;
+  kt.tk = k0 + wave * 16 + c;
+  // queries that see this lane's key: [tk + 1 - diag, min(tk + win, T - 1)]
+  kt.qlo = kt.tk + 1 - p.diag;
+  kt.qhi = kt.tk >= T ? -1 : (kt.tk > T - 1 - p.win ? T - 1 : kt.tk + p.win);
+  // queries that see any key of this wave (a 16-query group outside is skipped)
+  const int ka = k0 + wave * 16;
+  const int kz = ka + 15 < T - 1 ? ka + 15 : T - 1;
+  kt.wq_lo = ka + 1 - p.diag;
+  kt.wq_hi = kz < ka ? -1 : (kz > T - 1 - p.win ? T - 1 : kz + p.win);
+  // query tiles k .. k + nqt - 1
+  const int last_q = k0 + kTile - 1 > T - 1 - p.win ? T - 1 : k0 + kTile - 1 + p.win;
+  kt.nqt = last_q < k0 ? 0 : (last_q >> 6) - (k0 >> 6) + 1;
+#pragma unroll
+  for (int m = 0; m < D / 16; ++m) kt.dk[m] = kt.dv[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// The lane's key row (features 8 (4 ch + g) .. +7 of K and V) as loaded.
+template <int NT, int D>
+struct KeyRaw {
+  RawFrag<NT> k[D / 32];
+  RawFrag<1> v[D / 32];
+};
+
+template <int NT, int D>
+__device__ __forceinline__ KeyRaw<NT, D> key_raw_load(const Elem<NT>* kb_, int64_t ks, const bf16* vb_, int64_t vs,
+                                                      int tk, int T, int g) {
+  KeyRaw<NT, D> r;
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    r.k[ch] = frag_load<NT>(kb_, ks, tk, T, 4 * ch + g);
+    r.v[ch] = frag_load<1>(vb_, vs, tk, T, 4 * ch + g);
+  }
+  return r;
+}
+
+template <int NT, int D>
+__device__ __forceinline__ void key_raw_terms(const KeyRaw<NT, D>& r, KeyTile<NT, D>& kt) {
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    frag_terms<NT>(r.k[ch], kt.kf[ch]);
+    frag_terms<1>(r.v[ch], &kt.vf[ch]);
+  }
+}
+
+// Query tile q0 into LDS: Q terms at base, dOut terms after them, and its
+// rows' coefficients a, c (tau mass: from the workspace the dQ kernel wrote;
+// valid count: 1 / count; raw: 1, 0).
+template <int NT, int D, int NORM>
+__device__ __forceinline__ void dkv_stage(const BandParams& p, bf16* base, float* sa_, float* scf_, int q0,
+                                          const Raw<NT>& qx, const Raw<NT>& ox, int b, int h, int tid) {
+  store_raw<NT>(qx, base, tid);
+  store_raw<NT>(ox, base + NT * kDTile, tid);
+  if (tid < kTile) {
+    const int t = q0 + tid;
+    float a = 1.f, cv = 0.f;
+    if (t < p.T) {
+      if (NORM == NORM_MASS_) {
+        const int64_t nws = (int64_t)p.B * p.T * p.H;
+        const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
+        a = ((const float*)p.ws)[wi];
+        cv = ((const float*)p.ws)[nws + wi];
+      } else if (NORM == NORM_COUNT_) {
+        const int cnt = t < p.W ? t : p.W;
+        a = 1.f / (float)(cnt > 1 ? cnt : 1);
+      }
+    }
+    sa_[tid] = a;
+    scf_[tid] = cv;
+  }
+}
+
+// One query tile q0 (terms in LDS at qt, coefficient rows sa_ / scf_)
+// against key tile kt:  dV^T += dO^T (a P),  dK^T += Q^T G.  dtb / bb: dTau
+// and bias of this (b, h) (dtype of Q / float32).
+template <int NT, int D, bool BIAS, bool DTAU>
+__device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, const float* sa_, const float* scf_,
+                                          int q0, KeyTile<NT, D>& kt, const Elem<NT>* dtb, const float* bb,
+                                          float k2, int g, int c) {
+  const bf16* ot = qt + NT * kDTile;
+  float Pa[4][4], G[4][4];
+  bool live[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int qa = q0 + 16 * j;
+    live[j] = qa + 15 >= kt.wq_lo && qa <= kt.wq_hi;
+    if (!live[j]) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Pa[j][r] = G[j][r] = 0.f;
+      continue;
+    }
+    // S = Q K^T, dP = dO V^T: queries 16 j + 4 g + r (rows), key c (column)
+    f32x4 sv = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ch = 0; ch < D / 32; ++ch) {
+      bf16x8 qa_[NT], oa_[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        qa_[t] = dt_row8(qt + t * kDTile, 16 * j + c, 4 * ch + g);
+        oa_[t] = dt_row8(ot + t * kDTile, 16 * j + c, 4 * ch + g);
+      }
+      sv = mmx<NT, NT, 2>(qa_, kt.kf[ch], sv);
+      dp = mmx<NT, 1, 2>(oa_, &kt.vf[ch], dp);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ql = 16 * j + 4 * g + r;  // query - q0
+      const int t = q0 + ql;
+      const bool ok = t >= kt.qlo && t <= kt.qhi;
+      float b2 = 0.f;
+      if (BIAS && ok) b2 = -kLog2e * bb[(int64_t)t * p.bias.s1 + bias_col(p, t, kt.tk)];
+      const float pv = sigmoid_scaled(sv[r], k2, b2);
+      const float a = sa_[ql];
+      float dt = fmaf(dp[r], a, -scf_[ql]);
+      if (DTAU && ok) {
+        const int col = tau_col(p, t, kt.tk);
+        if (col >= 0) dt += (float)dtb[(int64_t)t * p.dtau.s1 + col];
+      }
+      Pa[j][r] = ok ? pv * a : 0.f;
+      G[j][r] = ok ? dt * (pv - pv * pv) : 0.f;
+    }
+  }
+  // dV^T += dO^T (a P),  dK^T += Q^T G over 32-query pairs
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    if (!live[2 * kk] && !live[2 * kk + 1]) continue;
+    bf16x8 ps[NT], gs[NT];
+    pack_terms<NT>(Pa[2 * kk], Pa[2 * kk + 1], ps);
+    pack_terms<NT>(G[2 * kk], G[2 * kk + 1], gs);
+#pragma unroll
+    for (int m = 0; m < D / 16; ++m) {
+      bf16x8 oa_[NT], qa_[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        oa_[t] = dt_tr8(ot + t * kDTile, m, 32 * kk, g, c);
+        qa_[t] = dt_tr8(qt + t * kDTile, m, 32 * kk, g, c);
+      }
+      kt.dv[m] = mmx<NT, NT, 1>(oa_, ps, kt.dv[m]);
+      kt.dk[m] = mmx<NT, NT, 2>(qa_, gs, kt.dk[m]);
+    }
+  }
+}
+
+// The lane's dK row (dtype of Q; times 1 / scale) and dV row (bf16).
+template <int NT, int D>
+__device__ __forceinline__ void dkv_store(const BandParams& p, const KeyTile<NT, D>& kt, int b, int h,
+                                          float inv_scale, int g) {
+  if (kt.tk >= p.T) return;
+  using E = Elem<NT>;
+  store_acc<E, D>((E*)p.dk.p + b * p.dk.s0 + (int64_t)kt.tk * p.dk.s1 + h * p.dk.s2, kt.dk, inv_scale, g);
+  store_acc<bf16, D>((bf16*)p.dv.p + b * p.dv.s0 + (int64_t)kt.tk * p.dv.s1 + h * p.dv.s2, kt.dv, 1.f, g);
+}
+
 // Key tile k: the query tiles whose band reaches it pass through LDS in
 // turn (Q and dOut as NT terms each, plus their rows' coefficients a, c).
 template <int NT, int D, int NORM, bool BIAS, bool DTAU>
@@ -710,19 +906,6 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
   const TileId id = tile_id(p, false);
   const int b = id.b, h = id.h, T = p.T;
   const int k0 = id.tile * kTile;
-  const int tk = k0 + wave * 16 + c;
-  const bool kok = tk < T;
-  // queries that see this lane's key: [tk + 1 - diag, min(tk + win, T - 1)]
-  const int qlo = tk + 1 - p.diag;
-  const int qhi = !kok ? -1 : (tk > T - 1 - p.win ? T - 1 : tk + p.win);
-  // queries that see any key of this wave (a 16-query group outside is skipped)
-  const int ka = k0 + wave * 16;
-  const int kz = ka + 15 < T - 1 ? ka + 15 : T - 1;
-  const int wq_lo = ka + 1 - p.diag;
-  const int wq_hi = kz < ka ? -1 : (kz > T - 1 - p.win ? T - 1 : kz + p.win);
-  // query tiles k .. k + nqt - 1
-  const int last_q = k0 + kTile - 1 > T - 1 - p.win ? T - 1 : k0 + kTile - 1 + p.win;
-  const int nqt = last_q < k0 ? 0 : (last_q >> 6) - id.tile + 1;
 
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
@@ -730,48 +913,20 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
   const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
 
-  // this lane's key row as B operands: K as terms, V exact
-  bf16x8 kf[D / 32][NT], vf[D / 32];
-#pragma unroll
-  for (int ch = 0; ch < D / 32; ++ch) {
-    frag_row<NT>(kb_, p.k.s1, tk, T, 4 * ch + g, kf[ch]);
-    frag_row<1>(vb_, p.v.s1, tk, T, 4 * ch + g, &vf[ch]);
-  }
-
-  auto stage = [&](int buf, int q0, const Raw<NT>& qx, const Raw<NT>& ox) {
-    bf16* base = lds + buf * TPB * kDTile;
-    store_raw<NT>(qx, base, tid);
-    store_raw<NT>(ox, base + NT * kDTile, tid);
-    if (tid < kTile) {
-      const int t = q0 + tid;
-      float a = 1.f, cv = 0.f;
-      if (t < T) {
-        if (NORM == NORM_MASS_) {
-          const int64_t nws = (int64_t)p.B * p.T * p.H;
-          const int64_t wi = ((int64_t)b * p.T + t) * p.H + h;
-          a = ((const float*)p.ws)[wi];
-          cv = ((const float*)p.ws)[nws + wi];
-        } else if (NORM == NORM_COUNT_) {
-          const int cnt = t < p.W ? t : p.W;
-          a = 1.f / (float)(cnt > 1 ? cnt : 1);
-        }
-      }
-      sa[buf][tid] = a;
-      scf[buf][tid] = cv;
-    }
-  };
+  KeyTile<NT, D> kt;
+  key_tile_init<NT, D>(p, k0, wave, c, kt);
+  key_raw_terms<NT, D>(key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
 
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
   // dTau (dtype of Q, host-checked) and bias (float32) of this (b, h)
   const E* const dtb = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;
   const float* const bb = BIAS ? (const float*)p.bias.p + b * p.bias.s0 : nullptr;
-  f32x4 dk[D / 16], dv[D / 16];
-#pragma unroll
-  for (int m = 0; m < D / 16; ++m) dk[m] = dv[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const int nqt = kt.nqt;
   if (nqt > 0) {
-    stage(0, k0, load_raw<NT, D>(qb_, p.q.s1, k0, T, tid), load_raw<NT, D>(ob_, p.dout.s1, k0, T, tid));
+    dkv_stage<NT, D, NORM>(p, lds, sa[0], scf[0], k0, load_raw<NT, D>(qb_, p.q.s1, k0, T, tid),
+                           load_raw<NT, D>(ob_, p.dout.s1, k0, T, tid), b, h, tid);
     __syncthreads();
   }
   for (int i = 0; i < nqt; ++i) {
@@ -783,78 +938,82 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
       qn = load_raw<NT, D>(qb_, p.q.s1, q0 + kTile, T, tid);
       on = load_raw<NT, D>(ob_, p.dout.s1, q0 + kTile, T, tid);
     }
-    const bf16* qt = lds + buf * TPB * kDTile;
-    const bf16* ot = qt + NT * kDTile;
-    float Pa[4][4], G[4][4];
-    bool live[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int qa = q0 + 16 * j;
-      live[j] = qa + 15 >= wq_lo && qa <= wq_hi;
-      if (!live[j]) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Pa[j][r] = G[j][r] = 0.f;
-        continue;
-      }
-      // S = Q K^T, dP = dO V^T: queries 16 j + 4 g + r (rows), key c (column)
-      f32x4 sv = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ch = 0; ch < D / 32; ++ch) {
-        bf16x8 qa_[NT], oa_[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          qa_[t] = dt_row8(qt + t * kDTile, 16 * j + c, 4 * ch + g);
-          oa_[t] = dt_row8(ot + t * kDTile, 16 * j + c, 4 * ch + g);
-        }
-        sv = mmx<NT, NT, 2>(qa_, kf[ch], sv);
-        dp = mmx<NT, 1, 2>(oa_, &vf[ch], dp);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int ql = 16 * j + 4 * g + r;  // query - q0
-        const int t = q0 + ql;
-        const bool ok = t >= qlo && t <= qhi;
-        float b2 = 0.f;
-        if (BIAS && ok) b2 = -kLog2e * bb[(int64_t)t * p.bias.s1 + bias_col(p, t, tk)];
-        const float pv = sigmoid_scaled(sv[r], k2, b2);
-        const float a = sa[buf][ql];
-        float dt = fmaf(dp[r], a, -scf[buf][ql]);
-        if (DTAU && ok) {
-          const int col = tau_col(p, t, tk);
-          if (col >= 0) dt += (float)dtb[(int64_t)t * p.dtau.s1 + col];
-        }
-        Pa[j][r] = ok ? pv * a : 0.f;
-        G[j][r] = ok ? dt * (pv - pv * pv) : 0.f;
-      }
-    }
-    // dV^T += dO^T (a P),  dK^T += Q^T G over 32-query pairs
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      if (!live[2 * kk] && !live[2 * kk + 1]) continue;
-      bf16x8 ps[NT], gs[NT];
-      pack_terms<NT>(Pa[2 * kk], Pa[2 * kk + 1], ps);
-      pack_terms<NT>(G[2 * kk], G[2 * kk + 1], gs);
-#pragma unroll
-      for (int m = 0; m < D / 16; ++m) {
-        bf16x8 oa_[NT], qa_[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          oa_[t] = dt_tr8(ot + t * kDTile, m, 32 * kk, g, c);
-          qa_[t] = dt_tr8(qt + t * kDTile, m, 32 * kk, g, c);
-        }
-        dv[m] = mmx<NT, NT, 1>(oa_, ps, dv[m]);
-        dk[m] = mmx<NT, NT, 2>(qa_, gs, dk[m]);
-      }
-    }
+    dkv_visit<NT, D, BIAS, DTAU>(p, lds + buf * TPB * kDTile, sa[buf], scf[buf], q0, kt, dtb, bb, k2, g, c);
     if (more) {
       if (NBUF == 1) __syncthreads();  // every wave is done with the buffer
-      stage(NBUF == 2 ? (buf ^ 1) : 0, q0 + kTile, qn, on);
+      const int nb = NBUF == 2 ? (buf ^ 1) : 0;
+      dkv_stage<NT, D, NORM>(p, lds + nb * TPB * kDTile, sa[nb], scf[nb], q0 + kTile, qn, on, b, h, tid);
       __syncthreads();
     }
   }
-  if (!kok) return;
-  store_acc<E, D>((E*)p.dk.p + b * p.dk.s0 + (int64_t)tk * p.dk.s1 + h * p.dk.s2, dk, inv_scale, g);
-  store_acc<bf16, D>((bf16*)p.dv.p + b * p.dv.s0 + (int64_t)tk * p.dv.s1 + h * p.dv.s2, dv, 1.f, g);
+  dkv_store<NT, D>(p, kt, b, h, inv_scale, g);
+}
+
+// Runs of key tiles for local windows W <= 64, where key tile k is seen by
+// query tiles k and k + 1 only: a workgroup owns key tiles [kA, kB) of one
+// (b, h) (p.chunk runs per (b, h)) and walks query tiles kA .. kB once --
+// query tile k + 1 serves the second visit of key tile k and the first of
+// key tile k + 1 from the same LDS buffer -- with the next query tile
+// loading into registers during a key tile's first visit and the next key
+// rows during its second.
+template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+__global__ __launch_bounds__(kThreads) void xb_dkv_run(BandParams p) {
+  constexpr int TPB = 2 * NT;
+  __shared__ __attribute__((aligned(16))) bf16 lds[TPB * kDTile];
+  __shared__ float sa[kTile], scf[kTile];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int nr = p.chunk;
+  const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+  const int bh = id / nr, run = id % nr;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int kA = (int)((int64_t)run * p.ntiles / nr);
+  const int kB = (int)((int64_t)(run + 1) * p.ntiles / nr);
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  const float inv_scale = (float)(1.0 / p.scale);
+  const float k2 = -kLog2e * inv_scale;
+  const E* const dtb = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;
+  const float* const bb = BIAS ? (const float*)p.bias.p + b * p.bias.s0 : nullptr;
+  if (kA >= kB) return;
+
+  KeyTile<NT, D> kt;
+  key_tile_init<NT, D>(p, kA * kTile, wave, c, kt);
+  key_raw_terms<NT, D>(key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
+  dkv_stage<NT, D, NORM>(p, lds, sa, scf, kA * kTile, load_raw<NT, D>(qb_, p.q.s1, kA * kTile, T, tid),
+                         load_raw<NT, D>(ob_, p.dout.s1, kA * kTile, T, tid), b, h, tid);
+  __syncthreads();
+  // LDS holds query tile k at the top of each trip: tile k + 1 sees every
+  // key tile k < ntiles - 1 (W >= 1), so the trip before staged it
+  for (int k = kA; k < kB; ++k) {
+    const int k0 = k * kTile;
+    const bool two = kt.nqt > 1;  // query tile k + 1 sees this key tile
+    Raw<NT> qn, on;
+    if (two) {
+      qn = load_raw<NT, D>(qb_, p.q.s1, k0 + kTile, T, tid);
+      on = load_raw<NT, D>(ob_, p.dout.s1, k0 + kTile, T, tid);
+    }
+    dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, k0, kt, dtb, bb, k2, g, c);
+    if (two) {
+      __syncthreads();  // every wave is done with query tile k
+      dkv_stage<NT, D, NORM>(p, lds, sa, scf, k0 + kTile, qn, on, b, h, tid);
+      __syncthreads();
+    }
+    const bool next = k + 1 < kB;
+    KeyRaw<NT, D> kr;
+    if (next) kr = key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, k0 + kTile + wave * 16 + c, T, g);
+    if (two) dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, k0 + kTile, kt, dtb, bb, k2, g, c);
+    dkv_store<NT, D>(p, kt, b, h, inv_scale, g);
+    if (next) {
+      key_tile_init<NT, D>(p, k0 + kTile, wave, c, kt);
+      key_raw_terms<NT, D>(kr, kt);
+    }
+  }
 }
 
 // ----------------------------------------------------------------- launch
@@ -892,7 +1051,8 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
     }
   } else {
     const bool opt = p.dtau.p != nullptr;
-    XB_BT(xb_dkv);
+    if (p.chunk > 0) XB_BT(xb_dkv_run);
+    else XB_BT(xb_dkv);
   }
 #undef XB_BT
 }
