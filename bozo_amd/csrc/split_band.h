@@ -467,55 +467,53 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
 // The tau-mass coefficients of each query (dtau = a dP - c + dTau,
 // a = 1 / m, c = sum_s P dP / m^2, model.py:257-258 differentiated) go to
 // the workspace for the dK / dV kernel.
-template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
-__global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
-  constexpr int NBUF = (NT == 1 || MODE == 1) ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
-  __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, c = lane & 15;
-  const TileId id = tile_id(p, p.glob != 0);
-  const int b = id.b, h = id.h, T = p.T;
-  const int t0 = id.tile * kTile;
-  const int tq = t0 + wave * 16 + c;
-  const bool qok = tq < T;
-  const int lo = tq - p.win > 0 ? tq - p.win : 0;
-  const int hi = qok ? tq - 1 + p.diag : -1;
-  const WaveBand wb = wave_band(p, t0 + wave * 16);
-  const Blocks bl = band_blocks(p, t0);
 
+// One query tile's lane state in the dQ kernels -- the lane's query row
+// (Q and dOut as terms), its band, the coefficients a = ca, c = cc, the dQ
+// accumulators -- and the pieces the MODE passes are made of.  dbh / dst:
+// dTau of this (b, h) and the wave's staging rows.
+template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+struct DqTile {
   using E = Elem<NT>;
-  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
-  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
-  const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  int b, h, g, c, lane;
+  int t0, t0w, tq, lo, hi;
+  bool qok;
+  WaveBand wb;
+  Blocks bl;
+  const float* brow;
+  const E* dbh;
+  E* dst;
+  float k2, ca, cc, msum, dsum;
   bf16x8 qf[D / 32][NT], of[D / 32][NT];
-#pragma unroll
-  for (int ch = 0; ch < D / 32; ++ch) {
-    frag_row<NT>(qb_, p.q.s1, tq, T, 4 * ch + g, qf[ch]);
-    frag_row<NT>(ob_, p.dout.s1, tq, T, 4 * ch + g, of[ch]);
-  }
-
-  const float inv_scale = (float)(1.0 / p.scale);
-  const float k2 = -kLog2e * inv_scale;
-  float ca = 1.f, cc = 0.f;
-  if (NORM == NORM_COUNT_) {
-    const int cnt = tq < p.W ? tq : p.W;
-    ca = 1.f / (float)(cnt > 1 ? cnt : 1);
-  }
-  // this lane's query row of dTau (dtype of Q, host-checked) and of the bias
-  const E* const dbh = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;  // this (b, h)
-  E* const dst = dstage + (DTAU ? wave * kStageRows : 0);
-  const int t0w = t0 + wave * 16;
-  const int tr = qok ? tq : T - 1;
-  const float* const brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
   f32x4 acc[D / 16];
+
+  // the tile at t0 for wave `wave`: band, bias row, count coefficient,
+  // cleared sums and accumulators (the fragments are set apart)
+  __device__ __forceinline__ void at(const BandParams& p, int t0_, int wave) {
+    const int T = p.T;
+    t0 = t0_;
+    t0w = t0 + wave * 16;
+    tq = t0w + c;
+    qok = tq < T;
+    lo = tq - p.win > 0 ? tq - p.win : 0;
+    hi = qok ? tq - 1 + p.diag : -1;
+    wb = wave_band(p, t0w);
+    bl = band_blocks(p, t0);
+    const int tr = qok ? tq : T - 1;
+    brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
+    ca = 1.f;
+    cc = 0.f;
+    if (NORM == NORM_COUNT_) {
+      const int cnt = tq < p.W ? tq : p.W;
+      ca = 1.f / (float)(cnt > 1 ? cnt : 1);
+    }
+    msum = dsum = 0.f;
 #pragma unroll
-  for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   // S^T and dP^T (keys 16 j + 4 g + r, query c) of one 16-key group
-  auto sdp = [&](const bf16* kt, int j, f32x4& sc, f32x4& dp) {
+  __device__ __forceinline__ void sdp(const bf16* kt, int j, f32x4& sc, f32x4& dp) const {
     sc = scores_t<NT, D>(kt, qf, j, g, c);
     dp = f32x4{0.f, 0.f, 0.f, 0.f};
     const bf16* vt = kt + NT * kDTile;
@@ -524,21 +522,24 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
       const bf16x8 va = dt_row8(vt, 16 * j + c, 4 * ch + g);
       dp = mmx<1, NT, 2>(&va, of[ch], dp);
     }
-  };
+  }
+
   // tau (masked) of one element
-  auto tau_of = [&](float s, int key, bool ok) {
+  __device__ __forceinline__ float tau_of(const BandParams& p, float s, int key, bool ok) const {
     float b2 = 0.f;
     if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
     return ok ? sigmoid_scaled(s, k2, b2) : 0.f;
-  };
-  // G = tau (1 - tau) (a dP - c + dTau), zero off the band (dtv: the
-  // staged dTau of the pair, zero where it has no slot)
-  auto g_of = [&](float pv, float dpv, float dtv, bool ok) {
+  }
+
+  // G = tau (1 - tau) (a dP - c + dTau), zero off the band (dtv: the staged
+  // dTau of the pair, zero where it has no slot)
+  __device__ __forceinline__ float g_of(float pv, float dpv, float dtv, bool ok) const {
     const float dt = fmaf(dpv, ca, -cc) + dtv;
     return ok ? dt * (pv - pv * pv) : 0.f;
-  };
+  }
+
   // dQ^T += K^T G^T over 32-key pairs (A = K^T read transposed)
-  auto dq_product = [&](const bf16* kt, const int* kind, float (*G)[4]) {
+  __device__ __forceinline__ void dq_product(const bf16* kt, const int* kind, float (*G)[4]) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       if (kind[2 * kk] == 0 && kind[2 * kk + 1] == 0) continue;
@@ -552,10 +553,11 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
         acc[m] = mmx<NT, NT, 2>(ka, gs, acc[m]);
       }
     }
-  };
+  }
+
   // one block's S, dP -> G -> dQ with the coefficients known; with dTau its
   // rows are loaded before the products and staged through LDS after them
-  auto g_pass = [&](const bf16* kt, int kb0) {
+  __device__ __forceinline__ void g_pass(const BandParams& p, const bf16* kt, int kb0) {
     E dv[DTAU ? 16 : 1];
     if constexpr (DTAU) dtau_rows_load(p, dbh, dv, t0w, kb0, lane);
     f32x4 sc[4], dp[4];
@@ -575,31 +577,113 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
-        G[j][r] = kind[j] != 0 ? g_of(tau_of(sc[j][r], key, ok), dp[j][r], dtv[r], ok) : 0.f;
+        G[j][r] = kind[j] != 0 ? g_of(tau_of(p, sc[j][r], key, ok), dp[j][r], dtv[r], ok) : 0.f;
       }
     }
     dq_product(kt, kind, G);
-  };
-  float msum = 0.f, dsum = 0.f;
-  auto coefficients = [&]() {
+  }
+
+  // a, c from the band sums (msum = sum P, dsum = sum P dP over the row)
+  __device__ __forceinline__ void coefficients(const BandParams& p) {
     msum = wave_sum_g(msum);
     dsum = wave_sum_g(dsum);
     const float m = msum > kMassEps ? msum : kMassEps;
     ca = 1.f / m;
     cc = msum >= kMassEps ? dsum * ca * ca : 0.f;
+    put_coefficients(p);
+  }
+
+  __device__ __forceinline__ void put_coefficients(const BandParams& p) const {
     if (p.ws && qok && g == 0) {
       const int64_t nws = (int64_t)p.B * p.T * p.H;
       const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
       ((float*)p.ws)[wi] = ca;
       ((float*)p.ws)[nws + wi] = cc;
     }
-  };
+  }
 
-  if constexpr (MODE == 0) {
-    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
-  } else if constexpr (MODE == 3) {
-    // dO . out over this lane's features (its dO terms summed back to the
-    // float32 value: t0 + t1 + t2 is exact in float32), then over the row
+  // MODE 1: the band's blocks (bl.n <= 2) sit in LDS buffers u0, u1
+  __device__ __forceinline__ void mode1(const BandParams& p, const bf16* lds, int u0, int u1) {
+    const bf16* kts[2] = {key_buf<NT>((bf16*)lds, u0), key_buf<NT>((bf16*)lds, u1)};
+    float P[2][4][4], Dp[2][4][4];
+    E dv[2][DTAU ? 16 : 1];
+    if constexpr (DTAU) {
+      dtau_rows_load(p, dbh, dv[0], t0w, bl.first, lane);
+      dtau_rows_load(p, dbh, dv[1], t0w, bl.first + kTile, lane);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) P[s][j][r] = Dp[s][j][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s >= bl.n) break;
+      const int kb0 = bl.first + s * kTile;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
+        f32x4 sc, dp;
+        sdp(kts[s], j, sc, dp);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * j + 4 * g + r;
+          const bool ok = (key >= lo) & (key <= hi);
+          const float pv = tau_of(p, sc[r], key, ok);
+          P[s][j][r] = pv;
+          Dp[s][j][r] = ok ? dp[r] : 0.f;
+          msum += pv;
+          dsum = fmaf(pv, Dp[s][j][r], dsum);
+        }
+      }
+    }
+    coefficients(p);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s >= bl.n) break;
+      const int kb0 = bl.first + s * kTile;
+      if constexpr (DTAU) dtau_rows_put(dst, dv[s], lane);
+      float G[4][4];
+      int kind[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kind[j] = sub_kind(wb, kb0 + 16 * j);
+        float dtv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (DTAU && kind[j] != 0) stage_get4(dst, c, j, g, dtv);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * j + 4 * g + r;
+          const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
+          G[j][r] = g_of(P[s][j][r], Dp[s][j][r], dtv[r], ok);
+        }
+      }
+      dq_product(kts[s], kind, G);
+    }
+  }
+
+  // MODE 2 first pass: the band sums of one block
+  __device__ __forceinline__ void sums_pass(const BandParams& p, const bf16* kt, int kb0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
+      f32x4 sc, dp;
+      sdp(kt, j, sc, dp);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * j + 4 * g + r;
+        const bool ok = (key >= lo) & (key <= hi);
+        const float pv = tau_of(p, sc[r], key, ok);
+        msum += pv;
+        dsum = fmaf(pv, ok ? dp[r] : 0.f, dsum);
+      }
+    }
+  }
+
+  // MODE 3: a, c from the saved output row and tau mass: dO . out over this
+  // lane's features (its dO terms summed back to the float32 value: t0 + t1
+  // + t2 is exact in float32), then over the row
+  __device__ __forceinline__ void saved_coefficients(const BandParams& p) {
     float dot = 0.f;
     if (qok) {
       const E* orow = (const E*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2;
@@ -623,27 +707,69 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
     const float m = qok ? ld<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2) : 1.f;
     ca = 1.f / (m > kMassEps ? m : kMassEps);
     cc = m >= kMassEps ? dot * ca : 0.f;
-    if (p.ws && qok && g == 0) {
-      const int64_t nws = (int64_t)p.B * p.T * p.H;
-      const int64_t wi = ((int64_t)b * p.T + tq) * p.H + h;
-      ((float*)p.ws)[wi] = ca;
-      ((float*)p.ws)[nws + wi] = cc;
-    }
+    put_coefficients(p);
+  }
+
+  __device__ __forceinline__ void store(const BandParams& p, float inv_scale) const {
+    if (!qok) return;
+    store_acc<E, D>((E*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2, acc, inv_scale, g);
+  }
+};
+
+// The lane's query-row fragments (Q, dOut) as loaded, for a load ahead of use.
+template <int NT, int D>
+struct QueryRaw {
+  RawFrag<NT> q[D / 32], o[D / 32];
+};
+
+template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+__device__ __forceinline__ DqTile<NT, D, NORM, BIAS, DTAU> dq_tile_base(const BandParams& p, int b, int h, int lane,
+                                                                        Elem<NT>* dst) {
+  DqTile<NT, D, NORM, BIAS, DTAU> q;
+  q.b = b;
+  q.h = h;
+  q.lane = lane;
+  q.g = lane >> 4;
+  q.c = lane & 15;
+  q.k2 = -kLog2e * (float)(1.0 / p.scale);
+  q.dbh = DTAU ? (const Elem<NT>*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;
+  q.dst = dst;
+  return q;
+}
+
+template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
+__global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
+  constexpr int NBUF = (NT == 1 || MODE == 1) ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const TileId id = tile_id(p, p.glob != 0);
+  const int b = id.b, h = id.h, T = p.T;
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  DqTile<NT, D, NORM, BIAS, DTAU> st =
+      dq_tile_base<NT, D, NORM, BIAS, DTAU>(p, b, h, lane, dstage + (DTAU ? wave * kStageRows : 0));
+  st.at(p, id.tile * kTile, wave);
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    frag_row<NT>(qb_, p.q.s1, st.tq, T, 4 * ch + st.g, st.qf[ch]);
+    frag_row<NT>(ob_, p.dout.s1, st.tq, T, 4 * ch + st.g, st.of[ch]);
+  }
+  const Blocks bl = st.bl;
+  auto g_pass = [&](const bf16* kt, int kb0) { st.g_pass(p, kt, kb0); };
+
+  if constexpr (MODE == 0) {
+    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+  } else if constexpr (MODE == 3) {
+    st.saved_coefficients(p);
     stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
   } else if constexpr (MODE == 1) {
     // both blocks stay resident (buffers 0 and 1)
-    float P[2][4][4], Dp[2][4][4];
-    E dv[2][DTAU ? 16 : 1];
-    if constexpr (DTAU) {
-      dtau_rows_load(p, dbh, dv[0], t0w, bl.first, lane);
-      dtau_rows_load(p, dbh, dv[1], t0w, bl.first + kTile, lane);
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) P[s][j][r] = Dp[s][j][r] = 0.f;
     if (bl.n > 0) {
       store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first, T, tid), key_buf<NT>(lds, 0), tid);
       store_raw<1>(load_raw<1, D>(vb_, p.v.s1, bl.first, T, tid), key_buf<NT>(lds, 0) + NT * kDTile, tid);
@@ -654,74 +780,95 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
                    tid);
     }
     __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (s >= bl.n) break;
-      const int kb0 = bl.first + s * kTile;
-      const bf16* kt = key_buf<NT>(lds, s);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
-        f32x4 sc, dp;
-        sdp(kt, j, sc, dp);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kb0 + 16 * j + 4 * g + r;
-          const bool ok = (key >= lo) & (key <= hi);
-          const float pv = tau_of(sc[r], key, ok);
-          P[s][j][r] = pv;
-          Dp[s][j][r] = ok ? dp[r] : 0.f;
-          msum += pv;
-          dsum = fmaf(pv, Dp[s][j][r], dsum);
-        }
-      }
-    }
-    coefficients();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (s >= bl.n) break;
-      const int kb0 = bl.first + s * kTile;
-      if constexpr (DTAU) {
-        dtau_rows_put(dst, dv[s], lane);
-      }
-      float G[4][4];
-      int kind[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        kind[j] = sub_kind(wb, kb0 + 16 * j);
-        float dtv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (DTAU && kind[j] != 0) stage_get4(dst, c, j, g, dtv);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kb0 + 16 * j + 4 * g + r;
-          const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
-          G[j][r] = g_of(P[s][j][r], Dp[s][j][r], dtv[r], ok);
-        }
-      }
-      dq_product(key_buf<NT>(lds, s), kind, G);
-    }
+    st.mode1(p, lds, 0, 1);
   } else {
-    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, [&](const bf16* kt, int kb0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
-        f32x4 sc, dp;
-        sdp(kt, j, sc, dp);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kb0 + 16 * j + 4 * g + r;
-          const bool ok = (key >= lo) & (key <= hi);
-          const float pv = tau_of(sc[r], key, ok);
-          msum += pv;
-          dsum = fmaf(pv, ok ? dp[r] : 0.f, dsum);
-        }
-      }
-    });
-    coefficients();
+    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid,
+                             [&](const bf16* kt, int kb0) { st.sums_pass(p, kt, kb0); });
+    st.coefficients(p);
     stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
   }
-  if (!qok) return;
-  store_acc<E, D>((E*)p.dq.p + b * p.dq.s0 + (int64_t)tq * p.dq.s1 + h * p.dq.s2, acc, inv_scale, g);
+  st.store(p, (float)(1.0 / p.scale));
+}
+
+// Runs of query tiles for local windows W <= 64 (MODE 0 or 1), where query
+// tile t sees key blocks t - 1 and t only: a workgroup owns query tiles
+// [tA, tB) of one (b, h) (p.chunk runs per (b, h)); key block j sits in LDS
+// buffer j & 1, so tile t + 1 finds block t where tile t left it, and block
+// t + 1 and the next tile's query rows load into registers while tile t
+// computes.
+template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void xb_dq_run(BandParams p) {
+  static_assert(MODE == 0 || MODE == 1, "runs take the one-pass and register tau-mass modes");
+  __shared__ __attribute__((aligned(16))) bf16 lds[2 * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nr = p.chunk;
+  const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+  const int bh = id / nr, run = id % nr;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int tA = (int)((int64_t)run * p.ntiles / nr);
+  const int tB = (int)((int64_t)(run + 1) * p.ntiles / nr);
+  if (tA >= tB) return;
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
+  const float inv_scale = (float)(1.0 / p.scale);
+  DqTile<NT, D, NORM, BIAS, DTAU> st =
+      dq_tile_base<NT, D, NORM, BIAS, DTAU>(p, b, h, lane, dstage + (DTAU ? wave * kStageRows : 0));
+  st.at(p, tA * kTile, wave);
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    frag_row<NT>(qb_, p.q.s1, st.tq, T, 4 * ch + st.g, st.qf[ch]);
+    frag_row<NT>(ob_, p.dout.s1, st.tq, T, 4 * ch + st.g, st.of[ch]);
+  }
+  // blocks tA - 1 (when tA > 0) and tA
+  for (int j = tA > 0 ? tA - 1 : 0; j <= tA; ++j) {
+    bf16* kbuf = key_buf<NT>(lds, j & 1);
+    store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, j * kTile, T, tid), kbuf, tid);
+    store_raw<1>(load_raw<1, D>(vb_, p.v.s1, j * kTile, T, tid), kbuf + NT * kDTile, tid);
+  }
+  __syncthreads();
+  for (int t = tA; t < tB; ++t) {
+    const bool more = t + 1 < tB;
+    Raw<NT> kn;
+    Raw<1> vn;
+    QueryRaw<NT, D> qn;
+    if (more) {
+      kn = load_raw<NT, D>(kb_, p.k.s1, (t + 1) * kTile, T, tid);
+      vn = load_raw<1, D>(vb_, p.v.s1, (t + 1) * kTile, T, tid);
+      const int tq1 = st.tq + kTile;
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) {
+        qn.q[ch] = frag_load<NT>(qb_, p.q.s1, tq1, T, 4 * ch + st.g);
+        qn.o[ch] = frag_load<NT>(ob_, p.dout.s1, tq1, T, 4 * ch + st.g);
+      }
+    }
+    // the band of tile t: blocks bl.first (t - 1, or 0 for t = 0) and on
+    const int j0 = st.bl.first / kTile;
+    if constexpr (MODE == 1) {
+      st.mode1(p, lds, j0 & 1, (j0 + 1) & 1);
+    } else {
+      for (int s = 0; s < st.bl.n; ++s) st.g_pass(p, key_buf<NT>(lds, (j0 + s) & 1), (j0 + s) * kTile);
+    }
+    st.store(p, inv_scale);
+    if (more) {
+      __syncthreads();  // every wave is done with block t - 1's buffer
+      bf16* kbuf = key_buf<NT>(lds, (t + 1) & 1);
+      store_raw<NT>(kn, kbuf, tid);
+      store_raw<1>(vn, kbuf + NT * kDTile, tid);
+      st.at(p, (t + 1) * kTile, wave);
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) {
+        frag_terms<NT>(qn.q[ch], st.qf[ch]);
+        frag_terms<NT>(qn.o[ch], st.of[ch]);
+      }
+      __syncthreads();
+    }
+  }
 }
 
 // ----------------------------------------------------------------- dK / dV
@@ -1037,7 +1184,16 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
     XB_BT(xb_fwd);
   } else if constexpr (PHASE == 1) {
     const bool opt = p.dtau.p != nullptr;
-    if constexpr (NORM != NORM_MASS_) {
+    // runs of tiles (a local window W <= 64): float32 Q / K at head dim 32
+    // without dTau, where they measured faster (B32 H4 T1024 W32 tau-mass
+    // step 82.8 -> 76.5 us); at head dim 64 the run kernel's registers
+    // (246 VGPRs, and spills with dTau) cost what the shared blocks save
+    constexpr bool kRuns = NT == 3 && D == 32;
+    if (kRuns && p.chunk > 0 && !opt) {
+      constexpr int M = NORM == NORM_MASS_ ? 1 : 0;
+      if (bias) hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, true, false, M>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, false, false, M>), grid, block, 0, st, p);
+    } else if constexpr (NORM != NORM_MASS_) {
       XB_BT(xb_dq, , 0);
     } else if constexpr (NT == 3) {
       // a band within two blocks keeps P and dP in registers (faster than
