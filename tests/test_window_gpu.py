@@ -442,6 +442,40 @@ def test_bf16_head_dim_32(dev, T, W, normalize, bias, tau):
     compare(hip, ref, torch.bfloat16, tau)
 
 
+@pytest.mark.parametrize("dtype,D,W,normalize,bias,dtau", [
+    ("f32qk", 32, 17, "mass", False, False),   # dQ and dK / dV runs
+    ("f32qk", 32, 64, "count", True, False),   # runs with a bias
+    ("f32qk", 32, 64, None, False, True),      # dTau: dK / dV runs, dQ per tile
+    ("f32qk", 64, 33, "mass", True, True),     # head dim 64: dK / dV runs
+    ("bf16", 32, 48, "mass", True, True),      # one bf16 term: dK / dV runs
+])
+def test_backward_runs(dev, dtype, D, W, normalize, bias, dtau):
+    """Local windows W <= 64 on shapes with more tiles than workgroups per
+    (b, h): the split backward walks runs of consecutive tiles (dK / dV
+    always, dQ for float32 Q / K at head dim 32 without dTau), with T ragged
+    (the last tile partly past the sequence) so the runs end on a partial
+    tile.  B * H = 128 on 16 tiles per sequence: 4 runs each on a 256-CU
+    device."""
+    from bozo_amd import _lib as L
+    B, H, T = 32, 4, 1000
+    seed = 100 + D + W
+    if dtype == "f32qk":
+        inp = mixed_inputs(B, T, H, seed=seed, W=W, dtau_std=0.1 if dtau else None,
+                           bias_std=0.5 if bias else None, D=D)
+    else:
+        inp = make_inputs(B, T, H, D, seed=seed, std=0.5, dtype=torch.bfloat16, W=W,
+                          dtau_std=0.1 if dtau else None, bias_std=0.5 if bias else None,
+                          bias_shape=(B, T, W) if bias else None)
+    print(f"[runs] {dtype} D={D} W={W} normalize={normalize} bias={bias} dtau={dtau}", flush=True)
+    hip = hip_run(inp, W, math.sqrt(D), dev, normalize=normalize, return_tau=dtau, use_bias=bias, use_dtau=dtau)
+    assert last_kernel() == (L.KERNEL_SPLIT_F32 if dtype == "f32qk" else L.KERNEL_SPLIT_BF16)
+    ref = oracle_run(inp, W, math.sqrt(D), normalize=normalize, use_bias=bias, use_dtau=dtau)
+    if dtype == "f32qk":
+        check_mixed(hip, ref, dtau)
+    else:
+        compare(hip, ref, torch.bfloat16, dtau)
+
+
 def test_empty_batch(dev):
     from bozo_amd import causal_tension
     Q = torch.zeros(0, 16, 2, 64, device=dev, dtype=torch.bfloat16)
