@@ -51,7 +51,10 @@ constexpr int kCacheAux = 2;
 // reference's autocast dtype flow: rotated Q / K promoted to float32); a K
 // row is then 256 bytes, two 16-byte loads per lane, and the dot products
 // are float32 products.  Not with TENSION_DECODE_SELF.
-template <int NW, int NP, bool KF32 = false>
+// SELF: TENSION_DECODE_SELF (a compile-time choice: with the flag read at
+// run time the compiler waited for the position counter, which only the
+// self-key step's descriptor range needs, before issuing any cache load).
+template <int NW, int NP, bool KF32 = false, bool SELF = false>
 __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   constexpr int kRows = 8 * NW;  // cache rows per pass
   constexpr int kKBytes = KF32 ? 4 : 2;   // bytes per K / q / out element
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   // cache, filled from slot 0 and never wrapped), the live rows only: that
   // cache is long and partly empty, and the position read it needs first
   // costs little there.  Window caches keep the loads ahead of that read.
-  const bool self_key = (p.flags & TENSION_DECODE_SELF) != 0;
+  constexpr bool self_key = SELF;
   int rows = W;
   if (self_key) {
     const int pe = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
@@ -308,18 +311,24 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
   } else if (fast) {
     // fast requires D == 64, W <= 1024
     const dim3 grid((unsigned)(p.N * p.H));
-    if (p.W <= 32)
-      hipLaunchKernelGGL((decode_bf16_d64<4, 1>), grid, dim3(256), 0, st, p);
-    else if (p.W <= 64)
-      hipLaunchKernelGGL((decode_bf16_d64<8, 1>), grid, dim3(512), 0, st, p);
-    else if (p.W <= 128)
-      hipLaunchKernelGGL((decode_bf16_d64<8, 2>), grid, dim3(512), 0, st, p);
-    else if (p.W <= 256)  // 4 waves x 8 passes: 2% faster than 8 x 4 at config 4
-      hipLaunchKernelGGL((decode_bf16_d64<4, 8>), grid, dim3(256), 0, st, p);
-    else if (p.W <= 512)
-      hipLaunchKernelGGL((decode_bf16_d64<8, 8>), grid, dim3(512), 0, st, p);
-    else
-      hipLaunchKernelGGL((decode_bf16_d64<8, 16>), grid, dim3(512), 0, st, p);
+#define DECODE_FAST(SELF)                                                                    \
+  do {                                                                                       \
+    if (p.W <= 32)                                                                           \
+      hipLaunchKernelGGL((decode_bf16_d64<4, 1, false, SELF>), grid, dim3(256), 0, st, p);  \
+    else if (p.W <= 64)                                                                      \
+      hipLaunchKernelGGL((decode_bf16_d64<8, 1, false, SELF>), grid, dim3(512), 0, st, p);  \
+    else if (p.W <= 128)                                                                     \
+      hipLaunchKernelGGL((decode_bf16_d64<8, 2, false, SELF>), grid, dim3(512), 0, st, p);  \
+    else if (p.W <= 256) /* 4 waves x 8 passes: 2% faster than 8 x 4 at config 4 */         \
+      hipLaunchKernelGGL((decode_bf16_d64<4, 8, false, SELF>), grid, dim3(256), 0, st, p);  \
+    else if (p.W <= 512)                                                                     \
+      hipLaunchKernelGGL((decode_bf16_d64<8, 8, false, SELF>), grid, dim3(512), 0, st, p);  \
+    else                                                                                     \
+      hipLaunchKernelGGL((decode_bf16_d64<8, 16, false, SELF>), grid, dim3(512), 0, st, p); \
+  } while (0)
+    if (p.flags & TENSION_DECODE_SELF) DECODE_FAST(true);
+    else DECODE_FAST(false);
+#undef DECODE_FAST
   } else {
     const unsigned grid = (unsigned)((p.N * p.H + 63) / 64);
     if (f64)
