@@ -54,8 +54,29 @@ constexpr int kCacheAux = 2;
 // SELF: TENSION_DECODE_SELF (a compile-time choice: with the flag read at
 // run time the compiler waited for the position counter, which only the
 // self-key step's descriptor range needs, before issuing any cache load).
+// Arguments of the fast kernel: row pointers and 32-bit element strides, 43
+// dwords against the 96 of DecodeParams, so the kernel argument reads that
+// precede the cache loads take fewer dependent rounds of scalar loads.  The
+// host takes the fast path only when every stride fits in 32 bits.
+struct DecodeFastArgs {
+  const void* q;
+  const void* kn;
+  const void* vn;
+  void* kc;
+  void* vc;
+  void* out;
+  void* tau;
+  const int32_t* pos_in;
+  int32_t* pos_out;
+  int q_n, q_h, kn_n, kn_h, vn_n, vn_h;
+  int kc_n, kc_h, kc_w, vc_n, vc_h, vc_w;
+  int out_n, out_h, tau_n, tau_h, tau_dt;
+  int H, W, flags;
+  float inv_scale;
+};
+
 template <int NW, int NP, bool KF32 = false, bool SELF = false>
-__global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
+__global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
   constexpr int kRows = 8 * NW;  // cache rows per pass
   constexpr int kKBytes = KF32 ? 4 : 2;   // bytes per K / q / out element
   constexpr int kKChunks = KF32 ? 16 : 8;  // 16-byte chunks of a K row
@@ -68,11 +89,11 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   // this lane's 8 query features (8 ch .. +7)
   u16x8 qbits, qbits2;
   if constexpr (KF32) {
-    const float* qrow = (const float*)p.q.p + n * p.q.s0 + h * p.q.s1 + 8 * ch;
+    const float* qrow = (const float*)p.q + (int64_t)n * p.q_n + (int64_t)h * p.q_h + 8 * ch;
     qbits = *(const u16x8*)qrow;
     qbits2 = *(const u16x8*)(qrow + 4);
   } else {
-    const bf16* qrow = (const bf16*)p.q.p + n * p.q.s0 + h * p.q.s1;
+    const bf16* qrow = (const bf16*)p.q + (int64_t)n * p.q_n + (int64_t)h * p.q_h;
     qbits = *(const u16x8*)(qrow + 8 * ch);
   }
   // The new token's K / V rows are appended after the reduction, but fetched
@@ -83,10 +104,10 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
   // loads need no branch.
   const int ai = tid - 64;
   const __amdgpu_buffer_rsrc_t knr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const char*)p.kn.p + (n * p.kn.s0 + h * p.kn.s1) * kKBytes), (short)0, 16 * kKChunks,
+      (void*)((const char*)p.kn + ((int64_t)n * p.kn_n + (int64_t)h * p.kn_h) * kKBytes), (short)0, 16 * kKChunks,
       kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vnr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const bf16*)p.vn.p + n * p.vn.s0 + h * p.vn.s1), (short)0, 128, kRawBufWord3);
+      (void*)((const bf16*)p.vn + (int64_t)n * p.vn_n + (int64_t)h * p.vn_h), (short)0, 128, kRawBufWord3);
   const u16x8 knew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
       knr, (ai >= 0 && ai < kKChunks) ? 16 * ai : 16 * kKChunks, 0, 0));
   const u16x8 vnew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
@@ -103,16 +124,16 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
     const int pe = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
     rows = pe < W ? pe : W;
   }
-  const char* kbase = (const char*)p.kc.p + (n * p.kc.s0 + h * p.kc.s1) * kKBytes;
-  const bf16* vbase = (const bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1;
+  const char* kbase = (const char*)p.kc + ((int64_t)n * p.kc_n + (int64_t)h * p.kc_h) * kKBytes;
+  const bf16* vbase = (const bf16*)p.vc + (int64_t)n * p.vc_n + (int64_t)h * p.vc_h;
   const __amdgpu_buffer_rsrc_t kr_ = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)kbase, (short)0, (int)((int64_t)rows * p.kc.s2 * kKBytes), kRawBufWord3);
+      (void*)kbase, (short)0, (int)((int64_t)rows * p.kc_w * kKBytes), kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vr_ = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)vbase, (short)0, (int)((int64_t)rows * p.vc.s2 * 2), kRawBufWord3);
+      (void*)vbase, (short)0, (int)((int64_t)rows * p.vc_w * 2), kRawBufWord3);
   const uint32_t row0 = (uint32_t)(wave * 8 + rw);
-  const uint32_t kstep = (uint32_t)(kRows * p.kc.s2 * kKBytes), vstep = (uint32_t)(kRows * p.vc.s2 * 2);
-  const uint32_t koff = row0 * (uint32_t)(p.kc.s2 * kKBytes) + 8 * kKBytes * ch;
-  const uint32_t voff = row0 * (uint32_t)(p.vc.s2 * 2) + 16 * ch;
+  const uint32_t kstep = (uint32_t)(kRows * p.kc_w * kKBytes), vstep = (uint32_t)(kRows * p.vc_w * 2);
+  const uint32_t koff = row0 * (uint32_t)(p.kc_w * kKBytes) + 8 * kKBytes * ch;
+  const uint32_t voff = row0 * (uint32_t)(p.vc_w * 2) + 16 * ch;
   u16x8 kr[NP], kr2[KF32 ? NP : 1], vr[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
@@ -159,8 +180,15 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
     }
     part = row_sum8(part);
     const float tau = slot < live ? sigmoid_fast(part) : 0.f;
-    if (p.tau.p && ch == 0 && slot < W)
-      st<float>(p.tau, n * p.tau.s0 + h * p.tau.s1 + ring_w(slot, pos, W), tau);
+    if (p.tau && ch == 0 && slot < W) {
+      const int64_t to = (int64_t)n * p.tau_n + (int64_t)h * p.tau_h + ring_w(slot, pos, W);
+      switch (p.tau_dt) {
+        case TENSION_F32: ((float*)p.tau)[to] = tau; break;
+        case TENSION_BF16: ((bf16*)p.tau)[to] = (bf16)tau; break;
+        case TENSION_F16: ((f16*)p.tau)[to] = (f16)tau; break;
+        default: ((double*)p.tau)[to] = (double)tau; break;
+      }
+    }
     msum += tau;
     const bf16x8 vv = __builtin_bit_cast(bf16x8, vr[i]);
 #pragma unroll
@@ -214,19 +242,19 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeParams p) {
     }
     const float inv = decode_norm(p.flags, m, live + (self_key ? 1 : 0));
     if constexpr (KF32) {
-      ((float*)p.out.p)[n * p.out.s0 + h * p.out.s1 + tid] = o * inv;
+      ((float*)p.out)[(int64_t)n * p.out_n + (int64_t)h * p.out_h + tid] = o * inv;
     } else {
-      bf16* orow = (bf16*)p.out.p + n * p.out.s0 + h * p.out.s1;
+      bf16* orow = (bf16*)p.out + (int64_t)n * p.out_n + (int64_t)h * p.out_h;
       orow[tid] = (bf16)(o * inv);
     }
   } else if (ai < kKChunks + 8) {
     // append k_new / v_new at slot pos % W (16 bytes per lane)
     const int slot = pos % W;
     if (ai < kKChunks) {
-      char* dst = (char*)p.kc.p + (n * p.kc.s0 + h * p.kc.s1 + (int64_t)slot * p.kc.s2) * kKBytes;
+      char* dst = (char*)p.kc + ((int64_t)n * p.kc_n + (int64_t)h * p.kc_h + (int64_t)slot * p.kc_w) * kKBytes;
       *(u16x8*)(dst + 16 * ai) = knew;
     } else {
-      bf16* dst = (bf16*)p.vc.p + n * p.vc.s0 + h * p.vc.s1 + (int64_t)slot * p.vc.s2;
+      bf16* dst = (bf16*)p.vc + (int64_t)n * p.vc_n + (int64_t)h * p.vc_h + (int64_t)slot * p.vc_w;
       *(u16x8*)(dst + 8 * (ai - kKChunks)) = vnew;
     }
   } else if (ai == kKChunks + 8 && h == 0 && p.pos_out) {
@@ -292,10 +320,38 @@ __global__ __launch_bounds__(64) void decode_exact(DecodeParams p) {
   if (h == 0 && p.pos_out) p.pos_out[n] = pos + 1;
 }
 
-int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32) {
+namespace {
+
+bool fits32(int64_t s) { return s >= 0 && s <= 0x7fffffff; }
+
+// The fast kernel's arguments, or false when a stride needs 64 bits.
+bool fast_args(const DecodeParams& p, DecodeFastArgs* a) {
+  const int64_t st[] = {p.q.s0, p.q.s1, p.kn.s0, p.kn.s1, p.vn.s0, p.vn.s1, p.kc.s0, p.kc.s1, p.kc.s2,
+                        p.vc.s0, p.vc.s1, p.vc.s2, p.out.s0, p.out.s1, p.tau.s0, p.tau.s1};
+  for (int64_t x : st)
+    if (!fits32(x)) return false;
+  a->q = p.q.p; a->kn = p.kn.p; a->vn = p.vn.p;
+  a->kc = (void*)p.kc.p; a->vc = (void*)p.vc.p; a->out = (void*)p.out.p; a->tau = (void*)p.tau.p;
+  a->pos_in = p.pos_in; a->pos_out = p.pos_out;
+  a->q_n = (int)p.q.s0; a->q_h = (int)p.q.s1; a->kn_n = (int)p.kn.s0; a->kn_h = (int)p.kn.s1;
+  a->vn_n = (int)p.vn.s0; a->vn_h = (int)p.vn.s1;
+  a->kc_n = (int)p.kc.s0; a->kc_h = (int)p.kc.s1; a->kc_w = (int)p.kc.s2;
+  a->vc_n = (int)p.vc.s0; a->vc_h = (int)p.vc.s1; a->vc_w = (int)p.vc.s2;
+  a->out_n = (int)p.out.s0; a->out_h = (int)p.out.s1;
+  a->tau_n = (int)p.tau.s0; a->tau_h = (int)p.tau.s1; a->tau_dt = p.tau.dt;
+  a->H = p.H; a->W = p.W; a->flags = p.flags; a->inv_scale = p.inv_scale;
+  return true;
+}
+
+}  // namespace
+
+int launch_decode(bool fast, bool f64, const DecodeParams& p_in, hipStream_t st, hipError_t* err, bool kf32) {
+  DecodeFastArgs p;
+  if (fast && !fast_args(p_in, &p)) fast = false;
+  if (!fast) kf32 = false;
   if (fast && kf32) {
     // float32 q / K / out, bf16 V (D == 64, W <= 1024, no self key)
-    const dim3 grid((unsigned)(p.N * p.H));
+    const dim3 grid((unsigned)(p_in.N * p_in.H));
     if (p.W <= 32)
       hipLaunchKernelGGL((decode_bf16_d64<4, 1, true>), grid, dim3(256), 0, st, p);
     else if (p.W <= 64)
@@ -310,7 +366,7 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
       hipLaunchKernelGGL((decode_bf16_d64<8, 16, true>), grid, dim3(512), 0, st, p);
   } else if (fast) {
     // fast requires D == 64, W <= 1024
-    const dim3 grid((unsigned)(p.N * p.H));
+    const dim3 grid((unsigned)(p_in.N * p_in.H));
 #define DECODE_FAST(SELF)                                                                    \
   do {                                                                                       \
     if (p.W <= 32)                                                                           \
@@ -330,11 +386,11 @@ int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hi
     else DECODE_FAST(false);
 #undef DECODE_FAST
   } else {
-    const unsigned grid = (unsigned)((p.N * p.H + 63) / 64);
+    const unsigned grid = (unsigned)((p_in.N * p_in.H + 63) / 64);
     if (f64)
-      hipLaunchKernelGGL(decode_exact<double>, dim3(grid), dim3(64), 0, st, p);
+      hipLaunchKernelGGL(decode_exact<double>, dim3(grid), dim3(64), 0, st, p_in);
     else
-      hipLaunchKernelGGL(decode_exact<float>, dim3(grid), dim3(64), 0, st, p);
+      hipLaunchKernelGGL(decode_exact<float>, dim3(grid), dim3(64), 0, st, p_in);
   }
   *err = hipGetLastError();
   return 0;
