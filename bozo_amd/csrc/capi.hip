@@ -178,6 +178,10 @@ thread_local int g_last_kernel = -1;
 
 int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_t stream, const char* what) {
   hipError_t e = hipSuccess;
+  // the MFMA and split kernels take 32-bit strides (BandArgs); a tensor with
+  // a larger one runs on the exact kernels
+  BandArgs probe;
+  if (kind != KERNEL_EXACT && phase != 3 && !band_args(p, &probe)) kind = KERNEL_EXACT;
   int r = kind == KERNEL_SPLIT_F32    ? launch_split(phase, true, p, hs(stream), &e)
           : kind == KERNEL_SPLIT_BF16 ? launch_split(phase, false, p, hs(stream), &e)
           : kind == KERNEL_MFMA       ? launch_mfma(phase, p, hs(stream), &e)
@@ -449,7 +453,8 @@ int window_bwd(const tension_buf* q, const tension_buf* k, const tension_buf* v,
       p.dq = make_buf(dq);
       p.dk = make_buf(dk);
       p.dv = make_buf(dv);
-      return run_band(3, KERNEL_MFMA, false, p, stream, "tension_window_bwd");
+      BandArgs probe;  // 32-bit strides, else the split pair below
+      if (band_args(p, &probe)) return run_band(3, KERNEL_MFMA, false, p, stream, "tension_window_bwd");
     }
   }
   TRY(band_bwd_dq(q, k, v, dout, dtau, bias, dq, ws, sh, W, scale, flags, stream, false, out, mass));

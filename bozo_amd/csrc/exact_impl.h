@@ -14,6 +14,7 @@ namespace tension {
 
 template <typename A, int D>
 __global__ __launch_bounds__(128) void exact_fwd(BandParams p) {
+  touch_args(p);
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)p.B * p.H * p.T;
   if (idx >= total) return;
@@ -87,6 +88,7 @@ __global__ __launch_bounds__(128) void exact_fwd(BandParams p) {
 // dO.v_s - dO.out cancels when a query has one dominant key.
 template <typename A, int D>
 __global__ __launch_bounds__(128) void exact_bwd_dq(BandParams p) {
+  touch_args(p);
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)p.B * p.H * p.T;
   if (idx >= total) return;
@@ -187,6 +189,7 @@ __global__ __launch_bounds__(128) void exact_bwd_dq(BandParams p) {
 
 template <typename A, int D>
 __global__ __launch_bounds__(128) void exact_bwd_dkv(BandParams p) {
+  touch_args(p);
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)p.B * p.H * p.T;
   if (idx >= total) return;

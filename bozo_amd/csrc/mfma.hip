@@ -33,6 +33,8 @@ int device_cus() {
 }
 
 int launch_mfma(int phase, const BandParams& p_in, hipStream_t st, hipError_t* err) {
+  BandArgs probe;
+  if (!band_args(p_in, &probe)) return -1;  // the kernels take 32-bit strides
   BandParams p = p_in;
   p.ntiles = (p.T + kTile - 1) / kTile;
   const int64_t nwg = (int64_t)p.B * p.H * p.ntiles;

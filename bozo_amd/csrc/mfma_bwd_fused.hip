@@ -78,8 +78,10 @@ namespace tension {
 // rows wait in each wave's G exchange sub-tiles until phase 1 reads them.
 template <int NORM, bool BIAS, bool DTAU, bool FAST>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_BWD_WAVES_PER_EU, TENSION_BWD_WAVES_PER_EU)))
-void mfma_bwd_fused(BandParams p) {
+void mfma_bwd_fused(BandArgs args) {
   static_assert(!FAST || !BIAS, "the fast path has no bias");
+  touch_args(args);
+  const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 Kt[2][kDTile];  // key block k in slot k & 1
   __shared__ __attribute__((aligned(16))) bf16 Vt[2][kDTile];
   __shared__ __attribute__((aligned(16))) bf16 Qt[kDTile];     // query tile of the step
@@ -623,7 +625,9 @@ void mfma_bwd_fused(BandParams p) {
 
 template <int NORM, bool BIAS, bool DTAU, bool FAST>
 static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
-  hipLaunchKernelGGL((mfma_bwd_fused<NORM, BIAS, DTAU, FAST>), dim3(nwg), dim3(kThreads), 0, st, p);
+  BandArgs a;
+  if (!band_args(p, &a)) return;  // the host takes this kernel only with 32-bit strides
+  hipLaunchKernelGGL((mfma_bwd_fused<NORM, BIAS, DTAU, FAST>), dim3(nwg), dim3(kThreads), 0, st, a);
 }
 
 template <int NORM>

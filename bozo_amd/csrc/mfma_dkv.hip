@@ -15,7 +15,9 @@
 namespace tension {
 
 template <int NORM, bool BIAS, bool DTAU>
-__global__ __launch_bounds__(kThreads) void mfma_bwd_dkv(BandParams p) {
+__global__ __launch_bounds__(kThreads) void mfma_bwd_dkv(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 Qs[kTileElems];
   __shared__ __attribute__((aligned(16))) bf16 Gs[kTileElems];
   __shared__ __attribute__((aligned(16))) bf16 Qt[kTElems];
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_dkv(BandParams p) {
 
 template <int NORM, bool BIAS, bool DTAU>
 static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
-  hipLaunchKernelGGL((mfma_bwd_dkv<NORM, BIAS, DTAU>), dim3(nwg), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((mfma_bwd_dkv<NORM, BIAS, DTAU>), dim3(nwg), dim3(kThreads), 0, st, to_args(p));
 }
 
 template <int NORM>

@@ -24,7 +24,9 @@ namespace tension {
 // (0 when m_t < eps, as in the band pass).  Eight lanes per (b, t, h) row, 16
 // bytes of out and dO each; the grid covers whole 8-lane groups, so a group
 // is either fully inside [0, B*T*H) or fully outside.
-__global__ __launch_bounds__(256) void coef_from_out(BandParams p) {
+__global__ __launch_bounds__(256) void coef_from_out(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   const int64_t n = (int64_t)p.B * p.T * p.H;
   const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;  // (b*T + t)*H + h
   const int ch = threadIdx.x & 7;
@@ -61,7 +63,9 @@ __device__ __forceinline__ void scores_block(const bf16* Ks, const bf16* Vs, con
 }
 
 template <int NORM, bool BIAS, bool DTAU, bool HOLD>
-__global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandParams p) {
+__global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   constexpr int NKT = HOLD ? 2 : 1;
   __shared__ __attribute__((aligned(16))) bf16 Ks[kTileElems];
   __shared__ __attribute__((aligned(16))) bf16 Vs[kTileElems];
@@ -255,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_dq(BandParams p) {
 
 template <int NORM, bool BIAS, bool DTAU, bool HOLD>
 static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
-  hipLaunchKernelGGL((mfma_bwd_dq<NORM, BIAS, DTAU, HOLD>), dim3(nwg), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((mfma_bwd_dq<NORM, BIAS, DTAU, HOLD>), dim3(nwg), dim3(kThreads), 0, st, to_args(p));
 }
 
 template <int NORM, bool HOLD>
@@ -286,7 +290,7 @@ void launch_mfma_dq(const BandParams& p, hipStream_t st, unsigned nwg, int norm)
     }
 #endif
     const int64_t threads = (int64_t)p.B * p.T * p.H * 8;
-    hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(coef_from_out, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, to_args(p));
   }
   switch (norm) {
     case NORM_MASS_: go_n<NORM_MASS_>(p, st, nwg, bias, dtau, hold); break;

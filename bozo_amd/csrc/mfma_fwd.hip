@@ -253,7 +253,9 @@ __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, co
 }
 
 template <int NORM, bool BIAS, bool TAU, bool FAST>
-__global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
+__global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   // the six ring tiles form one LDS object (separate objects make the
   // compiler wait for every copy in flight before each ring read); the
   // slots are still chosen at compile time
@@ -432,7 +434,9 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandParams p) {
 // ------------------------------------------------------------------ streaming kernel
 
 template <int NORM, bool BIAS, bool TAU>
-__global__ __launch_bounds__(kThreads) void mfma_fwd(BandParams p) {
+__global__ __launch_bounds__(kThreads) void mfma_fwd(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 Kb[2][kDTile];
   __shared__ __attribute__((aligned(16))) bf16 Vb[2][kDTile];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -497,17 +501,21 @@ static void go(const BandParams& p, hipStream_t st, unsigned nwg, bool ring) {
     const Buf& tb = p.tau;
     const bool tau_rows = !TAU || (tb.dt == TENSION_BF16 && ((tb.s0 | tb.s1 | tb.s2) & 7) == 0 &&
                                    ((uintptr_t)tb.p & 15) == 0);
+    BandArgs a;
+    if (!band_args(p, &a)) return;  // the host takes the ring kernel only with 32-bit strides
     if (!BIAS && tau_rows && p.win == kTile && p.T % kTile == 0) {
-      BandParams q = p;
-      if (q.chunk > 2) q.chunk = 2;
-      const unsigned nq = (unsigned)((int64_t)q.B * q.H * ((q.ntiles + q.chunk - 1) / q.chunk));
-      hipLaunchKernelGGL((mfma_fwd_ring<NORM, false, TAU, true>), dim3(nq), dim3(kThreads), 0, st, q);
+      if (a.chunk > 2) a.chunk = 2;
+      const unsigned nq = (unsigned)((int64_t)a.B * a.H * ((a.ntiles + a.chunk - 1) / a.chunk));
+      hipLaunchKernelGGL((mfma_fwd_ring<NORM, false, TAU, true>), dim3(nq), dim3(kThreads), 0, st, a);
       return;
     }
+#else
+    BandArgs a;
+    if (!band_args(p, &a)) return;
 #endif
-    hipLaunchKernelGGL((mfma_fwd_ring<NORM, BIAS, TAU, false>), dim3(n), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((mfma_fwd_ring<NORM, BIAS, TAU, false>), dim3(n), dim3(kThreads), 0, st, a);
   } else {
-    hipLaunchKernelGGL((mfma_fwd<NORM, BIAS, TAU>), dim3(nwg), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((mfma_fwd<NORM, BIAS, TAU>), dim3(nwg), dim3(kThreads), 0, st, to_args(p));
   }
 }
 

@@ -277,7 +277,9 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
 template <bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(BIAS || TAU ? TENSION_GL_FWD_WPE_OPT : TENSION_GL_FWD_WPE, 8)))
-void gl_fwd(BandParams p) {
+void gl_fwd(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
   const int BH = p.B * p.H;
   const int id = (int)blockIdx.x;
@@ -308,7 +310,9 @@ void gl_fwd(BandParams p) {
 //   dQ^T += K^T G^T                  (A = K^T read transposed)
 template <bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DQ_WPE, 8)))
-void gl_dq(BandParams p) {
+void gl_dq(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
   bf16(*Kb)[kDTile] = lds;
   bf16(*Vb)[kDTile] = lds + 2;
@@ -490,7 +494,9 @@ void gl_dq(BandParams p) {
 // Query rows past T get a = c = 0, which zeroes their P and G.
 template <bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_GL_DKV_WPE, 8)))
-void gl_dkv(BandParams p) {
+void gl_dkv(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   // one LDS object: the Q / dO ring (4 tiles) and, behind it, the
   // coefficient ring coef[slot][a, c][query] (with a second object the
   // compiler waits for every copy in flight before each ring read)
@@ -725,16 +731,17 @@ void gl_dkv(BandParams p) {
 
 // the optional operands are template switches (BIAS: p.bias, TAU / DTAU:
 // p.tau / p.dtau)
-#define GL_LAUNCH(kernel, x, y)                                                        \
-  do {                                                                                 \
-    const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);                      \
-    if (x) {                                                                           \
-      if (y) hipLaunchKernelGGL((kernel<true, true>), dim3(n), dim3(kThreads), 0, st, p);   \
-      else hipLaunchKernelGGL((kernel<true, false>), dim3(n), dim3(kThreads), 0, st, p);    \
-    } else {                                                                           \
-      if (y) hipLaunchKernelGGL((kernel<false, true>), dim3(n), dim3(kThreads), 0, st, p);  \
-      else hipLaunchKernelGGL((kernel<false, false>), dim3(n), dim3(kThreads), 0, st, p);   \
-    }                                                                                  \
+#define GL_LAUNCH(kernel, x, y)                                                            \
+  do {                                                                                     \
+    const unsigned n = (unsigned)((int64_t)p.B * p.H * p.ntiles);                          \
+    const BandArgs a = to_args(p);                                                         \
+    if (x) {                                                                               \
+      if (y) hipLaunchKernelGGL((kernel<true, true>), dim3(n), dim3(kThreads), 0, st, a);   \
+      else hipLaunchKernelGGL((kernel<true, false>), dim3(n), dim3(kThreads), 0, st, a);    \
+    } else {                                                                               \
+      if (y) hipLaunchKernelGGL((kernel<false, true>), dim3(n), dim3(kThreads), 0, st, a);  \
+      else hipLaunchKernelGGL((kernel<false, false>), dim3(n), dim3(kThreads), 0, st, a);   \
+    }                                                                                      \
   } while (0)
 
 void launch_gl_dq(const BandParams& p, hipStream_t st) { GL_LAUNCH(gl_dq, p.bias.p, p.dtau.p); }

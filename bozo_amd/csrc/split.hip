@@ -12,6 +12,8 @@ void launch_split_dq_f32(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_dkv_f32(const BandParams& p, hipStream_t st, unsigned n);
 
 int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hipError_t* err) {
+  BandArgs probe;
+  if (!band_args(p_in, &probe)) return -1;  // the kernels take 32-bit strides
   BandParams p = p_in;
   if (p.D != 32 && p.D != 64) return -1;
   p.ntiles = (p.T + 63) / 64;

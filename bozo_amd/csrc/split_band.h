@@ -360,7 +360,9 @@ __device__ __forceinline__ void dtau_rows_put(E* st, const E* v, int lane) {
 // ----------------------------------------------------------------- forward
 
 template <int NT, int D, int NORM, bool BIAS, bool TAU>
-__global__ __launch_bounds__(kThreads) void xb_fwd(BandParams p) {
+__global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   constexpr int NBUF = NT == 1 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
@@ -738,7 +740,9 @@ __device__ __forceinline__ DqTile<NT, D, NORM, BIAS, DTAU> dq_tile_base(const Ba
 }
 
 template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
-__global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
+__global__ __launch_bounds__(kThreads) void xb_dq(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   constexpr int NBUF = (NT == 1 || MODE == 1) ? 2 : 1;
   __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
@@ -797,7 +801,9 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandParams p) {
 // t + 1 and the next tile's query rows load into registers while tile t
 // computes.
 template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void xb_dq_run(BandParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void xb_dq_run(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   static_assert(MODE == 0 || MODE == 1, "runs take the one-pass and register tau-mass modes");
   __shared__ __attribute__((aligned(16))) bf16 lds[2 * (NT + 1) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
@@ -1042,7 +1048,9 @@ __device__ __forceinline__ void dkv_store(const BandParams& p, const KeyTile<NT,
 // Key tile k: the query tiles whose band reaches it pass through LDS in
 // turn (Q and dOut as NT terms each, plus their rows' coefficients a, c).
 template <int NT, int D, int NORM, bool BIAS, bool DTAU>
-__global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
+__global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   constexpr int NBUF = NT == 1 ? 2 : 1;
   constexpr int TPB = 2 * NT;  // tiles per buffer: Q terms, then dOut terms
   __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * TPB * kDTile];
@@ -1104,7 +1112,9 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandParams p) {
 // loading into registers during a key tile's first visit and the next key
 // rows during its second.
 template <int NT, int D, int NORM, bool BIAS, bool DTAU>
-__global__ __launch_bounds__(kThreads) void xb_dkv_run(BandParams p) {
+__global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
   constexpr int TPB = 2 * NT;
   __shared__ __attribute__((aligned(16))) bf16 lds[TPB * kDTile];
   __shared__ float sa[kTile], scf[kTile];
@@ -1169,15 +1179,16 @@ template <int NT, int D, int NORM, int PHASE>
 void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
   const bool bias = p.bias.p != nullptr;
   const dim3 grid(n), block(kThreads);
-#define XB_BT(K, ...)                                                                                \
-  do {                                                                                               \
-    if (bias) {                                                                                      \
-      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, true, true __VA_ARGS__>), grid, block, 0, st, p);  \
-      else hipLaunchKernelGGL((K<NT, D, NORM, true, false __VA_ARGS__>), grid, block, 0, st, p);     \
-    } else {                                                                                         \
-      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, false, true __VA_ARGS__>), grid, block, 0, st, p); \
-      else hipLaunchKernelGGL((K<NT, D, NORM, false, false __VA_ARGS__>), grid, block, 0, st, p);    \
-    }                                                                                                \
+  const BandArgs a = to_args(p);
+#define XB_BT(K, ...)                                                                           \
+  do {                                                                                          \
+    if (bias) {                                                                                 \
+      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, true, true __VA_ARGS__>), grid, block, 0, st, a);  \
+      else hipLaunchKernelGGL((K<NT, D, NORM, true, false __VA_ARGS__>), grid, block, 0, st, a);     \
+    } else {                                                                                    \
+      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, false, true __VA_ARGS__>), grid, block, 0, st, a); \
+      else hipLaunchKernelGGL((K<NT, D, NORM, false, false __VA_ARGS__>), grid, block, 0, st, a);    \
+    }                                                                                           \
   } while (0)
   if constexpr (PHASE == 0) {
     const bool opt = p.tau.p != nullptr;
@@ -1191,8 +1202,8 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
     constexpr bool kRuns = NT == 3 && D == 32;
     if (kRuns && p.chunk > 0 && !opt) {
       constexpr int M = NORM == NORM_MASS_ ? 1 : 0;
-      if (bias) hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, true, false, M>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, false, false, M>), grid, block, 0, st, p);
+      if (bias) hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, true, false, M>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, false, false, M>), grid, block, 0, st, a);
     } else if constexpr (NORM != NORM_MASS_) {
       XB_BT(xb_dq, , 0);
     } else if constexpr (NT == 3) {
