@@ -476,6 +476,35 @@ def test_backward_runs(dev, dtype, D, W, normalize, bias, dtau):
         compare(hip, ref, torch.bfloat16, dtau)
 
 
+def test_strides_beyond_int32_take_exact_kernels(dev):
+    """A batch stride above 2^31 elements: the MFMA and split kernels take
+    32-bit strides, so the call runs on the exact kernels (strides read in
+    place, 64-bit offsets), and matches the oracle.  Q, K, V are views with
+    gaps into one 4.3 GB buffer."""
+    from bozo_amd import _lib as L
+    B, T, H, D, W = 2, 128, 2, 64, 16
+    S = (1 << 31) + 64  # batch stride in elements
+    n = T * H * D
+    buf = torch.zeros(S + 3 * n, dtype=torch.bfloat16, device=dev)
+    ref_in = make_inputs(B, T, H, D, seed=77, std=0.5, dtype=torch.bfloat16, W=W)
+    views = {}
+    for i, name in enumerate("QKV"):
+        v = buf.as_strided((B, T, H, D), (S, H * D, D, 1), i * n)
+        v.copy_(ref_in[name].to(dev))
+        views[name] = v
+    from bozo_amd import causal_tension
+    Q, K, V = (views[c].detach().requires_grad_(True) for c in "QKV")
+    assert Q.stride(0) == S
+    out = causal_tension(Q, K, V, W, 8.0, normalize="mass")
+    assert last_kernel() == L.KERNEL_EXACT
+    (out.float() * ref_in["dO"].to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    assert last_kernel() == L.KERNEL_EXACT
+    ref = oracle_run(ref_in, W, 8.0, normalize="mass")
+    compare((out, None, (Q.grad, K.grad, V.grad)), ref, torch.bfloat16, False)
+    del buf, views, Q, K, V, out
+
+
 def test_empty_batch(dev):
     from bozo_amd import causal_tension
     Q = torch.zeros(0, 16, 2, 64, device=dev, dtype=torch.bfloat16)
