@@ -1107,10 +1107,13 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
 // Runs of key tiles for local windows W <= 64, where key tile k is seen by
 // query tiles k and k + 1 only: a workgroup owns key tiles [kA, kB) of one
 // (b, h) (p.chunk runs per (b, h)) and walks query tiles kA .. kB once --
-// query tile k + 1 serves the second visit of key tile k and the first of
-// key tile k + 1 from the same LDS buffer -- with the next query tile
-// loading into registers during a key tile's first visit and the next key
-// rows during its second.
+// consecutive key tiles share a query tile, which stays in the LDS buffer
+// from the last visit of one to the first visit of the next -- with the
+// next query tile loading into registers during a key tile's first visit
+// and the next key rows during its second.  Odd runs walk down (key tile k
+// visits query tile k + 1, then k): two runs that share a boundary query
+// tile then read it at the same time (both at their ends or both at their
+// starts), and the second read is an L2 hit.
 template <int NT, int D, int NORM, bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   touch_args(args);
@@ -1127,6 +1130,7 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   const int b = bh / p.H, h = bh % p.H, T = p.T;
   const int kA = (int)((int64_t)run * p.ntiles / nr);
   const int kB = (int)((int64_t)(run + 1) * p.ntiles / nr);
+  const bool desc = (run & 1) != 0;
 
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
@@ -1137,37 +1141,45 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   const float k2 = -kLog2e * inv_scale;
   const E* const dtb = DTAU ? (const E*)p.dtau.p + b * p.dtau.s0 + h * p.dtau.s2 : nullptr;
   const float* const bb = BIAS ? (const float*)p.bias.p + b * p.bias.s0 : nullptr;
-  if (kA >= kB) return;
+  const int n = kB - kA;
+  if (n <= 0) return;
 
+  const int kfirst = desc ? kB - 1 : kA;
   KeyTile<NT, D> kt;
-  key_tile_init<NT, D>(p, kA * kTile, wave, c, kt);
+  key_tile_init<NT, D>(p, kfirst * kTile, wave, c, kt);
   key_raw_terms<NT, D>(key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
-  dkv_stage<NT, D, NORM>(p, lds, sa, scf, kA * kTile, load_raw<NT, D>(qb_, p.q.s1, kA * kTile, T, tid),
-                         load_raw<NT, D>(ob_, p.dout.s1, kA * kTile, T, tid), b, h, tid);
+  {
+    // a key tile's first visit: query tile k (up), k + 1 when it sees the
+    // tile (down); the trip before left that tile in LDS
+    const int q0 = (desc && kt.nqt > 1 ? kfirst + 1 : kfirst) * kTile;
+    dkv_stage<NT, D, NORM>(p, lds, sa, scf, q0, load_raw<NT, D>(qb_, p.q.s1, q0, T, tid),
+                           load_raw<NT, D>(ob_, p.dout.s1, q0, T, tid), b, h, tid);
+  }
   __syncthreads();
-  // LDS holds query tile k at the top of each trip: tile k + 1 sees every
-  // key tile k < ntiles - 1 (W >= 1), so the trip before staged it
-  for (int k = kA; k < kB; ++k) {
-    const int k0 = k * kTile;
+  for (int i = 0; i < n; ++i) {
+    const int k = desc ? kB - 1 - i : kA + i;
     const bool two = kt.nqt > 1;  // query tile k + 1 sees this key tile
+    const int q1 = (desc && two ? k + 1 : k) * kTile;  // in LDS
+    const int q2 = (desc ? k : k + 1) * kTile;         // the second visit, when two
     Raw<NT> qn, on;
     if (two) {
-      qn = load_raw<NT, D>(qb_, p.q.s1, k0 + kTile, T, tid);
-      on = load_raw<NT, D>(ob_, p.dout.s1, k0 + kTile, T, tid);
+      qn = load_raw<NT, D>(qb_, p.q.s1, q2, T, tid);
+      on = load_raw<NT, D>(ob_, p.dout.s1, q2, T, tid);
     }
-    dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, k0, kt, dtb, bb, k2, g, c);
+    dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, q1, kt, dtb, bb, k2, g, c);
     if (two) {
-      __syncthreads();  // every wave is done with query tile k
-      dkv_stage<NT, D, NORM>(p, lds, sa, scf, k0 + kTile, qn, on, b, h, tid);
+      __syncthreads();  // every wave is done with the first visit's tile
+      dkv_stage<NT, D, NORM>(p, lds, sa, scf, q2, qn, on, b, h, tid);
       __syncthreads();
     }
-    const bool next = k + 1 < kB;
+    const bool next = i + 1 < n;
+    const int kn0 = (desc ? k - 1 : k + 1) * kTile;
     KeyRaw<NT, D> kr;
-    if (next) kr = key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, k0 + kTile + wave * 16 + c, T, g);
-    if (two) dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, k0 + kTile, kt, dtb, bb, k2, g, c);
+    if (next) kr = key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kn0 + wave * 16 + c, T, g);
+    if (two) dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, q2, kt, dtb, bb, k2, g, c);
     dkv_store<NT, D>(p, kt, b, h, inv_scale, g);
     if (next) {
-      key_tile_init<NT, D>(p, k0 + kTile, wave, c, kt);
+      key_tile_init<NT, D>(p, kn0, wave, c, kt);
       key_raw_terms<NT, D>(kr, kt);
     }
   }
