@@ -974,6 +974,22 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
   const bf16* ot = qt + NT * kDTile;
   float Pa[4][4], G[4][4];
   bool live[4];
+  // dTau of the visit's pairs, loaded before the products so its latency
+  // runs under them: every load is issued (a pair without a slot reads the
+  // (b, h)'s first element) and masked afterwards
+  float dtv[DTAU ? 4 : 1][4];
+  if constexpr (DTAU) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = q0 + 16 * j + 4 * g + r;
+        const bool ok = t >= kt.qlo && t <= kt.qhi;
+        const int col = ok ? tau_col(p, t, kt.tk) : -1;
+        const float x = (float)dtb[col >= 0 ? (int64_t)t * p.dtau.s1 + col : 0];
+        dtv[j][r] = col >= 0 ? x : 0.f;
+      }
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int qa = q0 + 16 * j;
@@ -1006,10 +1022,7 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
       const float pv = sigmoid_scaled(sv[r], k2, b2);
       const float a = sa_[ql];
       float dt = fmaf(dp[r], a, -scf_[ql]);
-      if (DTAU && ok) {
-        const int col = tau_col(p, t, kt.tk);
-        if (col >= 0) dt += (float)dtb[(int64_t)t * p.dtau.s1 + col];
-      }
+      if constexpr (DTAU) dt += dtv[j][r];
       Pa[j][r] = ok ? pv * a : 0.f;
       G[j][r] = ok ? dt * (pv - pv * pv) : 0.f;
     }
