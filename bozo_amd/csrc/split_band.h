@@ -326,6 +326,24 @@ __device__ __forceinline__ int band_tau_col(const BandParams& p, int t, int key)
   return tau_col(p, t, key);
 }
 
+// The pre-sigmoid bias of a lane's 16 pairs of one key block (query tq, row
+// `brow` of the bias; keys kb0 + 16 j + 4 g + r) times -log2(e), zero off
+// the band [lo, hi]: loaded together ahead of the block's products, so the
+// loads' latency runs under them (a pair off the band reads the row's first
+// element).
+__device__ __forceinline__ void bias_block(const BandParams& p, const float* brow, int tq, int kb0, int g, int lo,
+                                           int hi, float (*b2)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = kb0 + 16 * j + 4 * g + r;
+      const bool ok = (key >= lo) & (key <= hi);
+      const float x = brow[ok ? bias_col(p, tq, key) : 0];
+      b2[j][r] = ok ? -kLog2e * x : 0.f;
+    }
+}
+
 // Rows t0w .. t0w + 15 (the wave's queries) of a [B,T,H,Wtau] tau / dTau of
 // this (b, h): lane l moves key kb0 + l of each row.
 template <typename E>
@@ -401,6 +419,8 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
   stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, [&](const bf16* kt, int kb0) {
     float pr[4][4];
     int kind[4];
+    float b2v[BIAS ? 4 : 1][4];
+    if constexpr (BIAS) bias_block(p, brow, tq, kb0, g, lo, hi, b2v);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       kind[j] = sub_kind(wb, kb0 + 16 * j);
@@ -414,8 +434,7 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = (key >= lo) & (key <= hi);
-        float b2 = 0.f;
-        if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
+        const float b2 = BIAS ? b2v[j][r] : 0.f;
         const float pv = ok ? sigmoid_scaled(sc[r], k2, b2) : 0.f;
         msum += pv;
         pr[j][r] = pv;
@@ -526,11 +545,14 @@ struct DqTile {
     }
   }
 
-  // tau (masked) of one element
-  __device__ __forceinline__ float tau_of(const BandParams& p, float s, int key, bool ok) const {
-    float b2 = 0.f;
-    if (BIAS && ok) b2 = -kLog2e * brow[bias_col(p, tq, key)];
-    return ok ? sigmoid_scaled(s, k2, b2) : 0.f;
+  // tau (masked) of one element; b2: its bias_block value
+  __device__ __forceinline__ float tau_of(float s, float b2, bool ok) const {
+    return ok ? sigmoid_scaled(s, k2, BIAS ? b2 : 0.f) : 0.f;
+  }
+
+  // bias_block of key block kb0 for this lane (nothing without a bias)
+  __device__ __forceinline__ void bias_of(const BandParams& p, int kb0, float (*b2)[4]) const {
+    if constexpr (BIAS) bias_block(p, brow, tq, kb0, g, lo, hi, b2);
   }
 
   // G = tau (1 - tau) (a dP - c + dTau), zero off the band (dtv: the staged
@@ -562,6 +584,8 @@ struct DqTile {
   __device__ __forceinline__ void g_pass(const BandParams& p, const bf16* kt, int kb0) {
     E dv[DTAU ? 16 : 1];
     if constexpr (DTAU) dtau_rows_load(p, dbh, dv, t0w, kb0, lane);
+    float b2v[BIAS ? 4 : 1][4];
+    bias_of(p, kb0, b2v);
     f32x4 sc[4], dp[4];
     int kind[4];
 #pragma unroll
@@ -579,7 +603,7 @@ struct DqTile {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = kind[j] != 0 && (key >= lo) & (key <= hi);
-        G[j][r] = kind[j] != 0 ? g_of(tau_of(p, sc[j][r], key, ok), dp[j][r], dtv[r], ok) : 0.f;
+        G[j][r] = kind[j] != 0 ? g_of(tau_of(sc[j][r], BIAS ? b2v[j][r] : 0.f, ok), dp[j][r], dtv[r], ok) : 0.f;
       }
     }
     dq_product(kt, kind, G);
@@ -623,6 +647,8 @@ struct DqTile {
     for (int s = 0; s < 2; ++s) {
       if (s >= bl.n) break;
       const int kb0 = bl.first + s * kTile;
+      float b2v[BIAS ? 4 : 1][4];
+      bias_of(p, kb0, b2v);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
@@ -632,7 +658,7 @@ struct DqTile {
         for (int r = 0; r < 4; ++r) {
           const int key = kb0 + 16 * j + 4 * g + r;
           const bool ok = (key >= lo) & (key <= hi);
-          const float pv = tau_of(p, sc[r], key, ok);
+          const float pv = tau_of(sc[r], BIAS ? b2v[j][r] : 0.f, ok);
           P[s][j][r] = pv;
           Dp[s][j][r] = ok ? dp[r] : 0.f;
           msum += pv;
@@ -666,6 +692,8 @@ struct DqTile {
 
   // MODE 2 first pass: the band sums of one block
   __device__ __forceinline__ void sums_pass(const BandParams& p, const bf16* kt, int kb0) {
+    float b2v[BIAS ? 4 : 1][4];
+    bias_of(p, kb0, b2v);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (sub_kind(wb, kb0 + 16 * j) == 0) continue;
@@ -675,7 +703,7 @@ struct DqTile {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = (key >= lo) & (key <= hi);
-        const float pv = tau_of(p, sc[r], key, ok);
+        const float pv = tau_of(sc[r], BIAS ? b2v[j][r] : 0.f, ok);
         msum += pv;
         dsum = fmaf(pv, ok ? dp[r] : 0.f, dsum);
       }
@@ -977,7 +1005,18 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
   // dTau of the visit's pairs, loaded before the products so its latency
   // runs under them: every load is issued (a pair without a slot reads the
   // (b, h)'s first element) and masked afterwards
-  float dtv[DTAU ? 4 : 1][4];
+  float dtv[DTAU ? 4 : 1][4], b2v[BIAS ? 4 : 1][4];
+  if constexpr (BIAS) {  // the bias of the same pairs, likewise
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = q0 + 16 * j + 4 * g + r;
+        const bool ok = t >= kt.qlo && t <= kt.qhi;
+        const float x = bb[ok ? (int64_t)t * p.bias.s1 + bias_col(p, t, kt.tk) : 0];
+        b2v[j][r] = ok ? -kLog2e * x : 0.f;
+      }
+  }
   if constexpr (DTAU) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -1017,9 +1056,7 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
       const int ql = 16 * j + 4 * g + r;  // query - q0
       const int t = q0 + ql;
       const bool ok = t >= kt.qlo && t <= kt.qhi;
-      float b2 = 0.f;
-      if (BIAS && ok) b2 = -kLog2e * bb[(int64_t)t * p.bias.s1 + bias_col(p, t, kt.tk)];
-      const float pv = sigmoid_scaled(sv[r], k2, b2);
+      const float pv = sigmoid_scaled(sv[r], k2, BIAS ? b2v[j][r] : 0.f);
       const float a = sa_[ql];
       float dt = fmaf(dp[r], a, -scf_[ql]);
       if constexpr (DTAU) dt += dtv[j][r];
