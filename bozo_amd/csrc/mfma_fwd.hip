@@ -39,6 +39,20 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
                                           float& msum, f32x4* macc = nullptr) {
   float pr[4][4];
   int kind[4];
+  // the block's bias, loaded ahead of its products so the loads' latency
+  // runs under them (pairs off the band read the batch's first element)
+  float b2v[BIAS ? 4 : 1][4];
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * j + 4 * g + r;
+        const bool ok = (key >= lo) & (key <= hi);
+        const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
+        b2v[j][r] = ok ? -kLog2e * x : 0.f;
+      }
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     kind[j] = sub_kind(wb, kb0 + 16 * j);
@@ -56,8 +70,7 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
       // kind 2 covers every valid row of the wave; rows past T (hi < lo)
       // stay masked so no tau store or bias load leaves the tensors
       const bool ok = kind[j] == 2 ? hi >= lo : ((key >= lo) & (key <= hi));
-      float b2 = 0.f;
-      if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+      const float b2 = BIAS ? b2v[j][r] : 0.f;
       // computed on every lane (finite inputs) and selected: a conditional
       // sigmoid becomes a branch per element
       const float sg = sigmoid_scaled(s[r], k2, b2);

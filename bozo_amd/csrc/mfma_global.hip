@@ -139,6 +139,18 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
     constexpr bool diag = decltype(diag_tag)::value;
     constexpr bool TB = TAU && decltype(tau_tag)::value;
     constexpr uint32_t KO = S * kDTile * 2, VO = (2 + S) * kDTile * 2;
+    // the block's bias, loaded ahead of its products so the loads' latency
+    // runs under them
+    float b2v[BIAS ? 2 : 1][2][4];
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            b2v[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, blk * kTile + 32 * kh + 16 * j + 4 * g + r);
+    }
     // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
     f32x4 s[2][2];
 #pragma unroll
@@ -165,7 +177,7 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = blk * kTile + 32 * kh + 16 * j + 4 * g + r, query = t0 + dq;
-          const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
+          const float b2 = BIAS ? b2v[i][j][r] : 0.f;
           const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
           pr[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : pv;
           if (TB) {
@@ -382,6 +394,17 @@ void gl_dq(BandArgs args) {
     constexpr bool TB = DTAU && decltype(tau_tag)::value;  // the block holds dtau_local columns
     const bf16* Ks = Kb[blk & 1];
     const bf16* Vs = Vb[blk & 1];
+    // the block's bias, loaded ahead of its products
+    float b2v[BIAS ? 2 : 1][2][4];
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            b2v[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, blk * kTile + 32 * kh + 16 * j + 4 * g + r);
+    }
     f32x4 s[2][2], dp[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -411,7 +434,7 @@ void gl_dq(BandArgs args) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = blk * kTile + 32 * kh + 16 * j + 4 * g + r, query = t0 + dq;
-          const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
+          const float b2 = BIAS ? b2v[i][j][r] : 0.f;
           const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
           float dt = dp[i][j][r] * ca[i] - cc[i];
           if (TB) {
