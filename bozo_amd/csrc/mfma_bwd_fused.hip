@@ -360,6 +360,21 @@ void mfma_bwd_fused(BandArgs args) {
     f32x4 dpv[kXSlots];
     int kind[kXSlots];
     float msum = 0.f, dsum = 0.f;
+    // the band's bias, loaded ahead of the products so the loads' latency
+    // runs under them (pairs off the band read the batch's first element)
+    float b2v[BIAS ? kXSlots : 1][4];
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int sl = 0; sl < kXSlots; ++sl)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int gg = w + sl;
+          const int key = (t - 1 + (gg >> 2)) * kTile + 16 * (gg & 3) + 4 * g + r;
+          const bool ok = (key >= lo) & (key <= hi);
+          const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
+          b2v[sl][r] = ok ? -kLog2e * x : 0.f;
+        }
+    }
 #pragma unroll
     for (int sl = 0; sl < kXSlots; ++sl) {
       const int gg = w + sl;  // key group among the 8 of blocks t-1, t
@@ -407,8 +422,7 @@ void mfma_bwd_fused(BandArgs args) {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 4 * g + r;
         const bool ok = full ? rowok : ((key >= lo) & (key <= hi));
-        float b2 = 0.f;
-        if (BIAS && ok) b2 = -kLog2e * ld<float>(p.bias, bias_off(p, b, tq, key));
+        const float b2 = BIAS ? b2v[sl][r] : 0.f;
         // computed on every lane (finite inputs) and selected: a conditional
         // sigmoid becomes a branch per element
         const float sg = sigmoid_scaled(s[r], k2, b2);
