@@ -107,8 +107,8 @@ void mfma_bwd_fused(BandArgs args) {
   const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
   const int bh = id / nch, run = id % nch;
   const int b = bh / p.H, h = bh % p.H, T = p.T;
-  const int tA = (int)((int64_t)run * p.ntiles / nch);
-  const int tB = (int)((int64_t)(run + 1) * p.ntiles / nch);
+  const int tA = run_bound(run, p.ntiles, nch);
+  const int tB = run_bound(run + 1, p.ntiles, nch);
   const int tE = tB < p.ntiles ? tB : tB - 1;  // the halo step when tB < ntiles, else tB - 1
   // the run's direction (uniform): odd runs step down from tE to tA
   const bool desc = TENSION_BWD_ALTERNATE && (run & 1) != 0;

@@ -116,6 +116,15 @@ __device__ __forceinline__ float wave_sum_g(float x) {
   return x;
 }
 
+// First tile of run `run` of `nch` runs over `ntiles` tiles, run * ntiles /
+// nch: in 32 bits whenever the product fits (the branch is uniform), since
+// a 64-bit division is ~150 scalar instructions, all of them issued before
+// the kernel's first load.
+__device__ __forceinline__ int run_bound(int run, int ntiles, int nch) {
+  if (ntiles <= 46340) return (int)((unsigned)(run * ntiles) / (unsigned)nch);
+  return (int)((int64_t)run * ntiles / nch);
+}
+
 struct TileId {
   int b, h, tile;
 };

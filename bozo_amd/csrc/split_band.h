@@ -841,8 +841,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
   const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
   const int bh = id / nr, run = id % nr;
   const int b = bh / p.H, h = bh % p.H, T = p.T;
-  const int tA = (int)((int64_t)run * p.ntiles / nr);
-  const int tB = (int)((int64_t)(run + 1) * p.ntiles / nr);
+  const int tA = run_bound(run, p.ntiles, nr);
+  const int tB = run_bound(run + 1, p.ntiles, nr);
   if (tA >= tB) return;
 
   using E = Elem<NT>;
@@ -1178,8 +1178,8 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
   const int bh = id / nr, run = id % nr;
   const int b = bh / p.H, h = bh % p.H, T = p.T;
-  const int kA = (int)((int64_t)run * p.ntiles / nr);
-  const int kB = (int)((int64_t)(run + 1) * p.ntiles / nr);
+  const int kA = run_bound(run, p.ntiles, nr);
+  const int kB = run_bound(run + 1, p.ntiles, nr);
   const bool desc = (run & 1) != 0;
 
   using E = Elem<NT>;
