@@ -33,6 +33,44 @@ __device__ __forceinline__ float gl_bias2(const BandParams& p, int b, int q, int
   return -kLog2e * ld<float>(p.bias, (int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + (int64_t)kk * p.bias.s2);
 }
 
+// The bias of query q at keys k .. k + 3 (k a multiple of 4, k + 3 < T) as
+// one 16-byte load, times -log2(e); rows past T read row T-1 (masked).  For
+// a bias with unit column stride and 16-byte aligned rows (gl_bias_rows4).
+__device__ __forceinline__ f32x4 gl_bias2x4(const BandParams& p, int b, int q, int k) {
+  const int qq = q < p.T ? q : p.T - 1;
+  const f32x4 x = *(const f32x4*)((const float*)p.bias.p + (int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + k);
+  return x * -kLog2e;
+}
+
+__device__ __forceinline__ bool gl_bias_rows4(const BandParams& p) {
+  return p.bias.s2 == 1 && (p.bias.s1 & 3) == 0 && (p.bias.s0 & 3) == 0 && ((uintptr_t)p.bias.p & 15) == 0;
+}
+
+// A lane's bias of one key block (queries t0 + 32 qh + 16 i + c, keys
+// blk * 64 + 32 kh + 16 j + 4 g + r): four 16-byte loads when the block lies
+// inside [0, T) and the rows allow it, else sixteen element loads.
+__device__ __forceinline__ void gl_bias_block(const BandParams& p, int b, int t0, int blk, int qh, int kh, int g,
+                                              int c, bool rows4, float (*b2)[2][4]) {
+  const int kbase = blk * kTile + 32 * kh + 4 * g;
+  if (rows4 && (blk + 1) * kTile <= p.T) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x4 x = gl_bias2x4(p, b, t0 + 32 * qh + 16 * i + c, kbase + 16 * j);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b2[i][j][r] = x[r];
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b2[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, kbase + 16 * j + r);
+  }
+}
+
 __device__ __forceinline__ int gl_tau_col(const BandParams& p, int q, int k) {
   const int j = p.T - 1 - k;
   return (q < p.T && k < p.T && j < p.Wtau) ? j : -1;
@@ -128,6 +166,7 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
   copy(0, S0{});
   copy(1, S1{});
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  const bool rows4 = BIAS && gl_bias_rows4(p);  // 16-byte bias loads (gl_bias_block)
   const bf16x8 ones = ones_bf16x8();
   f32x4 acc[2][4] = {};
   f32x4 macc[2] = {};
@@ -142,15 +181,7 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
     // the block's bias, loaded ahead of its products so the loads' latency
     // runs under them
     float b2v[BIAS ? 2 : 1][2][4];
-    if constexpr (BIAS) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            b2v[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, blk * kTile + 32 * kh + 16 * j + 4 * g + r);
-    }
+    if constexpr (BIAS) gl_bias_block(p, b, t0, blk, qh, kh, g, c, rows4, b2v);
     // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
     f32x4 s[2][2];
 #pragma unroll
@@ -387,6 +418,7 @@ void gl_dq(BandArgs args) {
     tile_async_src(vsrc, kTile, Vb[1], wave);
   }
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
+  const bool rows4 = BIAS && gl_bias_rows4(p);  // 16-byte bias loads (gl_bias_block)
   f32x4 acc[2][4] = {};
 
   auto block = [&](int blk, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
@@ -396,15 +428,7 @@ void gl_dq(BandArgs args) {
     const bf16* Vs = Vb[blk & 1];
     // the block's bias, loaded ahead of its products
     float b2v[BIAS ? 2 : 1][2][4];
-    if constexpr (BIAS) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            b2v[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, blk * kTile + 32 * kh + 16 * j + 4 * g + r);
-    }
+    if constexpr (BIAS) gl_bias_block(p, b, t0, blk, qh, kh, g, c, rows4, b2v);
     f32x4 s[2][2], dp[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
