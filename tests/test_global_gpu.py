@@ -59,6 +59,27 @@ def test_global_bf16_bias_tau_local(dev, use_bias, use_tl):
     check(hip, ref, torch.bfloat16, use_tl)
 
 
+@pytest.mark.parametrize("pad", [1, 4])
+def test_global_bf16_bias_row_views(dev, pad):
+    """The bias as a view into wider rows (row stride T + pad): with pad 4
+    the rows stay 16-byte aligned and the kernels read a block's bias in
+    16-byte pieces (the last, ragged block element by element); with pad 1
+    every load is an element load."""
+    B, H, T, D = 2, 3, 200, 64
+    inp = make_inputs(B, T, H, D, seed=11 + pad, std=0.5, dtype=torch.bfloat16, W=64)
+    wide = torch.randn(B, T, T + pad, generator=torch.Generator().manual_seed(pad)) * 0.5
+    inp["bias"] = wide[:, :, :T]
+    from bozo_amd import global_tension
+    Q, K, V = (inp[n].to(dev).requires_grad_(True) for n in "QKV")
+    bias = wide.to(dev)[:, :, :T]
+    assert bias.stride(1) == T + pad
+    out = global_tension(Q, K, V, 8.0, bias=bias)
+    (out.float() * inp["dO"].to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    ref = oracle_run(inp, 8.0, use_bias=True)
+    check((out, None, (Q.grad, K.grad, V.grad)), ref, torch.bfloat16)
+
+
 def test_config3_bf16_full_size(dev):
     """B4 H12 T2048 d64 bf16, full causal, tau-mass."""
     B, H, T, D = 4, 12, 2048, 64
