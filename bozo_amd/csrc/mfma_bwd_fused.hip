@@ -365,15 +365,27 @@ void mfma_bwd_fused(BandArgs args) {
     float b2v[BIAS ? kXSlots : 1][4];
     if constexpr (BIAS) {
 #pragma unroll
-      for (int sl = 0; sl < kXSlots; ++sl)
+      for (int sl = 0; sl < kXSlots; ++sl) {
+        const int gg = w + sl;
+        const int key0 = (t - 1 + (gg >> 2)) * kTile + 16 * (gg & 3) + 4 * g;
+        if (rowok && p.bias.s2 == 1 && sub_kind(wb, key0 - 4 * g) == 2) {
+          // every key of the group is in the row's band: its four columns
+          // are consecutive (one 16-byte load)
+          const float* src = (const float*)p.bias.p + bias_off(p, b, tq, key0);
+          float x[4];
+          __builtin_memcpy(x, src, 16);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int gg = w + sl;
-          const int key = (t - 1 + (gg >> 2)) * kTile + 16 * (gg & 3) + 4 * g + r;
-          const bool ok = (key >= lo) & (key <= hi);
-          const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
-          b2v[sl][r] = ok ? -kLog2e * x : 0.f;
+          for (int r = 0; r < 4; ++r) b2v[sl][r] = -kLog2e * x[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = key0 + r;
+            const bool ok = (key >= lo) & (key <= hi);
+            const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
+            b2v[sl][r] = ok ? -kLog2e * x : 0.f;
+          }
         }
+      }
     }
 #pragma unroll
     for (int sl = 0; sl < kXSlots; ++sl) {

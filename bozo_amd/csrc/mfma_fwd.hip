@@ -44,14 +44,26 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
   float b2v[BIAS ? 4 : 1][4];
   if constexpr (BIAS) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      const int key0 = kb0 + 16 * j + 4 * g;
+      if (hi >= lo && p.bias.s2 == 1 && sub_kind(wb, kb0 + 16 * j) == 2) {
+        // every key of the group is in the row's band: its four columns are
+        // consecutive (one 16-byte load)
+        const float* src = (const float*)p.bias.p + bias_off(p, b, tq, key0);
+        float x[4];
+        __builtin_memcpy(x, src, 16);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb0 + 16 * j + 4 * g + r;
-        const bool ok = (key >= lo) & (key <= hi);
-        const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
-        b2v[j][r] = ok ? -kLog2e * x : 0.f;
+        for (int r = 0; r < 4; ++r) b2v[j][r] = -kLog2e * x[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = key0 + r;
+          const bool ok = (key >= lo) & (key <= hi);
+          const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
+          b2v[j][r] = ok ? -kLog2e * x : 0.f;
+        }
       }
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
