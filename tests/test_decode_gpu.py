@@ -169,6 +169,43 @@ def test_decode_config4_shape_steps(dev):
         pin, pout = pout, pin
 
 
+def test_decode_strided_views(dev):
+    """Caches and rows as views with padding (the kernel reads strides, not
+    shapes): caches sliced from [N, H + 1, W, D + 8] storage, q / k_new /
+    v_new rows from [N, H, D + 16]; the fast kernel's 32-bit strides and
+    the ring append land on the views, checked against the oracle."""
+    from bozo_amd import decode_step
+    N, H, D, W, S = 8, 4, 64, 96, 3
+    g = torch.Generator().manual_seed(21)
+    kbig = (torch.randn(N, H + 1, W, D + 8, generator=g) * 0.5).to(torch.bfloat16)
+    vbig = (torch.randn(N, H + 1, W, D + 8, generator=g) * 0.5).to(torch.bfloat16)
+    kbd, vbd = kbig.to(dev), vbig.to(dev)
+    kd, vd = kbd[:, 1:, :, :D], vbd[:, 1:, :, :D]
+    assert kd.stride() == ((H + 1) * W * (D + 8), W * (D + 8), D + 8, 1)
+    kc, vc = kbig[:, 1:, :, :D].contiguous(), vbig[:, 1:, :, :D].contiguous()
+    pos = torch.tensor([0, 1, 50, 95, 96, 97, 200, 7], dtype=torch.int32)
+    pin, pout = pos.to(dev), torch.empty(N, dtype=torch.int32, device=dev)
+    for s in range(S):
+        rows = [(torch.randn(N, H, D + 16, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3)]
+        q, kn, vn = (r[:, :, 8:8 + D] for r in rows)
+        qd, knd, vnd = (r.to(dev)[:, :, 8:8 + D] for r in rows)
+        assert qd.stride(1) == D + 16
+        tau = torch.empty(N, H, W, dtype=torch.bfloat16, device=dev)
+        out = decode_step(qd, knd, vnd, kd, vd, pin, pout, 8.0, True, tau)
+        ro, rt = O.decode_step(f64(q), f64(kc), f64(vc), pos.numpy(), W, 8.0)
+        assert rel_l2(f64(out), ro) <= 2e-2
+        assert max_abs(f64(tau), rt) <= 4e-3
+        kc_np, vc_np, pos_np = O.decode_append(kc.float().numpy(), vc.float().numpy(), pos.numpy(),
+                                               kn.float().numpy(), vn.float().numpy(), W)
+        kc, vc = torch.from_numpy(kc_np).to(torch.bfloat16), torch.from_numpy(vc_np).to(torch.bfloat16)
+        pos = torch.from_numpy(pos_np.astype(np.int32))
+        assert torch.equal(kd.cpu(), kc) and torch.equal(vd.cpu(), vc)
+        assert torch.equal(pout.cpu(), pos)
+        pin, pout = pout, pin
+    # the padding around the views is untouched
+    assert torch.equal(kbd[:, 0].cpu(), kbig[:, 0]) and torch.equal(kbd[..., D:].cpu(), kbig[..., D:])
+
+
 @pytest.mark.parametrize("dtype,out_dtype", [(torch.float32, None), (torch.bfloat16, torch.float32),
                                              (torch.float64, None), (torch.bfloat16, None)])
 def test_rope(dev, dtype, out_dtype):
