@@ -16,7 +16,8 @@
 //   * the two key halves of a query half meet once, through LDS, at the end.
 // Workgroups go out heaviest tile first; blockIdx -> (b, h) keeps every tile
 // of one (b, h) on one XCD (round-robin dispatch, B*H a multiple of 8), so its
-// 512 KB of K/V stays in that XCD's L2.
+// 512 KB of K/V stays in that XCD's L2, and groups the heads of a sequence on
+// as few XCDs as it can (gl_slot).
 #include <type_traits>
 
 #include "mfma_common.h"
@@ -28,9 +29,10 @@ namespace tension {
 // column of the down-sampled tau_local / dtau_local [B, T, H, Wl] (slot j =
 // key T-1-j, model.py:235-236), -1 when the pair has no slot there.  Rows and
 // keys past T are clamped for the bias load (those pairs are masked).
+// The host takes these kernels with a float32 bias only.
 __device__ __forceinline__ float gl_bias2(const BandParams& p, int b, int q, int k) {
   const int qq = q < p.T ? q : p.T - 1, kk = k < p.T ? k : p.T - 1;
-  return -kLog2e * ld<float>(p.bias, (int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + (int64_t)kk * p.bias.s2);
+  return -kLog2e * ((const float*)p.bias.p)[(int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + (int64_t)kk * p.bias.s2];
 }
 
 // The bias of query q at keys k .. k + 3 (k a multiple of 4, k + 3 < T) as
@@ -69,6 +71,23 @@ __device__ __forceinline__ void gl_bias_block(const BandParams& p, int b, int t0
 #pragma unroll
         for (int r = 0; r < 4; ++r) b2[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, kbase + 16 * j + r);
   }
+}
+
+// blockIdx -> (tile rank, b * H + h).  Dispatch is round-robin over the 8
+// XCDs (id % 8).  With B H a multiple of 8, XCD x takes the B H / 8
+// consecutive (b, h) pairs from x B H / 8 on, rank by rank: every tile of one
+// (b, h) runs on one XCD (its K / V or Q / dO stays in that XCD's L2), and the
+// heads of one sequence share as few XCDs as the count allows (they read the
+// same head-agnostic bias rows).  Otherwise (b, h) = id % (B H).
+struct GlSlot {
+  int rank, bh;
+};
+__device__ __forceinline__ GlSlot gl_slot(int BH, int id) {
+  if ((BH & 7) == 0) {
+    const int per = BH >> 3, n = id >> 3;
+    return {n / per, (id & 7) * per + n % per};
+  }
+  return {id / BH, id % BH};
 }
 
 __device__ __forceinline__ int gl_tau_col(const BandParams& p, int q, int k) {
@@ -314,7 +333,7 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
 }
 
 // A workgroup owns one 64-query tile of one (b, h); workgroups go out
-// heaviest tile first, and blockIdx -> (b, h) = id % (B H) keeps the tiles of
+// heaviest tile first, and blockIdx -> (b, h) (gl_slot) keeps the tiles of
 // one (b, h) on one XCD (round-robin dispatch).  (Pairing a heavy and a light
 // tile per workgroup, one round of equal workgroups, measured slower.)
 template <bool BIAS, bool TAU>
@@ -324,10 +343,8 @@ void gl_fwd(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 lds[4][kDTile];
-  const int BH = p.B * p.H;
-  const int id = (int)blockIdx.x;
-  const int bh = id % BH;
-  gl_fwd_tile<BIAS, TAU>(p, p.ntiles - 1 - id / BH, bh / p.H, bh % p.H, lds);
+  const GlSlot sl = gl_slot(p.B * p.H, (int)blockIdx.x);
+  gl_fwd_tile<BIAS, TAU>(p, p.ntiles - 1 - sl.rank, sl.bh / p.H, sl.bh % p.H, lds);
 }
 
 // ---------------------------------------------------------------- backward
@@ -363,10 +380,9 @@ void gl_dq(BandArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int qh = wave & 1, kh = wave >> 1;
-  const int BH = p.B * p.H;
-  const int id = (int)blockIdx.x;
-  const int tile = p.ntiles - 1 - id / BH;  // heaviest first
-  const int bh = id % BH;
+  const GlSlot sl = gl_slot(p.B * p.H, (int)blockIdx.x);
+  const int tile = p.ntiles - 1 - sl.rank;  // heaviest first
+  const int bh = sl.bh;
   const int b = bh / p.H, h = bh % p.H, T = p.T;
   const int t0 = tile * kTile;
   const int nblk = tile + 1;
@@ -556,10 +572,9 @@ void gl_dkv(BandArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int kh = wave & 1, qh = wave >> 1;
-  const int BH = p.B * p.H;
-  const int id = (int)blockIdx.x;
-  const int tile = id / BH;  // key tile 0 sees every query block: heaviest first
-  const int bh = id % BH;
+  const GlSlot sl = gl_slot(p.B * p.H, (int)blockIdx.x);
+  const int tile = sl.rank;  // key tile 0 sees every query block: heaviest first
+  const int bh = sl.bh;
   const int b = bh / p.H, h = bh % p.H, T = p.T;
   const int k0 = tile * kTile;
   const int nblk = p.ntiles - tile;
@@ -593,6 +608,55 @@ void gl_dkv(BandArgs args) {
   if (tid < 128) coef[0][tid >> 6][tid & 63] = coef_load(q_first);
   float cnext = nblk > 1 ? coef_load(q_first + 1) : 0.f;
   const TileSrc qsrc = tile_src(qb_, p.q.s1, T, wave, lane), gsrc = tile_src(gb_, p.dout.s1, T, wave, lane);
+  // bias (float32, host-checked): the lane's two key columns (keys past T
+  // read column T-1; those pairs are masked) from its first query row of a
+  // block's half, 32 qh + 4 g
+  const float* bcol[2] = {nullptr, nullptr};
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = k0 + 32 * kh + 16 * i + c;
+      bcol[i] = (const float*)p.bias.p + b * p.bias.s0 + (int64_t)(key < T ? key : T - 1) * p.bias.s2 +
+                (int64_t)(32 * qh + 4 * g) * p.bias.s1;
+    }
+  }
+  // the bias of block blk's pairs (query 16 j + 4 g + r of the half, key
+  // tile i) into b2n; rows past T (the last block of a ragged sequence) read
+  // row T-1 (masked).  BPRE: block blk + 1's is loaded at the end of block
+  // blk, ahead of the ring copy of block blk + 2, so the wait for that
+  // copy's predecessor at the loop head also covers it.  With dtau_local
+  // that would spill; there each block loads its own at its start, ahead of
+  // its products.  (The empty asm statements keep the two paths' loads
+  // apart: merged, every row offset became a per-lane 64-bit product.)
+  constexpr bool BPRE = BIAS && !DTAU;
+  float b2n[BIAS ? 2 : 1][2][4];
+  auto bias_fetch = [&](int blk) __attribute__((always_inline)) {
+    const int qf = (q_first + blk) * kTile;
+    const int64_t s1 = p.bias.s1;
+    asm volatile("" ::: "memory");
+    if (qf + kTile <= T) {
+      const int64_t o = (int64_t)qf * s1;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) b2n[i][j][r] = bcol[i][o + (16 * j + r) * s1];
+      asm volatile("" ::: "memory");
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int q = qf + 32 * qh + 16 * j + 4 * g + r;
+            b2n[i][j][r] = bcol[i][(int64_t)((q < T ? q : T - 1) - 32 * qh - 4 * g) * s1];
+          }
+      asm volatile("" ::: "memory");
+    }
+  };
+  if constexpr (BPRE) bias_fetch(0);
   tile_async_src(qsrc, q_first * kTile, Qb[0], wave);
   tile_async_src(gsrc, q_first * kTile, Gb[0], wave);
   if (nblk > 1) {
@@ -613,6 +677,7 @@ void gl_dkv(BandArgs args) {
     cnext = coef_load(q_first + (blk + 2 < nblk ? blk + 2 : nblk - 1));
     const bf16* Qs = Qb[blk & 1];
     const bf16* Gs = Gb[blk & 1];
+    if constexpr (BIAS && !BPRE) bias_fetch(blk);
     f32x4 s[2][2], dp[2][2];  // [query tile j][key tile i]
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -661,7 +726,7 @@ void gl_dkv(BandArgs args) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int query = (q_first + blk) * kTile + 32 * qh + 16 * j + 4 * g + r, key = k0 + dk_;
-          const float b2 = BIAS ? gl_bias2(p, b, query, key) : 0.f;
+          const float b2 = BIAS ? -kLog2e * b2n[i][j][r] : 0.f;
           const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[j][i][r], k2, b2)));
           const bool off = diag && 32 * qh + 16 * j + 4 * g + r < dk_;  // query before key
           float dt = dp[j][i][r] * a4[j][r] - c4[j][r];
@@ -689,6 +754,9 @@ void gl_dkv(BandArgs args) {
         dk[i][m] = mfma(qt[m], gbv, dk[i][m]);
       }
     }
+    // unconditional (the last block loads its own again) for the same
+    // reason as the ring copies
+    if constexpr (BPRE) bias_fetch(blk + 1 < nblk ? blk + 1 : blk);
   };
   // Block blk's ring slot takes block blk + 2, or past the end a copy of the
   // last block that nothing reads: with every copy and coefficient load
