@@ -69,7 +69,7 @@ namespace tension {
 #define TENSION_BWD_ALTERNATE 1
 #endif
 
-// FAST (W = 64, T a multiple of 64, no bias; dTau in bf16 rows): the band of every
+// FAST (W = 64, T a multiple of 64; a bias or dTau in bf16 rows): the band of every
 // 16-query group is the same five key groups -- slot 0 the old block's
 // diagonal group (key >= query - 64, i.e. 4g + r >= c within the group),
 // slots 1..3 entirely valid, slot 4 the new block's diagonal group (key <=
@@ -79,7 +79,7 @@ namespace tension {
 template <int NORM, bool BIAS, bool DTAU, bool FAST>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TENSION_BWD_WAVES_PER_EU, TENSION_BWD_WAVES_PER_EU)))
 void mfma_bwd_fused(BandArgs args) {
-  static_assert(!FAST || !BIAS, "the fast path has no bias");
+  static_assert(!FAST || !(BIAS && DTAU), "the fast path takes a bias or dTau, not both");
   touch_args(args);
   const BandParams p = band_params(args);
   __shared__ __attribute__((aligned(16))) bf16 Kt[2][kDTile];  // key block k in slot k & 1
@@ -200,6 +200,7 @@ void mfma_bwd_fused(BandArgs args) {
   // dK/dV (key group w) of the block the current step completes: carried
   // in from the previous step (ascending block t-1, descending block t)
   f32x4 dk_old[4] = {}, dv_old[4] = {};
+
   TileRegs dnext;  // FAST dTau: the next step's rows
   // FAST: diagonal-group masks (1 valid, 0 not) for keys 4g + r of query c
   // (lane conditions: the compiler keeps them as scalar lane masks)
@@ -210,6 +211,22 @@ void mfma_bwd_fused(BandArgs args) {
   // FAST phase 1 with all five slots live (steps t >= 1; the halo only with
   // tau-mass normalisation): slot sl is key group w + sl of blocks t-1, t;
   // slot 0 is the old block's diagonal group, slot 4 the new block's
+  // the step's bias (band_tile_bias, groups in slot order: j = (w + sl) & 3,
+  // so slot sl reads bcur[sl & 3]; slots 0 and 4 share one element).  It
+  // enters as the initial accumulator of the score product, scaled by
+  // `scale` (sigma(S / scale + bias) = sigma((S + scale bias) / scale)), so
+  // its registers are free once the product is issued.
+  float bcur[BIAS ? 4 : 1][4];
+  const float bsc = (float)p.scale;
+  auto s_init = [&](int sl) -> f32x4 {
+    if constexpr (BIAS && !DTAU) {
+      const float* x = bcur[sl & 3];
+      return f32x4{x[0] * bsc, x[1] * bsc, x[2] * bsc, x[3] * bsc};
+    } else {
+      return f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
   auto phase1_live = [&](int t, auto dq_tag) {
     constexpr bool DQ = decltype(dq_tag)::value;
     const bf16* Kold = Kt[(t + 1) & 1];
@@ -225,7 +242,7 @@ void mfma_bwd_fused(BandArgs args) {
       const bf16* Ks = (gg >> 2) ? Knew : Kold;
       const bf16* Vs = (gg >> 2) ? Vnew : Vold;
       const int row = 16 * (gg & 3) + c;
-      f32x4 a = {}, d = {};
+      f32x4 a = s_init(sl), d = {};
       a = mfma(dt_row8(Ks, row, g), qf[0], a);
       a = mfma(dt_row8(Ks, row, 4 + g), qf[1], a);
       d = mfma(dt_row8(Vs, row, g), gf[0], d);
@@ -326,20 +343,32 @@ void mfma_bwd_fused(BandArgs args) {
       // registers live where the register file is full
       asm volatile("" ::: "memory");
     }
+    // the step's bias (band_tile_bias, groups in slot order: j = (w + sl) & 3)
+    // goes out ahead of the next step's loads, and with a bias every step
+    // issues those (the last step its own rows again, unused): on every path
+    // the same loads are younger than the bias, so its first use in phase 1
+    // waits for it alone, not for them
+    // (With dTau as well that would spill: there the bias is loaded where
+    // phase 1 starts.)
+    constexpr bool BEARLY = BIAS && !DTAU;
+    if constexpr (BEARLY) {
+      band_tile_bias(p, b, t * kTile, w, g, c, w, bcur);
+      asm volatile("" ::: "memory");
+    }
     TileRegs kn, vn, qn, on;
-    if (more) {
-      const uint32_t rb = (uint32_t)(bn * kTile);
+    if (more || BEARLY) {
+      const uint32_t rb = (uint32_t)((more ? bn : t) * kTile);
       kn = seq_tile_load(sk, rb * sk.rs2, loff(sk, lk0));
       vn = seq_tile_load(sv, rb * sv.rs2, loff(sv, lv0));
       if constexpr (!FAST) {  // fast path: issued at the start of phase 2
-        const uint32_t r0 = (uint32_t)(tn * kTile);
+        const uint32_t r0 = (uint32_t)((more ? tn : t) * kTile);
         qn = seq_tile_load(sq, r0 * sq.rs2, loff(sq, lq0));
         on = seq_tile_load(so, r0 * so.rs2, loff(so, lo0));
       }
     }
 
     // ---- phase 1: queries 16w..16w+15 of tile t
-    if (FAST && t >= 1 && (!halo || NORM == NORM_MASS_)) {
+    if (FAST && !BIAS && t >= 1 && (!halo || NORM == NORM_MASS_)) {
       // every slot live: one branch-free block, so the LDS reads, MFMAs and
       // sigmoids of different slots overlap
       if (!halo)
@@ -360,10 +389,10 @@ void mfma_bwd_fused(BandArgs args) {
     f32x4 dpv[kXSlots];
     int kind[kXSlots];
     float msum = 0.f, dsum = 0.f;
-    // the band's bias, loaded ahead of the products so the loads' latency
-    // runs under them (pairs off the band read the batch's first element)
-    float b2v[BIAS ? kXSlots : 1][4];
-    if constexpr (BIAS) {
+    // with dTau as well (BEARLY off): the band's bias, loaded ahead of the
+    // products (pairs off the band read the batch's first element)
+    float b2v[BIAS && !BEARLY ? kXSlots : 1][4];
+    if constexpr (BIAS && !BEARLY) {
 #pragma unroll
       for (int sl = 0; sl < kXSlots; ++sl) {
         const int gg = w + sl;
@@ -409,7 +438,7 @@ void mfma_bwd_fused(BandArgs args) {
       }
       const bf16* Ks = blk ? Knew : Kold;
       const bf16* Vs = blk ? Vnew : Vold;
-      f32x4 s = {}, d = {};
+      f32x4 s = s_init(sl), d = {};
       s = mfma(dt_row8(Ks, 16 * j + c, g), qf[0], s);
       s = mfma(dt_row8(Ks, 16 * j + c, 4 + g), qf[1], s);
       d = mfma(dt_row8(Vs, 16 * j + c, g), gf[0], d);
@@ -434,10 +463,9 @@ void mfma_bwd_fused(BandArgs args) {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 4 * g + r;
         const bool ok = full ? rowok : ((key >= lo) & (key <= hi));
-        const float b2 = BIAS ? b2v[sl][r] : 0.f;
         // computed on every lane (finite inputs) and selected: a conditional
         // sigmoid becomes a branch per element
-        const float sg = sigmoid_scaled(s[r], k2, b2);
+        const float sg = sigmoid_scaled(s[r], k2, BIAS && DTAU ? b2v[sl][r] : 0.f);
         const float x = ok ? sg : 0.f;
         pv[sl][r] = x;
         if (NORM == NORM_MASS_) {
@@ -659,7 +687,12 @@ static void go(const BandParams& p, hipStream_t st, unsigned nwg) {
 template <int NORM>
 static void go_n(const BandParams& p, hipStream_t st, unsigned nwg, bool bias, bool dtau) {
   if (bias) {
-    if (dtau) go<NORM, true, true, false>(p, st, nwg); else go<NORM, true, false, false>(p, st, nwg);
+    if (dtau)
+      go<NORM, true, true, false>(p, st, nwg);
+    else if (p.win == kTile && p.T % kTile == 0)
+      go<NORM, true, false, true>(p, st, nwg);
+    else
+      go<NORM, true, false, false>(p, st, nwg);
   } else if (dtau) {
     // bf16 dTau rows of 64 slots, 16-byte aligned: staged by the fast path
     const Buf& d = p.dtau;

@@ -476,6 +476,31 @@ __device__ __forceinline__ int sub_kind(const WaveBand& w, int k0) {
   return 1;
 }
 
+// The float32 bias [B, T, W] of a local band (W <= 64) for the 64-query tile
+// from t0, lane (c, g) of wave w: query row q = t0 + 16 w + c against keys
+// 16 j + 4 g + r of blocks t0 - 64 and t0.  With u = 16 j + 4 g + r - 16 w - c,
+// block t0 holds the key at column u + W (a band pair when -W <= u < 0) and
+// block t0 - 64 at column u + W - 64 (when 64 - W <= u), so each (j, r) is a
+// band pair in at most one of the two blocks and one element serves both:
+// x[s][r] for group j = (s + jrot) & 3.  Columns outside [0, W) (pairs of
+// neither block, masked where the bias is used) are clamped into the row,
+// rows past T read row T-1: every load is in bounds and branch-free.
+__device__ __forceinline__ void band_tile_bias(const BandParams& p, int b, int t0, int w, int g, int c, int jrot,
+                                               float (*x)[4]) {
+  const int q = t0 + 16 * w + c;
+  const float* row = (const float*)p.bias.p + (int64_t)b * p.bias.s0 + (int64_t)(q < p.T ? q : p.T - 1) * p.bias.s1;
+  const int u0 = 4 * g - 16 * w - c + p.W;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int col = u0 + 16 * ((s + jrot) & 3) + r;  // u + W
+      col = col >= p.W ? col - 64 : col;
+      col = col < 0 ? 0 : (col > p.W - 1 ? p.W - 1 : col);
+      x[s][r] = row[(int64_t)col * p.bias.s2];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // LDS rings filled by DMA (global_load_lds) without full waits.
 //

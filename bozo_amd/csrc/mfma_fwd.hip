@@ -32,39 +32,43 @@ namespace tension {
 // used (the tau-mass backward takes its coefficients from out and mass).
 // The per-lane sum (msum, reduced over the lane groups afterwards) is used
 // otherwise.
+// The raw bias (float32) of one key block's pairs for this lane's query tq:
+// keys kb0 + 16 j + 4 g + r.  Rows past T read row T-1.  A group inside the
+// band of every valid row of the wave (a wave-uniform test; row T-1's band
+// holds it too) is one 16-byte load per lane; other pairs read their column
+// clamped into the row, so pairs off the band read some element of the row.
+// Such pairs are masked where the bias is used, and the -log2(e) factor is
+// applied there: nothing waits for these loads before the products that
+// follow them, and no lane-divergent branch surrounds them.
+__device__ __forceinline__ void fwd_bias_load(const BandParams& p, int kb0, const WaveBand& wb, int b, int tq, int g,
+                                              float (*x)[4]) {
+  const int tr = tq < p.T ? tq : p.T - 1;
+  const float* row = (const float*)p.bias.p + (int64_t)b * p.bias.s0 + (int64_t)tr * p.bias.s1;
+  const int cmax = (p.glob ? p.T : p.W) - 1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c0 = bias_col(p, tr, kb0 + 16 * j + 4 * g);
+    if (p.bias.s2 == 1 && sub_kind(wb, kb0 + 16 * j) == 2) {
+      __builtin_memcpy(x[j], row + c0, 16);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int cc = c0 + r < 0 ? 0 : (c0 + r > cmax ? cmax : c0 + r);
+        x[j][r] = row[(int64_t)cc * p.bias.s2];
+      }
+    }
+  }
+}
+
+// One key block of a query tile: S^T, P, O^T += V^T P^T (and the mass).
+// braw: the block's raw bias (fwd_bias_load) when BIAS.
 template <bool BIAS, bool TAU, bool MMA_MASS = false>
 __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, const bf16* Vs, int kb0,
                                           const WaveBand& wb, int lo, int hi, int b, int h, int tq,
                                           int g, int c, const bf16x8* qf, float k2, f32x4* acc,
-                                          float& msum, f32x4* macc = nullptr) {
+                                          float& msum, f32x4* macc, const float (*braw)[4]) {
   float pr[4][4];
   int kind[4];
-  // the block's bias, loaded ahead of its products so the loads' latency
-  // runs under them (pairs off the band read the batch's first element)
-  float b2v[BIAS ? 4 : 1][4];
-  if constexpr (BIAS) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key0 = kb0 + 16 * j + 4 * g;
-      if (hi >= lo && p.bias.s2 == 1 && sub_kind(wb, kb0 + 16 * j) == 2) {
-        // every key of the group is in the row's band: its four columns are
-        // consecutive (one 16-byte load)
-        const float* src = (const float*)p.bias.p + bias_off(p, b, tq, key0);
-        float x[4];
-        __builtin_memcpy(x, src, 16);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) b2v[j][r] = -kLog2e * x[r];
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = key0 + r;
-          const bool ok = (key >= lo) & (key <= hi);
-          const float x = ld<float>(p.bias, ok ? bias_off(p, b, tq, key) : (int64_t)b * p.bias.s0);
-          b2v[j][r] = ok ? -kLog2e * x : 0.f;
-        }
-      }
-    }
-  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     kind[j] = sub_kind(wb, kb0 + 16 * j);
@@ -82,7 +86,7 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
       // kind 2 covers every valid row of the wave; rows past T (hi < lo)
       // stay masked so no tau store or bias load leaves the tensors
       const bool ok = kind[j] == 2 ? hi >= lo : ((key >= lo) & (key <= hi));
-      const float b2 = BIAS ? b2v[j][r] : 0.f;
+      const float b2 = BIAS ? -kLog2e * braw[j][r] : 0.f;
       // computed on every lane (finite inputs) and selected: a conditional
       // sigmoid becomes a branch per element
       const float sg = sigmoid_scaled(s[r], k2, b2);
@@ -209,7 +213,7 @@ __device__ __forceinline__ void fwd_store_tau_staged(const BandParams& p, int b,
 
 // ------------------------------------------------------------------ ring kernel (W <= 64)
 
-// One query tile at W = 64 with T % 64 == 0 (no bias, no tau): the band of
+// One query tile at W = 64 with T % 64 == 0 (bias: BIAS, bx): the band of
 // wave w (queries t0 + 16w + c) is 16-key sub-blocks s = w .. w+4 of the
 // 128 keys of blocks t-1 (s < 4) and t (s >= 4).  Sub-block w keeps key
 // index kk = 4g + r >= c, sub-block w+4 keeps kk < c, the three between are
@@ -221,11 +225,12 @@ __device__ __forceinline__ void fwd_store_tau_staged(const BandParams& p, int b,
 // so that every band decision is static.  TV: the tau of the lane's pairs,
 // sub-block s5 = 0..4 of the band, as bf16 bits in tv[s5] (zero where masked
 // or absent).
-template <int w, bool TV = false>
+template <int w, bool TV = false, bool BIAS = false>
 __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb,
                                               bool has_prev, int g, int c, const bf16x8* qf, float k2,
                                               const bool* mlo, const bool* mhi, f32x4* acc, f32x4& macc,
-                                              u16x4* tv = nullptr) {
+                                              u16x4* tv = nullptr, const float (*bx)[4] = nullptr,
+                                              float bsc = 0.f) {
   const bf16x8 ones = ones_bf16x8();
 #pragma unroll
   for (int pi = 0; pi < 3; ++pi) {
@@ -256,7 +261,14 @@ __device__ __forceinline__ void fwd_tile_fast(const bf16* Ka, const bf16* Va, co
         continue;
       }
       const int row = 16 * ((2 * pr + h2) & 3) + c;
+      // BIAS: the slot's bias (band_tile_bias with jrot = w: bx[s5 & 3]) times
+      // the scale starts the accumulator, sigma(S / scale + bias) =
+      // sigma((S + scale bias) / scale)
       f32x4 z = {};
+      if constexpr (BIAS) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = bx[s5 & 3][r] * bsc;
+      }
       z = mfma(dt_row8(Kt, row, g), qf[0], z);
       z = mfma(dt_row8(Kt, row, 4 + g), qf[1], z);
 #pragma unroll
@@ -340,17 +352,23 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandArgs args) {
     // TAU: the tile's tau leaves through tv and fwd_store_tau_staged, every
     // slot included (no separate zero fill)
     u16x4 tv[5];
-    auto fast_tile = [&](int t, const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb) -> OutRow {
+    // BIAS: each tile's bias (band_tile_bias, jrot = wave): tile t_first's
+    // goes out before the next block's copies, tile t_first + 1's behind the
+    // first wait, so that the products of tile t_first run under it
+    float bias0[BIAS ? 4 : 1][4], bias1[BIAS ? 4 : 1][4];
+    const float bsc = (float)p.scale;
+    auto fast_tile = [&](int t, const bf16* Ka, const bf16* Va, const bf16* Kb, const bf16* Vb,
+                         const float (*bx)[4]) -> OutRow {
       const int tq = t * kTile + wave * 16 + c;
       f32x4 acc[4] = {}, macc = {};
       // wave priority raised over the tile's arithmetic: a workgroup that is
       // staging and storing rows issues in its gaps (0.05-0.1 us at config 2)
       __builtin_amdgcn_s_setprio(1);
       switch (wave) {
-        case 0: fwd_tile_fast<0, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
-        case 1: fwd_tile_fast<1, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
-        case 2: fwd_tile_fast<2, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
-        default: fwd_tile_fast<3, TAU>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv); break;
+        case 0: fwd_tile_fast<0, TAU, BIAS>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv, bx, bsc); break;
+        case 1: fwd_tile_fast<1, TAU, BIAS>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv, bx, bsc); break;
+        case 2: fwd_tile_fast<2, TAU, BIAS>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv, bx, bsc); break;
+        default: fwd_tile_fast<3, TAU, BIAS>(Ka, Va, Kb, Vb, t >= 1, g, c, qf, k2, mlo, mhi, acc, macc, tv, bx, bsc); break;
       }
       __builtin_amdgcn_s_setprio(0);
       return fwd_finish<NORM, false>(p, b, h, tq, g, acc, macc[0], true);
@@ -359,32 +377,39 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandArgs args) {
       load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
       fetch_any(t_first - 1, K0, V0);
       fetch_any(t_first, K1, V1);
+      if constexpr (BIAS) band_tile_bias(p, b, t_first * kTile, wave, g, c, wave, bias0);
       fetch_any(t_first + 1, K2, V2);
       load_qfrag(qb_, p.q.s1, (t_first + 1) * kTile + wave * 16 + c, T, g, qn);
       wait_vm<6>();  // block t_first + 1 (4 copies) and qn (2 loads) may be in flight
       lds_barrier();
-      const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1);
+      if constexpr (BIAS) band_tile_bias(p, b, (t_first + 1) * kTile, wave, g, c, wave, bias1);
+      const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1, bias0);
       wait_vm<0>();
       lds_barrier();  // slots K0 / V0 (block t_first - 1) are free: they stage the rows
       fwd_store_staged(p, b, h, g, c, lane, wave, o0, K0);
       if constexpr (TAU) fwd_store_tau_staged(p, b, h, g, c, lane, wave, t_first * kTile, tv, V0);
       qf[0] = qn[0];
       qf[1] = qn[1];
-      const OutRow o1 = fast_tile(t_first + 1, K1, V1, K2, V2);
+      const OutRow o1 = fast_tile(t_first + 1, K1, V1, K2, V2, bias1);
       fwd_store_staged(p, b, h, g, c, lane, wave, o1, K0);
       if constexpr (TAU) fwd_store_tau_staged(p, b, h, g, c, lane, wave, (t_first + 1) * kTile, tv, V0);
     } else {
       load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
       fetch_any(t_first - 1, K0, V0);
       fetch_any(t_first, K1, V1);
+      if constexpr (BIAS) band_tile_bias(p, b, t_first * kTile, wave, g, c, wave, bias0);
       wait_vm<0>();
       lds_barrier();
-      const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1);
+      const OutRow o0 = fast_tile(t_first, K0, V0, K1, V1, bias0);
       fwd_store_staged(p, b, h, g, c, lane, wave, o0, K2);  // slot 2 holds no block
       if constexpr (TAU) fwd_store_tau_staged(p, b, h, g, c, lane, wave, t_first * kTile, tv, V2);
     }
     return;
   }
+  // the bias of tile t_first (the generic path; band_tile_bias), then one
+  // tile ahead in each step
+  float bcur[BIAS ? 4 : 1][4], bnext[BIAS ? 4 : 1][4];
+  if constexpr (BIAS && !FAST) band_tile_bias(p, b, t_first * kTile, wave, g, c, 0, bcur);
   load_qfrag(qb_, p.q.s1, t_first * kTile + wave * 16 + c, T, g, qf);
   fetch(t_first - 1, K0, V0);
   fetch(t_first, K1, V1);
@@ -415,12 +440,20 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandArgs args) {
       if (FAST) fwd_store_staged(p, b, h, g, c, lane, wave, pend, Kn); else fwd_store(p, b, h, g, pend);
     }
     stage = Kn;
+    const int t0 = t * kTile;
+    const int tq = t0 + wave * 16 + c;
+    // the next tile's bias (after the last tile, this tile's again) goes out
+    // ahead of the next tile's copies: the wait for those at the next step
+    // covers it, and this tile's (bcur, loaded one step earlier) has nothing
+    // outstanding when its products need it
+    if constexpr (BIAS && !FAST) {
+      band_tile_bias(p, b, (more ? t + 1 : t) * kTile, wave, g, c, 0, bnext);
+      asm volatile("" ::: "memory");
+    }
     if (more && lt > 0) {
       load_qfrag(qb_, p.q.s1, (t + 1) * kTile + wave * 16 + c, T, g, qn);
       fetch(t + 1, Kn, Vn);
     }
-    const int t0 = t * kTile;
-    const int tq = t0 + wave * 16 + c;
     f32x4 acc[4] = {};
     if (FAST) {
       f32x4 macc = {};
@@ -437,12 +470,19 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd_ring(BandArgs args) {
       const WaveBand wb = wave_band(p, t0 + wave * 16);
       // rows past T hold row T-1 (finite) and are masked out entirely
       float msum = 0.f;
-      if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
-      fwd_block<BIAS, TAU>(p, Kb, Vb, t0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum);
+      // bcur serves both blocks (band_tile_bias)
+      if (t >= 1) fwd_block<BIAS, TAU>(p, Ka, Va, t0 - kTile, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum, nullptr, bcur);
+      fwd_block<BIAS, TAU>(p, Kb, Vb, t0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum, nullptr, bcur);
       pend = fwd_finish<NORM, TAU>(p, b, h, tq, g, acc, msum);
     }
     has_pend = true;
     if (more) { qf[0] = qn[0]; qf[1] = qn[1]; }
+    if constexpr (BIAS && !FAST) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bcur[j][r] = bnext[j][r];
+    }
     return true;
   };
 
@@ -502,8 +542,10 @@ __global__ __launch_bounds__(kThreads) void mfma_fwd(BandArgs args) {
     const int kb0 = kb_first + blk * kTile;
     if (blk + 1 < nblk) wait_vm<4>(); else wait_vm<0>();
     __syncthreads();
+    float braw[BIAS ? 4 : 1][4];
+    if constexpr (BIAS) fwd_bias_load(p, kb0, wb, b, tq, g, braw);
     fwd_block<BIAS, TAU, true>(p, Kb[blk & 1], Vb[blk & 1], kb0, wb, lo, hi, b, h, tq, g, c, qf, k2, acc, msum,
-                               &macc);
+                               &macc, braw);
     if (blk + 2 < nblk) {
       __syncthreads();  // every wave is done with this ring slot
       tile_async(kb_, p.k.s1, kb0 + 2 * kTile, T, Kb[blk & 1], wave, lane);
@@ -528,10 +570,10 @@ static void go(const BandParams& p, hipStream_t st, unsigned nwg, bool ring) {
                                    ((uintptr_t)tb.p & 15) == 0);
     BandArgs a;
     if (!band_args(p, &a)) return;  // the host takes the ring kernel only with 32-bit strides
-    if (!BIAS && tau_rows && p.win == kTile && p.T % kTile == 0) {
+    if (tau_rows && p.win == kTile && p.T % kTile == 0) {
       if (a.chunk > 2) a.chunk = 2;
       const unsigned nq = (unsigned)((int64_t)a.B * a.H * ((a.ntiles + a.chunk - 1) / a.chunk));
-      hipLaunchKernelGGL((mfma_fwd_ring<NORM, false, TAU, true>), dim3(nq), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((mfma_fwd_ring<NORM, BIAS, TAU, true>), dim3(nq), dim3(kThreads), 0, st, a);
       return;
     }
 #else

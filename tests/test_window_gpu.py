@@ -122,6 +122,27 @@ def test_config2_bf16_with_tau_and_dtau(dev):
     compare(hip, ref, torch.bfloat16, True)
 
 
+@pytest.mark.parametrize("B,H,T,normalize,tau", [(8, 12, 1024, None, False), (8, 12, 1024, "count", False),
+                                                  (8, 12, 1024, "mass", False), (8, 12, 1024, "mass", True),
+                                                  (1, 2, 192, "mass", False), (1, 2, 192, None, True)])
+def test_config2_geometry_bias(dev, B, H, T, normalize, tau):
+    """A [B,T,W] bias at the config-2 launch geometry (B8 H12 T1024 W64
+    bf16): the fast forward (two tiles per workgroup, the second tile's bias
+    loaded while the first computes) and the fast backward (runs of 3-4
+    tiles and a halo step, each step's bias issued ahead of the next step's
+    loads); with tau the backward takes the bias with dTau on the generic
+    path.  The small shape has one-tile workgroups and runs."""
+    D, W = 64, 64
+    chunk, runs, longest = fused_geometry(B, H, T)
+    print(f"[c2 bias] normalize={normalize} tau={tau} fwd tiles/wg={min(chunk, 2)} bwd runs={runs} "
+          f"longest={longest}", flush=True)
+    inp = make_inputs(B, T, H, D, seed=5, std=0.5, dtype=torch.bfloat16, W=W, bias_std=0.5,
+                      bias_shape=(B, T, W), dtau_std=0.1 if tau else None)
+    hip = hip_run(inp, W, 8.0, dev, normalize=normalize, return_tau=tau, use_bias=True, use_dtau=tau)
+    ref = oracle_run(inp, W, 8.0, normalize=normalize, use_bias=True, use_dtau=tau)
+    compare(hip, ref, torch.bfloat16, tau)
+
+
 @pytest.mark.parametrize("normalize", [None, "count", "mass"])
 def test_117m_geometry_tau_and_dtau(dev, normalize):
     """The kernel variants of the model's aux-loss step and of the tau
