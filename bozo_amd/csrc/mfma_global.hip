@@ -25,51 +25,53 @@
 namespace tension {
 
 // Optional operands of the global block, per (query, key) pair of one lane:
-// the pre-sigmoid bias [B, T, T] (head-agnostic) as -log2(e) * bias, and the
-// column of the down-sampled tau_local / dtau_local [B, T, H, Wl] (slot j =
-// key T-1-j, model.py:235-236), -1 when the pair has no slot there.  Rows and
-// keys past T are clamped for the bias load (those pairs are masked).
-// The host takes these kernels with a float32 bias only.
-__device__ __forceinline__ float gl_bias2(const BandParams& p, int b, int q, int k) {
-  const int qq = q < p.T ? q : p.T - 1, kk = k < p.T ? k : p.T - 1;
-  return -kLog2e * ((const float*)p.bias.p)[(int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + (int64_t)kk * p.bias.s2];
-}
-
-// The bias of query q at keys k .. k + 3 (k a multiple of 4, k + 3 < T) as
-// one 16-byte load, times -log2(e); rows past T read row T-1 (masked).  For
-// a bias with unit column stride and 16-byte aligned rows (gl_bias_rows4).
-__device__ __forceinline__ f32x4 gl_bias2x4(const BandParams& p, int b, int q, int k) {
-  const int qq = q < p.T ? q : p.T - 1;
-  const f32x4 x = *(const f32x4*)((const float*)p.bias.p + (int64_t)b * p.bias.s0 + (int64_t)qq * p.bias.s1 + k);
-  return x * -kLog2e;
-}
-
+// the pre-sigmoid bias [B, T, T] (head-agnostic; float32, host-checked), and
+// the column of the down-sampled tau_local / dtau_local [B, T, H, Wl] (slot
+// j = key T-1-j, model.py:235-236), -1 when the pair has no slot there.
 __device__ __forceinline__ bool gl_bias_rows4(const BandParams& p) {
   return p.bias.s2 == 1 && (p.bias.s1 & 3) == 0 && (p.bias.s0 & 3) == 0 && ((uintptr_t)p.bias.p & 15) == 0;
 }
 
-// A lane's bias of one key block (queries t0 + 32 qh + 16 i + c, keys
+// A lane's raw bias of one key block (queries t0 + 32 qh + 16 i + c, keys
 // blk * 64 + 32 kh + 16 j + 4 g + r): four 16-byte loads when the block lies
-// inside [0, T) and the rows allow it, else sixteen element loads.
+// inside [0, T) and the rows allow it (rows4: unit column stride, 16-byte
+// aligned rows), else sixteen element loads; rows and keys past T read T-1
+// (those pairs are masked).  Nothing is computed from the values here: the
+// callers start their score accumulators with them (times the scale), and
+// the empty asm statements keep the loads of the two forms apart (merged,
+// every address became a per-lane product).
 __device__ __forceinline__ void gl_bias_block(const BandParams& p, int b, int t0, int blk, int qh, int kh, int g,
                                               int c, bool rows4, float (*b2)[2][4]) {
+  const float* bb = (const float*)p.bias.p + b * p.bias.s0;
   const int kbase = blk * kTile + 32 * kh + 4 * g;
+  asm volatile("" ::: "memory");
   if (rows4 && (blk + 1) * kTile <= p.T) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+      const int q = t0 + 32 * qh + 16 * i + c;
+      const float* row = bb + (int64_t)(q < p.T ? q : p.T - 1) * p.bias.s1 + kbase;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const f32x4 x = gl_bias2x4(p, b, t0 + 32 * qh + 16 * i + c, kbase + 16 * j);
+        const f32x4 x = *(const f32x4*)(row + 16 * j);
 #pragma unroll
         for (int r = 0; r < 4; ++r) b2[i][j][r] = x[r];
       }
+    }
+    asm volatile("" ::: "memory");
   } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+      const int q = t0 + 32 * qh + 16 * i + c;
+      const float* row = bb + (int64_t)(q < p.T ? q : p.T - 1) * p.bias.s1;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) b2[i][j][r] = gl_bias2(p, b, t0 + 32 * qh + 16 * i + c, kbase + 16 * j + r);
+        for (int r = 0; r < 4; ++r) {
+          const int k = kbase + 16 * j + r;
+          b2[i][j][r] = row[(int64_t)(k < p.T ? k : p.T - 1) * p.bias.s2];
+        }
+    }
+    asm volatile("" ::: "memory");
   }
 }
 
@@ -182,10 +184,23 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
   }
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
+  // bias (gl_bias_block): it starts the score accumulators, sigma(S / scale
+  // + bias) = sigma((S + scale bias) / scale).  With tau_local (BPRE) block
+  // 0's goes out before the first copies, and each block loads the next
+  // one's once its score products have taken its own, ahead of that block's
+  // ring copy, so the wait for the copy before it also covers the bias, whose
+  // latency runs under the rest of the block (the last block loads its own
+  // again, unused).  Without tau_local each block loads its own at its start:
+  // the one-ahead form needs more registers there, and at two waves per SIMD
+  // instead of three it measured slower (74 -> 90 us, B4 H12 T2048 with a bias).
+  constexpr bool BPRE = BIAS && TAU;
+  const bool rows4 = BIAS && gl_bias_rows4(p);  // 16-byte bias loads
+  const float bsc = (float)p.scale;
+  float b2v[BIAS ? 2 : 1][2][4];
+  if constexpr (BPRE) gl_bias_block(p, b, t0, 0, qh, kh, g, c, rows4, b2v);
   copy(0, S0{});
   copy(1, S1{});
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
-  const bool rows4 = BIAS && gl_bias_rows4(p);  // 16-byte bias loads (gl_bias_block)
   const bf16x8 ones = ones_bf16x8();
   f32x4 acc[2][4] = {};
   f32x4 macc[2] = {};
@@ -197,11 +212,9 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
     constexpr bool diag = decltype(diag_tag)::value;
     constexpr bool TB = TAU && decltype(tau_tag)::value;
     constexpr uint32_t KO = S * kDTile * 2, VO = (2 + S) * kDTile * 2;
-    // the block's bias, loaded ahead of its products so the loads' latency
-    // runs under them
-    float b2v[BIAS ? 2 : 1][2][4];
-    if constexpr (BIAS) gl_bias_block(p, b, t0, blk, qh, kh, g, c, rows4, b2v);
-    // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c
+    if constexpr (BIAS && !BPRE) gl_bias_block(p, b, t0, blk, qh, kh, g, c, rows4, b2v);
+    // S^T = K Q^T for keys 32 kh + 16 j + (4 g + r), queries 16 i + c (plus
+    // scale times the bias)
     f32x4 s[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -210,10 +223,15 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         f32x4 z = {};
+        if constexpr (BIAS) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) z[r] = b2v[i][j][r] * bsc;
+        }
         z = mfma(a0, qf[i][0], z);
         s[i][j] = mfma(a1, qf[i][1], z);
       }
     }
+    if constexpr (BPRE) gl_bias_block(p, b, t0, blk + 1 < nblk ? blk + 1 : blk, qh, kh, g, c, rows4, b2v);
     TrRead vr[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) vr[m] = tr8_issue_at<VO>(vlo[m], vhi[m]);
@@ -227,8 +245,7 @@ __device__ __forceinline__ void gl_fwd_tile(const BandParams& p, int tile, int b
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = blk * kTile + 32 * kh + 16 * j + 4 * g + r, query = t0 + dq;
-          const float b2 = BIAS ? b2v[i][j][r] : 0.f;
-          const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
+          const float pv = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[i][j][r] * k2));
           pr[j][r] = (diag && 32 * kh + 16 * j + 4 * g + r > dq) ? 0.f : pv;
           if (TB) {
             const int col = gl_tau_col(p, query, key);
@@ -427,6 +444,14 @@ void gl_dq(BandArgs args) {
     }
   }
   const TileSrc ksrc = tile_src(kb_, p.k.s1, T, wave, lane), vsrc = tile_src(vb_, p.v.s1, T, wave, lane);
+  // bias as in the forward (gl_bias_block, one block ahead, starting the
+  // score accumulators); with a bias every block issues a ring copy (past
+  // the last block, a copy of it into the free slot), so that the bias
+  // loads have the same younger loads on every path
+  const bool rows4 = BIAS && gl_bias_rows4(p);  // 16-byte bias loads
+  const float bsc = (float)p.scale;
+  float b2v[BIAS ? 2 : 1][2][4];
+  if constexpr (BIAS) gl_bias_block(p, b, t0, 0, qh, kh, g, c, rows4, b2v);
   tile_async_src(ksrc, 0, Kb[0], wave);
   tile_async_src(vsrc, 0, Vb[0], wave);
   if (nblk > 1) {
@@ -434,7 +459,6 @@ void gl_dq(BandArgs args) {
     tile_async_src(vsrc, kTile, Vb[1], wave);
   }
   const float k2 = -kLog2e * (float)(1.0 / p.scale);
-  const bool rows4 = BIAS && gl_bias_rows4(p);  // 16-byte bias loads (gl_bias_block)
   f32x4 acc[2][4] = {};
 
   auto block = [&](int blk, auto diag_tag, auto tau_tag) __attribute__((always_inline)) {
@@ -442,9 +466,6 @@ void gl_dq(BandArgs args) {
     constexpr bool TB = DTAU && decltype(tau_tag)::value;  // the block holds dtau_local columns
     const bf16* Ks = Kb[blk & 1];
     const bf16* Vs = Vb[blk & 1];
-    // the block's bias, loaded ahead of its products
-    float b2v[BIAS ? 2 : 1][2][4];
-    if constexpr (BIAS) gl_bias_block(p, b, t0, blk, qh, kh, g, c, rows4, b2v);
     f32x4 s[2][2], dp[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -454,6 +475,10 @@ void gl_dq(BandArgs args) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         f32x4 z = {};
+        if constexpr (BIAS) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) z[r] = b2v[i][j][r] * bsc;
+        }
         z = mfma(k0, qf[i][0], z);
         s[i][j] = mfma(k1, qf[i][1], z);
         f32x4 y = {};
@@ -461,6 +486,7 @@ void gl_dq(BandArgs args) {
         dp[i][j] = mfma(v1, gf[i][1], y);
       }
     }
+    if constexpr (BIAS) gl_bias_block(p, b, t0, blk + 1 < nblk ? blk + 1 : blk, qh, kh, g, c, rows4, b2v);
     TrRead kr[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) kr[m] = dt_tr8_issue(Ks, m, 32 * kh, g, c);
@@ -474,8 +500,7 @@ void gl_dq(BandArgs args) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = blk * kTile + 32 * kh + 16 * j + 4 * g + r, query = t0 + dq;
-          const float b2 = BIAS ? b2v[i][j][r] : 0.f;
-          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(fmaf(s[i][j][r], k2, b2)));
+          const float x = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s[i][j][r] * k2));
           float dt = dp[i][j][r] * ca[i] - cc[i];
           if (TB) {
             const int col = gl_tau_col(p, query, key);
@@ -507,15 +532,19 @@ void gl_dq(BandArgs args) {
     wait_vm<4>();
     lds_barrier();
     visit(blk, std::false_type{});
-    if (blk + 2 < nblk) {
+    if (BIAS || blk + 2 < nblk) {
+      const int nb = blk + 2 < nblk ? blk + 2 : nblk - 1;
       lds_barrier();
-      tile_async_src(ksrc, (blk + 2) * kTile, Kb[blk & 1], wave);
-      tile_async_src(vsrc, (blk + 2) * kTile, Vb[blk & 1], wave);
+      tile_async_src(ksrc, nb * kTile, Kb[blk & 1], wave);
+      tile_async_src(vsrc, nb * kTile, Vb[blk & 1], wave);
     }
   }
-  wait_vm<0>();
+  // with a bias and nblk > 1 the last copy (of block nblk - 1 again, into
+  // the other slot) may stay in flight until the merge below
+  if (BIAS && nblk > 1) wait_vm<4>(); else wait_vm<0>();
   lds_barrier();
   visit(nblk - 1, std::true_type{});
+  if constexpr (BIAS) wait_vm<0>();  // the merge reuses the ring's LDS
 
   // key halves meet (as in the forward): 16 floats per lane
   __syncthreads();
