@@ -21,15 +21,16 @@ int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hi
   if (nwg <= 0) return -1;
   if (nwg > 0x7fffffff) return kGridTooLarge;
   // p.chunk > 0: runs of consecutive tiles per workgroup (p.chunk runs per
-  // (b, h)) for the backward kernels of a local window W <= 64, sized for
-  // about two resident workgroups per CU: dK / dV always, dQ for float32
-  // Q / K at head dim 32 without dTau (where its run kernel measured
-  // faster); 0: one tile per workgroup
+  // (b, h)) for a local window W <= 64: the forward, sized for about three
+  // resident workgroups per CU, and the backward kernels for about two: dK /
+  // dV always, dQ for float32 Q / K at head dim 32 without dTau (where its
+  // run kernel measured faster); 0: one tile per workgroup
   p.chunk = 0;
   const bool dq_runs = f32 && p.D == 32 && p.dtau.p == nullptr;
-  if ((phase == 2 || (phase == 1 && dq_runs)) && !p.glob && p.win >= 1 && p.win <= 64) {
+  if ((phase == 0 || phase == 2 || (phase == 1 && dq_runs)) && !p.glob && p.win >= 1 && p.win <= 64) {
     const int64_t bh = (int64_t)p.B * p.H;
-    int64_t runs = (2 * (int64_t)device_cus() + bh / 2) / bh;
+    const int64_t per_cu = phase == 0 ? 3 : 2;
+    int64_t runs = (per_cu * (int64_t)device_cus() + bh / 2) / bh;
     if (runs < 1) runs = 1;
     if (runs < p.ntiles) {
       p.chunk = (int)runs;

@@ -377,46 +377,54 @@ __device__ __forceinline__ void dtau_rows_put(E* st, const E* v, int lane) {
 
 // ----------------------------------------------------------------- forward
 
+// One 64-query tile's lane state in the forward kernels: the lane's query
+// row as B operands (Q as NT terms), its band, its O^T accumulators and
+// tau mass, its rows of tau (dtype of Q, host-checked) and of the bias
+// (float32, unit column stride); rows past T are never written.
 template <int NT, int D, int NORM, bool BIAS, bool TAU>
-__global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
-  touch_args(args);
-  const BandParams p = band_params(args);
-  constexpr int NBUF = NT == 1 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
-  __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, c = lane & 15;
-  const TileId id = tile_id(p, p.glob != 0);
-  const int b = id.b, h = id.h, T = p.T;
-  const int t0 = id.tile * kTile;
-  const int tq = t0 + wave * 16 + c;
-  const int lo = tq - p.win > 0 ? tq - p.win : 0;
-  const int hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
-  const WaveBand wb = wave_band(p, t0 + wave * 16);
-  const Blocks bl = band_blocks(p, t0);
-
+struct FwdTile {
   using E = Elem<NT>;
-  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
-  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  int b, h, g, c, lane, wave, t0, tq, lo, hi;
+  WaveBand wb;
+  float k2, msum;
   bf16x8 qf[D / 32][NT];
-#pragma unroll
-  for (int ch = 0; ch < D / 32; ++ch) frag_row<NT>(qb_, p.q.s1, tq, T, 4 * ch + g, qf[ch]);
-
-  const float k2 = -kLog2e * (float)(1.0 / p.scale);
-  // this lane's query row of tau (dtype of Q, host-checked) and of the bias
-  // (float32, unit column stride); rows past T are never touched
-  const int tr = tq < T ? tq : T - 1;
-  E* const tbh = TAU ? (E*)p.tau.p + b * p.tau.s0 + h * p.tau.s2 : nullptr;  // tau of this (b, h)
-  E* const trow = TAU ? tbh + (int64_t)tr * p.tau.s1 : nullptr;
-  E* const tst = tstage + (TAU ? wave * kStageRows : 0);
-  const float* const brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
   f32x4 acc[D / 16];
+  E* tbh;  // tau of this (b, h)
+  E* trow;
+  E* tst;  // this wave's tau staging rows
+  const float* brow;
+
+  __device__ __forceinline__ void init(const BandParams& p, int b_, int h_, int lane_, int wave_, E* tstage) {
+    b = b_;
+    h = h_;
+    lane = lane_;
+    wave = wave_;
+    g = lane >> 4;
+    c = lane & 15;
+    k2 = -kLog2e * (float)(1.0 / p.scale);
+    tbh = TAU ? (E*)p.tau.p + b * p.tau.s0 + h * p.tau.s2 : nullptr;
+    tst = tstage + (TAU ? wave * kStageRows : 0);
+  }
+
+  // the tile at t0_: band, tau and bias rows, cleared sums (the query
+  // fragments are set apart)
+  __device__ __forceinline__ void at(const BandParams& p, int t0_) {
+    const int T = p.T;
+    t0 = t0_;
+    tq = t0 + wave * 16 + c;
+    lo = tq - p.win > 0 ? tq - p.win : 0;
+    hi = tq < T ? tq - 1 + p.diag : -1;  // hi < lo: no key for this row
+    wb = wave_band(p, t0 + wave * 16);
+    const int tr = tq < T ? tq : T - 1;
+    trow = TAU ? tbh + (int64_t)tr * p.tau.s1 : nullptr;
+    brow = BIAS ? (const float*)p.bias.p + b * p.bias.s0 + (int64_t)tr * p.bias.s1 : nullptr;
 #pragma unroll
-  for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float msum = 0.f;
-  stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, [&](const bf16* kt, int kb0) {
+    for (int m = 0; m < D / 16; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    msum = 0.f;
+  }
+
+  // one key block (tiles K_0 .. K_{NT-1}, V at kt; first key kb0)
+  __device__ __forceinline__ void visit(const BandParams& p, const bf16* kt, int kb0) {
     float pr[4][4];
     int kind[4];
     float b2v[BIAS ? 4 : 1][4];
@@ -442,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
     }
     // whole row segments out (keys outside each row's band are not stored;
     // a global block holds tau_local keys only from T - Wtau on)
-    if (TAU && !(p.glob && kb0 + kTile <= T - p.Wtau)) {
+    if (TAU && !(p.glob && kb0 + kTile <= p.T - p.Wtau)) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) stage_put4(tst, c, j, g, pr[j]);
       tau_rows_store(p, tbh, tst, t0 + wave * 16, kb0, lane);
@@ -460,15 +468,113 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
         acc[m] = mmx<1, NT, 2>(&va, ps, acc[m]);
       }
     }
-  });
-  msum = wave_sum_g(msum);
-  if (tq >= T) return;
-  store_acc<E, D>((E*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2, acc,
-                  out_factor<NORM>(msum, tq, p.W), g);
-  if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, msum);
-  if (TAU) {
-    const int e = tau_empty_bound(p, tq);
-    for (int col = g; col < e; col += 4) trow[col] = (E)0.f;
+  }
+
+  // the tile's output rows, mass and empty tau slots
+  __device__ __forceinline__ void finish(const BandParams& p) {
+    msum = wave_sum_g(msum);
+    if (tq >= p.T) return;
+    store_acc<E, D>((E*)p.out.p + b * p.out.s0 + (int64_t)tq * p.out.s1 + h * p.out.s2, acc,
+                    out_factor<NORM>(msum, tq, p.W), g);
+    if (p.mass.p && g == 0) st<float>(p.mass, b * p.mass.s0 + (int64_t)tq * p.mass.s1 + h * p.mass.s2, msum);
+    if (TAU) {
+      const int e = tau_empty_bound(p, tq);
+      for (int col = g; col < e; col += 4) trow[col] = (E)0.f;
+    }
+  }
+};
+
+template <int NT, int D, int NORM, bool BIAS, bool TAU>
+__global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
+  constexpr int NBUF = NT == 1 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const TileId id = tile_id(p, p.glob != 0);
+  const int T = p.T;
+  FwdTile<NT, D, NORM, BIAS, TAU> st;
+  st.init(p, id.b, id.h, lane, wave, tstage);
+  st.at(p, id.tile * kTile);
+  const Blocks bl = band_blocks(p, st.t0);
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + st.b * p.q.s0 + st.h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + st.b * p.k.s0 + st.h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + st.b * p.v.s0 + st.h * p.v.s2;
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) frag_row<NT>(qb_, p.q.s1, st.tq, T, 4 * ch + st.g, st.qf[ch]);
+  stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid,
+                           [&](const bf16* kt, int kb0) { st.visit(p, kt, kb0); });
+  st.finish(p);
+}
+
+// Runs of query tiles for local windows W <= 64, where tile t's band is key
+// blocks t-1 and t: a workgroup owns tiles [tA, tB) of one (b, h) (p.chunk
+// runs per (b, h)) and keeps one key block in LDS -- block t, which tile t
+// visits last, is the block tile t + 1 visits first -- loading block t + 1
+// into registers while tile t + 1 visits block t, and tile t + 1's query
+// rows while tile t visits block t.  Per tile one block staged instead of
+// two, and about three workgroups per CU in one round.
+template <int NT, int D, int NORM, bool BIAS, bool TAU>
+__global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
+  touch_args(args);
+  const BandParams p = band_params(args);
+  __shared__ __attribute__((aligned(16))) bf16 lds[(NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nr = p.chunk;
+  const int id = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
+  const int bh = id / nr, run = id % nr;
+  const int b = bh / p.H, h = bh % p.H, T = p.T;
+  const int tA = run_bound(run, p.ntiles, nr);
+  const int tB = run_bound(run + 1, p.ntiles, nr);
+  if (tA >= tB) return;
+
+  using E = Elem<NT>;
+  const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
+  const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
+  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  FwdTile<NT, D, NORM, BIAS, TAU> st;
+  st.init(p, b, h, lane, wave, tstage);
+  st.at(p, tA * kTile);
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) frag_row<NT>(qb_, p.q.s1, st.tq, T, 4 * ch + st.g, st.qf[ch]);
+  // the first block in LDS: block tA - 1 (block 0 for tA = 0, which tile 0
+  // visits as its only block)
+  {
+    const int r0 = (tA > 0 ? tA - 1 : 0) * kTile;
+    store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, r0, T, tid), lds, tid);
+    store_raw<1>(load_raw<1, D>(vb_, p.v.s1, r0, T, tid), lds + NT * kDTile, tid);
+  }
+  __syncthreads();
+  for (int t = tA; t < tB; ++t) {
+    if (t >= 1) {  // block t - 1, in LDS, while block t arrives
+      const Raw<NT> kn = load_raw<NT, D>(kb_, p.k.s1, t * kTile, T, tid);
+      const Raw<1> vn = load_raw<1, D>(vb_, p.v.s1, t * kTile, T, tid);
+      st.visit(p, lds, (t - 1) * kTile);
+      __syncthreads();  // every wave is done with block t - 1
+      store_raw<NT>(kn, lds, tid);
+      store_raw<1>(vn, lds + NT * kDTile, tid);
+      __syncthreads();
+    }
+    // block t, while tile t + 1's query rows arrive
+    const bool more = t + 1 < tB;
+    RawFrag<NT> qn[D / 32];
+    if (more) {
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) qn[ch] = frag_load<NT>(qb_, p.q.s1, st.tq + kTile, T, 4 * ch + st.g);
+    }
+    st.visit(p, lds, t * kTile);
+    st.finish(p);
+    if (more) {
+      st.at(p, (t + 1) * kTile);
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) frag_terms<NT>(qn[ch], st.qf[ch]);
+    }
   }
 }
 
@@ -1254,7 +1360,8 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
   } while (0)
   if constexpr (PHASE == 0) {
     const bool opt = p.tau.p != nullptr;
-    XB_BT(xb_fwd);
+    if (p.chunk > 0) XB_BT(xb_fwd_run);
+    else XB_BT(xb_fwd);
   } else if constexpr (PHASE == 1) {
     const bool opt = p.dtau.p != nullptr;
     // runs of tiles (a local window W <= 64): float32 Q / K at head dim 32
