@@ -1,27 +1,10 @@
-// Instantiates the exact band kernels for accumulator float and phase dkv.
+// The exact band kernel of phase dkv with accumulator float (exact_launch).
 #include "exact_impl.h"
 
 namespace tension {
 
-template <int D>
-static void launch_d(const BandParams& p, hipStream_t st, unsigned grid) {
-  hipLaunchKernelGGL((exact_bwd_dkv<float, D>), dim3(grid), dim3(128), 0, st, p);
-}
-
 int launch_exact_dkv_f32(const BandParams& p, hipStream_t st, hipError_t* err) {
-  const int64_t total = (int64_t)p.B * p.H * p.T;
-  if ((total + 127) / 128 > 0x7fffffff) return kGridTooLarge;
-  const unsigned grid = (unsigned)((total + 127) / 128);
-  switch (p.D) {
-    case 8: launch_d<8>(p, st, grid); break;
-    case 16: launch_d<16>(p, st, grid); break;
-    case 32: launch_d<32>(p, st, grid); break;
-    case 64: launch_d<64>(p, st, grid); break;
-    case 128: launch_d<128>(p, st, grid); break;
-    default: return -1;
-  }
-  *err = hipGetLastError();
-  return 0;
+  return exact_launch<float, 2>(p, st, err);
 }
 
 }  // namespace tension

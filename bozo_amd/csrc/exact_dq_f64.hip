@@ -1,27 +1,10 @@
-// Instantiates the exact band kernels for accumulator double and phase dq.
+// The exact band kernel of phase dq with accumulator double (exact_launch).
 #include "exact_impl.h"
 
 namespace tension {
 
-template <int D>
-static void launch_d(const BandParams& p, hipStream_t st, unsigned grid) {
-  hipLaunchKernelGGL((exact_bwd_dq<double, D>), dim3(grid), dim3(128), 0, st, p);
-}
-
 int launch_exact_dq_f64(const BandParams& p, hipStream_t st, hipError_t* err) {
-  const int64_t total = (int64_t)p.B * p.H * p.T;
-  if ((total + 127) / 128 > 0x7fffffff) return kGridTooLarge;
-  const unsigned grid = (unsigned)((total + 127) / 128);
-  switch (p.D) {
-    case 8: launch_d<8>(p, st, grid); break;
-    case 16: launch_d<16>(p, st, grid); break;
-    case 32: launch_d<32>(p, st, grid); break;
-    case 64: launch_d<64>(p, st, grid); break;
-    case 128: launch_d<128>(p, st, grid); break;
-    default: return -1;
-  }
-  *err = hipGetLastError();
-  return 0;
+  return exact_launch<double, 1>(p, st, err);
 }
 
 }  // namespace tension

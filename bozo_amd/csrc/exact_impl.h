@@ -273,4 +273,32 @@ __global__ __launch_bounds__(128) void exact_bwd_dkv(BandParams p) {
   }
 }
 
+// Host launch of the exact kernel of PHASE (0 fwd, 1 dQ, 2 dK / dV) with
+// accumulator A: one thread per (b, h, row), 128 per workgroup, head dims
+// 8 .. 128.  Each (phase, accumulator) pair is instantiated in a unit of its
+// own (exact_<phase>_<acc>.hip), so the six compile in parallel.
+template <typename A, int PHASE, int D>
+void exact_launch_d(const BandParams& p, hipStream_t st, unsigned grid) {
+  if constexpr (PHASE == 0) hipLaunchKernelGGL((exact_fwd<A, D>), dim3(grid), dim3(128), 0, st, p);
+  else if constexpr (PHASE == 1) hipLaunchKernelGGL((exact_bwd_dq<A, D>), dim3(grid), dim3(128), 0, st, p);
+  else hipLaunchKernelGGL((exact_bwd_dkv<A, D>), dim3(grid), dim3(128), 0, st, p);
+}
+
+template <typename A, int PHASE>
+int exact_launch(const BandParams& p, hipStream_t st, hipError_t* err) {
+  const int64_t total = (int64_t)p.B * p.H * p.T;
+  if ((total + 127) / 128 > 0x7fffffff) return kGridTooLarge;
+  const unsigned grid = (unsigned)((total + 127) / 128);
+  switch (p.D) {
+    case 8: exact_launch_d<A, PHASE, 8>(p, st, grid); break;
+    case 16: exact_launch_d<A, PHASE, 16>(p, st, grid); break;
+    case 32: exact_launch_d<A, PHASE, 32>(p, st, grid); break;
+    case 64: exact_launch_d<A, PHASE, 64>(p, st, grid); break;
+    case 128: exact_launch_d<A, PHASE, 128>(p, st, grid); break;
+    default: return -1;
+  }
+  *err = hipGetLastError();
+  return 0;
+}
+
 }  // namespace tension

@@ -326,11 +326,12 @@ __device__ __forceinline__ int band_tau_col(const BandParams& p, int t, int key)
   return tau_col(p, t, key);
 }
 
-// The pre-sigmoid bias of a lane's 16 pairs of one key block (query tq, row
-// `brow` of the bias; keys kb0 + 16 j + 4 g + r) times -log2(e), zero off
-// the band [lo, hi]: loaded together ahead of the block's products, so the
-// loads' latency runs under them (a pair off the band reads the row's first
-// element).
+// The raw pre-sigmoid bias of a lane's 16 pairs of one key block (query tq,
+// row `brow` of the bias; keys kb0 + 16 j + 4 g + r): loaded together ahead
+// of the block's products, so the loads' latency runs under them (a pair off
+// the band [lo, hi] reads the row's first element and is masked where the
+// bias is used).  The -log2(e) factor is applied at the use: nothing waits
+// for the loads right behind them.
 __device__ __forceinline__ void bias_block(const BandParams& p, const float* brow, int tq, int kb0, int g, int lo,
                                            int hi, float (*b2)[4]) {
 #pragma unroll
@@ -339,8 +340,7 @@ __device__ __forceinline__ void bias_block(const BandParams& p, const float* bro
     for (int r = 0; r < 4; ++r) {
       const int key = kb0 + 16 * j + 4 * g + r;
       const bool ok = (key >= lo) & (key <= hi);
-      const float x = brow[ok ? bias_col(p, tq, key) : 0];
-      b2[j][r] = ok ? -kLog2e * x : 0.f;
+      b2[j][r] = brow[ok ? bias_col(p, tq, key) : 0];
     }
 }
 
@@ -393,6 +393,7 @@ struct FwdTile {
   E* trow;
   E* tst;  // this wave's tau staging rows
   const float* brow;
+  float braw[BIAS ? 4 : 1][4];  // the raw bias of the block being visited
 
   __device__ __forceinline__ void init(const BandParams& p, int b_, int h_, int lane_, int wave_, E* tstage) {
     b = b_;
@@ -423,12 +424,18 @@ struct FwdTile {
     msum = 0.f;
   }
 
-  // one key block (tiles K_0 .. K_{NT-1}, V at kt; first key kb0)
+  // the raw bias of key block kb0 (nothing without a bias)
+  __device__ __forceinline__ void bias_load(const BandParams& p, int kb0) {
+    if constexpr (BIAS) bias_block(p, brow, tq, kb0, g, lo, hi, braw);
+  }
+
+  // one key block (tiles K_0 .. K_{NT-1}, V at kt; first key kb0); LOADED:
+  // its bias is in braw already (bias_load), else it is loaded here
+  template <bool LOADED = false>
   __device__ __forceinline__ void visit(const BandParams& p, const bf16* kt, int kb0) {
     float pr[4][4];
     int kind[4];
-    float b2v[BIAS ? 4 : 1][4];
-    if constexpr (BIAS) bias_block(p, brow, tq, kb0, g, lo, hi, b2v);
+    if constexpr (!LOADED) bias_load(p, kb0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       kind[j] = sub_kind(wb, kb0 + 16 * j);
@@ -442,7 +449,7 @@ struct FwdTile {
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = (key >= lo) & (key <= hi);
-        const float b2 = BIAS ? b2v[j][r] : 0.f;
+        const float b2 = BIAS ? -kLog2e * braw[j][r] : 0.f;
         const float pv = ok ? sigmoid_scaled(sc[r], k2, b2) : 0.f;
         msum += pv;
         pr[j][r] = pv;
@@ -551,11 +558,19 @@ __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
     store_raw<1>(load_raw<1, D>(vb_, p.v.s1, r0, T, tid), lds + NT * kDTile, tid);
   }
   __syncthreads();
+  // With a bias, each visit's bias loads go out ahead of the loads issued
+  // for what comes next (block t, tile t + 1's rows), which every tile then
+  // issues (the last its own rows again, unused), so that the wait for the
+  // bias does not include them.
   for (int t = tA; t < tB; ++t) {
     if (t >= 1) {  // block t - 1, in LDS, while block t arrives
+      if constexpr (BIAS) {
+        st.bias_load(p, (t - 1) * kTile);
+        asm volatile("" ::: "memory");
+      }
       const Raw<NT> kn = load_raw<NT, D>(kb_, p.k.s1, t * kTile, T, tid);
       const Raw<1> vn = load_raw<1, D>(vb_, p.v.s1, t * kTile, T, tid);
-      st.visit(p, lds, (t - 1) * kTile);
+      st.template visit<BIAS>(p, lds, (t - 1) * kTile);
       __syncthreads();  // every wave is done with block t - 1
       store_raw<NT>(kn, lds, tid);
       store_raw<1>(vn, lds + NT * kDTile, tid);
@@ -563,12 +578,18 @@ __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
     }
     // block t, while tile t + 1's query rows arrive
     const bool more = t + 1 < tB;
-    RawFrag<NT> qn[D / 32];
-    if (more) {
-#pragma unroll
-      for (int ch = 0; ch < D / 32; ++ch) qn[ch] = frag_load<NT>(qb_, p.q.s1, st.tq + kTile, T, 4 * ch + st.g);
+    if constexpr (BIAS) {
+      st.bias_load(p, t * kTile);
+      asm volatile("" ::: "memory");
     }
-    st.visit(p, lds, t * kTile);
+    RawFrag<NT> qn[D / 32];
+    if (more || BIAS) {
+      const int tq1 = BIAS && !more ? st.tq : st.tq + kTile;
+#pragma unroll
+      for (int ch = 0; ch < D / 32; ++ch) qn[ch] = frag_load<NT>(qb_, p.q.s1, tq1, T, 4 * ch + st.g);
+      if constexpr (BIAS) asm volatile("" ::: "memory");
+    }
+    st.template visit<BIAS>(p, lds, t * kTile);
     st.finish(p);
     if (more) {
       st.at(p, (t + 1) * kTile);
@@ -651,9 +672,9 @@ struct DqTile {
     }
   }
 
-  // tau (masked) of one element; b2: its bias_block value
+  // tau (masked) of one element; b2: its raw bias_block value
   __device__ __forceinline__ float tau_of(float s, float b2, bool ok) const {
-    return ok ? sigmoid_scaled(s, k2, BIAS ? b2 : 0.f) : 0.f;
+    return ok ? sigmoid_scaled(s, k2, BIAS ? -kLog2e * b2 : 0.f) : 0.f;
   }
 
   // bias_block of key block kb0 for this lane (nothing without a bias)
@@ -1119,8 +1140,7 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
       for (int r = 0; r < 4; ++r) {
         const int t = q0 + 16 * j + 4 * g + r;
         const bool ok = t >= kt.qlo && t <= kt.qhi;
-        const float x = bb[ok ? (int64_t)t * p.bias.s1 + bias_col(p, t, kt.tk) : 0];
-        b2v[j][r] = ok ? -kLog2e * x : 0.f;
+        b2v[j][r] = bb[ok ? (int64_t)t * p.bias.s1 + bias_col(p, t, kt.tk) : 0];  // raw; masked below
       }
   }
   if constexpr (DTAU) {
@@ -1162,7 +1182,7 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
       const int ql = 16 * j + 4 * g + r;  // query - q0
       const int t = q0 + ql;
       const bool ok = t >= kt.qlo && t <= kt.qhi;
-      const float pv = sigmoid_scaled(sv[r], k2, BIAS ? b2v[j][r] : 0.f);
+      const float pv = sigmoid_scaled(sv[r], k2, BIAS ? -kLog2e * b2v[j][r] : 0.f);
       const float a = sa_[ql];
       float dt = fmaf(dp[r], a, -scf_[ql]);
       if constexpr (DTAU) dt += dtv[j][r];
