@@ -450,7 +450,11 @@ struct FwdTile {
         const int key = kb0 + 16 * j + 4 * g + r;
         const bool ok = (key >= lo) & (key <= hi);
         const float b2 = BIAS ? -kLog2e * braw[j][r] : 0.f;
-        const float pv = ok ? sigmoid_scaled(sc[r], k2, b2) : 0.f;
+        // computed on every lane and selected (the bias of a pair off the
+        // band is some element of the row, finite): written as a
+        // conditional, the sigmoid with a bias became a branch per element
+        const float sg = sigmoid_scaled(sc[r], k2, b2);
+        const float pv = ok ? sg : 0.f;
         msum += pv;
         pr[j][r] = pv;
       }
