@@ -335,14 +335,6 @@ void mfma_bwd_fused(BandArgs args) {
     // t; at t = 1 block 0 is stored again over itself)
     const int bn = desc ? (t >= 2 ? t - 2 : 0) : t + 1;
     // ---- prefetch of step t+1 into registers
-    // dTau rows of this step, loaded during the previous step's phase 2
-    // (the previous phase 2 has finished reading the exchange tiles)
-    if (FDT && t != t0) {
-      dt_stage(dnext);
-      // the writes stay here: sunk into phase 1 they would keep dnext's
-      // registers live where the register file is full
-      asm volatile("" ::: "memory");
-    }
     // the step's bias (band_tile_bias, groups in slot order: j = (w + sl) & 3)
     // goes out ahead of the next step's loads, and with a bias every step
     // issues those (the last step its own rows again, unused): on every path
@@ -643,16 +635,6 @@ void mfma_bwd_fused(BandArgs args) {
         }
       }
     }
-    if (own_done) {
-      const uint32_t tk = (uint32_t)((desc ? t : t - 1) * kTile + 16 * w + c);
-      STORE_ROWS(sdk, tk, dk_old, inv_scale);
-      STORE_ROWS(sdv, tk, dv_old, 1.f);
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      dk_old[m] = dk_new[m];
-      dv_old[m] = dv_new[m];
-    }
     __syncthreads();  // phase 2 is done with X and the Q/dO tiles
 
     if (more) {
@@ -665,6 +647,27 @@ void mfma_bwd_fused(BandArgs args) {
       qf[1] = dt_row8(Qt, 16 * w + c, 4 + g);
       gf[0] = dt_row8(Ot, 16 * w + c, g);
       gf[1] = dt_row8(Ot, 16 * w + c, 4 + g);
+      // the next step's dTau rows (loaded during phase 2) into this wave's G
+      // exchange sub-tiles, which phase 2 has finished reading; here, ahead
+      // of the stores below, their wait does not include the stores
+      if constexpr (FDT) {
+        dt_stage(dnext);
+        asm volatile("" ::: "memory");
+      }
+    }
+    // the completed block's rows go out only now: on gfx9 stores count in
+    // vmcnt, and issued before the next tile's rows were waited for above
+    // (a store on some paths only, so the wait takes the stricter count)
+    // they made every step wait for its stores' completion
+    if (own_done) {
+      const uint32_t tk = (uint32_t)((desc ? t : t - 1) * kTile + 16 * w + c);
+      STORE_ROWS(sdk, tk, dk_old, inv_scale);
+      STORE_ROWS(sdv, tk, dv_old, 1.f);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      dk_old[m] = dk_new[m];
+      dv_old[m] = dv_new[m];
     }
   }
   // ascending, the last block of the sequence has no halo step: it is
