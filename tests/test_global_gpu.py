@@ -59,6 +59,22 @@ def test_global_bf16_bias_tau_local(dev, use_bias, use_tl):
     check(hip, ref, torch.bfloat16, use_tl)
 
 
+@pytest.mark.parametrize("B,H,T,wl", [(2, 4, 200, None), (2, 4, 200, 16), (1, 8, 130, 64), (2, 4, 64, None),
+                                      (1, 8, 64, 16), (3, 1, 129, None)])
+def test_global_bf16_bias_xcd_groups(dev, B, H, T, wl):
+    """A bias with B * H a multiple of 8 (the heads of a sequence grouped on
+    XCDs, gl_slot) and not (3 x 1), ragged and whole tiles, one query tile
+    (T = 64: the dQ kernel's single block), and with tau_local (the forward
+    loading the next block's bias behind its score products)."""
+    D = 64
+    inp = make_inputs(B, T, H, D, seed=B * 1000 + T, std=0.5, dtype=torch.bfloat16, W=wl or 1,
+                      dtau_std=0.1 if wl else None, bias_std=0.5, bias_shape=(B, T, T))
+    print(f"[global bias] B{B} H{H} T{T} W_local={wl}", flush=True)
+    hip = hip_run(inp, 8.0, dev, W_local=wl, use_bias=True, use_dtl=wl is not None)
+    ref = oracle_run(inp, 8.0, W_local=wl, use_bias=True, use_dtl=wl is not None)
+    check(hip, ref, torch.bfloat16, wl is not None)
+
+
 @pytest.mark.parametrize("pad", [1, 4])
 def test_global_bf16_bias_row_views(dev, pad):
     """The bias as a view into wider rows (row stride T + pad): with pad 4
