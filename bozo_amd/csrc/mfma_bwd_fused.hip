@@ -69,7 +69,7 @@ namespace tension {
 #define TENSION_BWD_ALTERNATE 1
 #endif
 
-// FAST (W = 64, T a multiple of 64; a bias or dTau in bf16 rows): the band of every
+// FAST (W = 64, T a multiple of 64; a bias, or else dTau in bf16 rows): the band of every
 // 16-query group is the same five key groups -- slot 0 the old block's
 // diagonal group (key >= query - 64, i.e. 4g + r >= c within the group),
 // slots 1..3 entirely valid, slot 4 the new block's diagonal group (key <=

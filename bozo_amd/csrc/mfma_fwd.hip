@@ -26,12 +26,6 @@
 
 namespace tension {
 
-// MMA_MASS: the tau mass comes from the P.V product itself -- one more MFMA
-// per 32 keys with an all-ones A operand sums the bf16-rounded P that the
-// output is built from, so out = msg / mass holds exactly for the weights
-// used (the tau-mass backward takes its coefficients from out and mass).
-// The per-lane sum (msum, reduced over the lane groups afterwards) is used
-// otherwise.
 // The raw bias (float32) of one key block's pairs for this lane's query tq:
 // keys kb0 + 16 j + 4 g + r.  Rows past T read row T-1.  A group inside the
 // band of every valid row of the wave (a wave-uniform test; row T-1's band
@@ -62,6 +56,12 @@ __device__ __forceinline__ void fwd_bias_load(const BandParams& p, int kb0, cons
 
 // One key block of a query tile: S^T, P, O^T += V^T P^T (and the mass).
 // braw: the block's raw bias (fwd_bias_load) when BIAS.
+// MMA_MASS: the tau mass comes from the P.V product itself -- one more MFMA
+// per 32 keys with an all-ones A operand sums the bf16-rounded P that the
+// output is built from, so out = msg / mass holds exactly for the weights
+// used (the tau-mass backward takes its coefficients from out and mass).
+// The per-lane sum (msum, reduced over the lane groups afterwards) is used
+// otherwise.
 template <bool BIAS, bool TAU, bool MMA_MASS = false>
 __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, const bf16* Vs, int kb0,
                                           const WaveBand& wb, int lo, int hi, int b, int h, int tq,
@@ -84,7 +84,7 @@ __device__ __forceinline__ void fwd_block(const BandParams& p, const bf16* Ks, c
     for (int r = 0; r < 4; ++r) {
       const int key = kb0 + 16 * j + 4 * g + r;
       // kind 2 covers every valid row of the wave; rows past T (hi < lo)
-      // stay masked so no tau store or bias load leaves the tensors
+      // stay masked so no tau store leaves the tensors
       const bool ok = kind[j] == 2 ? hi >= lo : ((key >= lo) & (key <= hi));
       const float b2 = BIAS ? -kLog2e * braw[j][r] : 0.f;
       // computed on every lane (finite inputs) and selected: a conditional
