@@ -130,31 +130,41 @@ bool aligned_f32_rows(const tension_buf* b) {
 }
 
 // Split-operand MFMA kernels (split_band.h), head dim 32 or 64, any window,
-// local or global: float32 Q / K with a bfloat16 V -- the reference's
-// autocast flow, float32 out / dOut / dQ / dK, bf16 dV -- on three bf16
-// terms per float32 value (SPLIT_F32), or bf16 everywhere (SPLIT_BF16) for
-// what the dedicated bf16 kernels (head dim 64) do not take.
-enum { SPLIT_NONE = 0, SPLIT_BF16 = 1, SPLIT_F32 = 2 };
+// local or global, every float32 value carried as three bf16 terms:
+// float32 Q / K with a bfloat16 V -- the reference's autocast flow,
+// float32 out / dOut / dQ / dK, bf16 dV -- (SPLIT_F32), float32 throughout
+// (SPLIT_F32V), or bf16 everywhere (SPLIT_BF16) for what the dedicated
+// bf16 kernels (head dim 64) do not take.
+enum { SPLIT_NONE = 0, SPLIT_BF16 = 1, SPLIT_F32 = 2, SPLIT_F32V = 3 };
 
 int split_kind(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* bias,
                int64_t D, int flags) {
   if ((flags & TENSION_FORCE_EXACT) || (D != 32 && D != 64)) return SPLIT_NONE;
-  if (!aligned_bf16_rows(v) || (bias && bias->dtype != TENSION_F32)) return SPLIT_NONE;
-  if (aligned_f32_rows(q) && aligned_f32_rows(k)) return SPLIT_F32;
-  if (aligned_bf16_rows(q) && aligned_bf16_rows(k)) return SPLIT_BF16;
+  if (bias && bias->dtype != TENSION_F32) return SPLIT_NONE;
+  if (aligned_f32_rows(q) && aligned_f32_rows(k)) {
+    if (aligned_bf16_rows(v)) return SPLIT_F32;
+    if (aligned_f32_rows(v)) return SPLIT_F32V;
+    return SPLIT_NONE;
+  }
+  if (aligned_bf16_rows(q) && aligned_bf16_rows(k) && aligned_bf16_rows(v)) return SPLIT_BF16;
   return SPLIT_NONE;
 }
 
-// A further operand of a split kernel: float32 rows with SPLIT_F32, bf16
-// rows with SPLIT_BF16 (outputs and gradients of Q / K / out).
+// A further operand of a split kernel: float32 rows with float32 Q / K,
+// bf16 rows with SPLIT_BF16 (outputs and gradients of Q / K / out).
 bool split_rows(int kind, const tension_buf* b) {
-  return kind == SPLIT_F32 ? aligned_f32_rows(b) : aligned_bf16_rows(b);
+  return kind == SPLIT_BF16 ? aligned_bf16_rows(b) : aligned_f32_rows(b);
+}
+
+// dV of a split kernel: rows in V's dtype.
+bool split_dv_rows(int kind, const tension_buf* b) {
+  return kind == SPLIT_F32V ? aligned_f32_rows(b) : aligned_bf16_rows(b);
 }
 
 // tau / dtau of a split kernel: absent, or in Q's dtype (the kernels index
 // them as typed rows).
 bool split_side(int kind, const tension_buf* b) {
-  return !b || b->dtype == (kind == SPLIT_F32 ? TENSION_F32 : TENSION_BF16);
+  return !b || b->dtype == (kind == SPLIT_BF16 ? TENSION_BF16 : TENSION_F32);
 }
 
 // Local windows wider than one 64-row tile run on the split kernels in bf16
@@ -172,7 +182,7 @@ bool wide_on_split(bool global, int64_t W) {
 #endif
 }
 
-enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_SPLIT_BF16 = 2, KERNEL_SPLIT_F32 = 3 };
+enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_SPLIT_BF16 = 2, KERNEL_SPLIT_F32 = 3, KERNEL_SPLIT_F32V = 4 };
 
 thread_local int g_last_kernel = -1;
 
@@ -182,8 +192,9 @@ int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_
   // a larger one runs on the exact kernels
   BandArgs probe;
   if (kind != KERNEL_EXACT && phase != 3 && !band_args(p, &probe)) kind = KERNEL_EXACT;
-  int r = kind == KERNEL_SPLIT_F32    ? launch_split(phase, true, p, hs(stream), &e)
-          : kind == KERNEL_SPLIT_BF16 ? launch_split(phase, false, p, hs(stream), &e)
+  int r = kind == KERNEL_SPLIT_F32V   ? launch_split(phase, SPLIT_FLOW_F32V, p, hs(stream), &e)
+          : kind == KERNEL_SPLIT_F32  ? launch_split(phase, SPLIT_FLOW_F32, p, hs(stream), &e)
+          : kind == KERNEL_SPLIT_BF16 ? launch_split(phase, SPLIT_FLOW_BF16, p, hs(stream), &e)
           : kind == KERNEL_MFMA       ? launch_mfma(phase, p, hs(stream), &e)
                                       : launch_exact(phase, f64, p, hs(stream), &e);
   if (r == kGridTooLarge)
@@ -195,7 +206,9 @@ int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_
   return launched(e, what);
 }
 
-int split_kernel(int kind) { return kind == SPLIT_F32 ? KERNEL_SPLIT_F32 : KERNEL_SPLIT_BF16; }
+int split_kernel(int kind) {
+  return kind == SPLIT_F32V ? KERNEL_SPLIT_F32V : kind == SPLIT_F32 ? KERNEL_SPLIT_F32 : KERNEL_SPLIT_BF16;
+}
 
 // ---------------------------------------------------------------- forward
 
@@ -322,7 +335,7 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
     TRY(check_buf(mass, "mass", true, -1));
     const bool f32_mass = mass->dtype == TENSION_F32;
     const bool rows_mf = mf && global && aligned_bf16_rows(out) && f32_mass;
-    const bool rows_sp = sp && sk == SPLIT_F32 && ((flags & TENSION_NORM_MASS) || global) &&
+    const bool rows_sp = sp && sk != SPLIT_BF16 && ((flags & TENSION_NORM_MASS) || global) &&
                          aligned_f32_rows(out) && f32_mass;
     if (rows_mf || rows_sp) {
       p.out = make_buf(out);
@@ -349,7 +362,7 @@ int band_bwd_dkv(const tension_buf* q, const tension_buf* k, const tension_buf* 
   bool mf = mfma_ok_bwd(q, k, v, dout, bias, dk, dv, sh.D, flags);
   if (wide_on_split(global, Wparam)) mf = false;
   const int sk = mf ? SPLIT_NONE : split_kind(q, k, v, bias, sh.D, flags);
-  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dk) && aligned_bf16_rows(dv) &&
+  const bool sp = sk != SPLIT_NONE && split_rows(sk, dout) && split_rows(sk, dk) && split_dv_rows(sk, dv) &&
                   split_side(sk, dtau);
   return run_band(2, sp ? split_kernel(sk) : mf ? KERNEL_MFMA : KERNEL_EXACT, any_f64(q, k, v), p, stream,
                   global ? "tension_global_bwd(dkv)" : "tension_window_bwd_dkv");

@@ -81,10 +81,12 @@ int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipEr
 int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
 // kf32 (with fast): float32 q / k_new / K cache / out and a bf16 V
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32 = false);
-// split-operand kernels (split_band.h): f32 = float32 Q / K / dOut with a
-// bfloat16 V, else bf16 throughout; head dim 32 or 64; phase 0 forward,
-// 1 dQ, 2 dK / dV
-int launch_split(int phase, bool f32, const BandParams& p, hipStream_t st, hipError_t* err);
+// split-operand kernels (split_band.h), by flow: SPLIT_FLOW_BF16 bf16
+// throughout, SPLIT_FLOW_F32 float32 Q / K / dOut with a bfloat16 V,
+// SPLIT_FLOW_F32V float32 Q / K / V / dOut; head dim 32 or 64; phase 0
+// forward, 1 dQ, 2 dK / dV
+enum { SPLIT_FLOW_BF16 = 0, SPLIT_FLOW_F32 = 1, SPLIT_FLOW_F32V = 2 };
+int launch_split(int phase, int flow, const BandParams& p, hipStream_t st, hipError_t* err);
 // Compute units of the current device (queried once per device).
 int device_cus();
 int launch_rope(bool f64, const RopeParams& p, hipStream_t st, hipError_t* err);

@@ -10,8 +10,13 @@ void launch_split_dkv_bf16(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_fwd_f32(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_dq_f32(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_dkv_f32(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_fwd_f32v(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dq_f32v(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dkv_f32v(const BandParams& p, hipStream_t st, unsigned n);
 
-int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hipError_t* err) {
+int launch_split(int phase, int flow, const BandParams& p_in, hipStream_t st, hipError_t* err) {
+  if (flow != SPLIT_FLOW_BF16 && flow != SPLIT_FLOW_F32 && flow != SPLIT_FLOW_F32V) return -1;
+  if (phase < 0 || phase > 2) return -1;
   BandArgs probe;
   if (!band_args(p_in, &probe)) return -1;  // the kernels take 32-bit strides
   BandParams p = p_in;
@@ -23,10 +28,10 @@ int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hi
   // p.chunk > 0: runs of consecutive tiles per workgroup (p.chunk runs per
   // (b, h)) for a local window W <= 64: the forward, sized for about three
   // resident workgroups per CU, and the backward kernels for about two: dK /
-  // dV always, dQ for float32 Q / K at head dim 32 without dTau (where its
-  // run kernel measured faster); 0: one tile per workgroup
+  // dV always, dQ for float32 Q / K with a bf16 V at head dim 32 without
+  // dTau (where its run kernel measured faster); 0: one tile per workgroup
   p.chunk = 0;
-  const bool dq_runs = f32 && p.D == 32 && p.dtau.p == nullptr;
+  const bool dq_runs = flow == SPLIT_FLOW_F32 && p.D == 32 && p.dtau.p == nullptr;
   if ((phase == 0 || phase == 2 || (phase == 1 && dq_runs)) && !p.glob && p.win >= 1 && p.win <= 64) {
     const int64_t bh = (int64_t)p.B * p.H;
     const int64_t per_cu = phase == 0 ? 3 : 2;
@@ -38,12 +43,12 @@ int launch_split(int phase, bool f32, const BandParams& p_in, hipStream_t st, hi
     }
   }
   const unsigned n = (unsigned)nwg;
-  switch (phase) {
-    case 0: (f32 ? launch_split_fwd_f32 : launch_split_fwd_bf16)(p, st, n); break;
-    case 1: (f32 ? launch_split_dq_f32 : launch_split_dq_bf16)(p, st, n); break;
-    case 2: (f32 ? launch_split_dkv_f32 : launch_split_dkv_bf16)(p, st, n); break;
-    default: return -1;
-  }
+  typedef void (*Launch)(const BandParams&, hipStream_t, unsigned);
+  static const Launch table[3][3] = {
+      {launch_split_fwd_bf16, launch_split_dq_bf16, launch_split_dkv_bf16},
+      {launch_split_fwd_f32, launch_split_dq_f32, launch_split_dkv_f32},
+      {launch_split_fwd_f32v, launch_split_dq_f32v, launch_split_dkv_f32v}};
+  table[flow][phase](p, st, n);
   *err = hipGetLastError();
   return 0;
 }

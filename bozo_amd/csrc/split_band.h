@@ -19,6 +19,11 @@
 // With NT = 1 the same kernels are the bf16 MFMA path of the head dims and
 // windows the dedicated bf16 kernels do not take.
 //
+// NV: the terms of V (and the element of dV), 1 for a bf16 V as above, 3
+// for a float32 V (the reference's float32 flow, no autocast: every input
+// and gradient float32).  Products with V then keep t_i v_j with
+// i + j <= 2, and dV, float32 too, keeps L = 2.
+//
 // Head dim D = 32 or 64: LDS tiles are 64 rows x 64 bf16 (direct tiles,
 // mfma_common.h); D = 32 fills the first four 16-byte chunks of each row
 // and runs half the feature chunks.  Any band (local window of any width,
@@ -67,6 +72,21 @@ __device__ __forceinline__ f32x4 mmx(const bf16x8* a, const bf16x8* b, f32x4 c) 
       if (j >= 0 && j < NB) c = mfma(a[i], b[j], c);
     }
   return c;
+}
+
+// The same sum for an accumulator that runs over many products (a band's
+// key or query pairs): with SEP the terms of this product gather in a
+// zero-started accumulator that joins C in one add, so C -- the largest
+// value -- takes one rounding per product instead of one per term (the
+// float32-V flow, where a product has six terms).
+template <int NA, int NB, int L, bool SEP>
+__device__ __forceinline__ f32x4 mmx_run(const bf16x8* a, const bf16x8* b, f32x4 c) {
+  if constexpr (SEP) {
+    const f32x4 z = mmx<NA, NB, L>(a, b, f32x4{0.f, 0.f, 0.f, 0.f});
+    return c + z;
+  } else {
+    return mmx<NA, NB, L>(a, b, c);
+  }
 }
 
 // B operand of a product over 32 tile rows from two 16-row groups of
@@ -223,39 +243,40 @@ __device__ __forceinline__ Blocks band_blocks(const BandParams& p, int t0) {
   return r;
 }
 
-// Keys go through LDS: buffer `buf` holds block terms K_0 .. K_{NT-1}, V.
-template <int NT>
+// Keys go through LDS: buffer `buf` holds block terms K_0 .. K_{NT-1},
+// V_0 .. V_{NV-1}.
+template <int NT, int NV>
 __device__ __forceinline__ bf16* key_buf(bf16* lds, int buf) {
-  return lds + buf * (NT + 1) * kDTile;
+  return lds + buf * (NT + NV) * kDTile;
 }
 
 // Stream the key blocks of a band through NBUF LDS buffers: block i is
 // staged (from registers loaded during block i - 1) while the waves work on
 // block i - 1 (NBUF = 2) or after they leave it (NBUF = 1);
 // body(tiles, first key) runs once per block with its buffer filled.
-template <int NT, int D, int NBUF, typename Body>
-__device__ __forceinline__ void stream_keys(bf16* lds, const Elem<NT>* kb_, int64_t ks, const bf16* vb_,
+template <int NT, int NV, int D, int NBUF, typename Body>
+__device__ __forceinline__ void stream_keys(bf16* lds, const Elem<NT>* kb_, int64_t ks, const Elem<NV>* vb_,
                                             int64_t vs, const Blocks& bl, int T, int tid, Body body) {
   if (bl.n <= 0) return;
-  store_raw<NT>(load_raw<NT, D>(kb_, ks, bl.first, T, tid), key_buf<NT>(lds, 0), tid);
-  store_raw<1>(load_raw<1, D>(vb_, vs, bl.first, T, tid), key_buf<NT>(lds, 0) + NT * kDTile, tid);
+  store_raw<NT>(load_raw<NT, D>(kb_, ks, bl.first, T, tid), key_buf<NT, NV>(lds, 0), tid);
+  store_raw<NV>(load_raw<NV, D>(vb_, vs, bl.first, T, tid), key_buf<NT, NV>(lds, 0) + NT * kDTile, tid);
   __syncthreads();
   for (int i = 0; i < bl.n; ++i) {
     const int kb0 = bl.first + i * kTile;
     const int buf = NBUF == 2 ? (i & 1) : 0;
     const bool more = i + 1 < bl.n;
     Raw<NT> kn;
-    Raw<1> vn;
+    Raw<NV> vn;
     if (more) {
       kn = load_raw<NT, D>(kb_, ks, kb0 + kTile, T, tid);
-      vn = load_raw<1, D>(vb_, vs, kb0 + kTile, T, tid);
+      vn = load_raw<NV, D>(vb_, vs, kb0 + kTile, T, tid);
     }
-    body((const bf16*)key_buf<NT>(lds, buf), kb0);
+    body((const bf16*)key_buf<NT, NV>(lds, buf), kb0);
     if (more) {
       if (NBUF == 1) __syncthreads();  // every wave is done with the buffer
-      bf16* nb = key_buf<NT>(lds, NBUF == 2 ? (buf ^ 1) : 0);
+      bf16* nb = key_buf<NT, NV>(lds, NBUF == 2 ? (buf ^ 1) : 0);
       store_raw<NT>(kn, nb, tid);
-      store_raw<1>(vn, nb + NT * kDTile, tid);
+      store_raw<NV>(vn, nb + NT * kDTile, tid);
     }
     __syncthreads();
   }
@@ -381,7 +402,7 @@ __device__ __forceinline__ void dtau_rows_put(E* st, const E* v, int lane) {
 // row as B operands (Q as NT terms), its band, its O^T accumulators and
 // tau mass, its rows of tau (dtype of Q, host-checked) and of the bias
 // (float32, unit column stride); rows past T are never written.
-template <int NT, int D, int NORM, bool BIAS, bool TAU>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool TAU>
 struct FwdTile {
   using E = Elem<NT>;
   int b, h, g, c, lane, wave, t0, tq, lo, hi;
@@ -429,7 +450,7 @@ struct FwdTile {
     if constexpr (BIAS) bias_block(p, brow, tq, kb0, g, lo, hi, braw);
   }
 
-  // one key block (tiles K_0 .. K_{NT-1}, V at kt; first key kb0); LOADED:
+  // one key block (tiles K_0 .. K_{NT-1}, V_0 .. at kt; first key kb0); LOADED:
   // its bias is in braw already (bias_load), else it is loaded here
   template <bool LOADED = false>
   __device__ __forceinline__ void visit(const BandParams& p, const bf16* kt, int kb0) {
@@ -475,8 +496,10 @@ struct FwdTile {
       pack_terms<NT>(pr[2 * kk], pr[2 * kk + 1], ps);
 #pragma unroll
       for (int m = 0; m < D / 16; ++m) {
-        const bf16x8 va = dt_tr8(vt, m, 32 * kk, g, c);
-        acc[m] = mmx<1, NT, 2>(&va, ps, acc[m]);
+        bf16x8 va[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) va[i] = dt_tr8(vt + i * kDTile, m, 32 * kk, g, c);
+        acc[m] = mmx_run<NV, NT, 2, NV == 3>(va, ps, acc[m]);
       }
     }
   }
@@ -495,18 +518,18 @@ struct FwdTile {
   }
 };
 
-template <int NT, int D, int NORM, bool BIAS, bool TAU>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
   constexpr int NBUF = NT == 1 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + NV) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const TileId id = tile_id(p, p.glob != 0);
   const int T = p.T;
-  FwdTile<NT, D, NORM, BIAS, TAU> st;
+  FwdTile<NT, NV, D, NORM, BIAS, TAU> st;
   st.init(p, id.b, id.h, lane, wave, tstage);
   st.at(p, id.tile * kTile);
   const Blocks bl = band_blocks(p, st.t0);
@@ -514,10 +537,10 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + st.b * p.q.s0 + st.h * p.q.s2;
   const E* kb_ = (const E*)p.k.p + st.b * p.k.s0 + st.h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + st.b * p.v.s0 + st.h * p.v.s2;
+  const Elem<NV>* vb_ = (const Elem<NV>*)p.v.p + st.b * p.v.s0 + st.h * p.v.s2;
 #pragma unroll
   for (int ch = 0; ch < D / 32; ++ch) frag_row<NT>(qb_, p.q.s1, st.tq, T, 4 * ch + st.g, st.qf[ch]);
-  stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid,
+  stream_keys<NT, NV, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid,
                            [&](const bf16* kt, int kb0) { st.visit(p, kt, kb0); });
   st.finish(p);
 }
@@ -529,11 +552,11 @@ __global__ __launch_bounds__(kThreads) void xb_fwd(BandArgs args) {
 // into registers while tile t + 1 visits block t, and tile t + 1's query
 // rows while tile t visits block t.  Per tile one block staged instead of
 // two, and about three workgroups per CU in one round.
-template <int NT, int D, int NORM, bool BIAS, bool TAU>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool TAU>
 __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
-  __shared__ __attribute__((aligned(16))) bf16 lds[(NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 lds[(NT + NV) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> tstage[TAU ? 4 * kStageRows : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -548,8 +571,8 @@ __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
-  FwdTile<NT, D, NORM, BIAS, TAU> st;
+  const Elem<NV>* vb_ = (const Elem<NV>*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  FwdTile<NT, NV, D, NORM, BIAS, TAU> st;
   st.init(p, b, h, lane, wave, tstage);
   st.at(p, tA * kTile);
 #pragma unroll
@@ -559,7 +582,7 @@ __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
   {
     const int r0 = (tA > 0 ? tA - 1 : 0) * kTile;
     store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, r0, T, tid), lds, tid);
-    store_raw<1>(load_raw<1, D>(vb_, p.v.s1, r0, T, tid), lds + NT * kDTile, tid);
+    store_raw<NV>(load_raw<NV, D>(vb_, p.v.s1, r0, T, tid), lds + NT * kDTile, tid);
   }
   __syncthreads();
   // With a bias, each visit's bias loads go out ahead of the loads issued
@@ -573,11 +596,11 @@ __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
         asm volatile("" ::: "memory");
       }
       const Raw<NT> kn = load_raw<NT, D>(kb_, p.k.s1, t * kTile, T, tid);
-      const Raw<1> vn = load_raw<1, D>(vb_, p.v.s1, t * kTile, T, tid);
+      const Raw<NV> vn = load_raw<NV, D>(vb_, p.v.s1, t * kTile, T, tid);
       st.template visit<BIAS>(p, lds, (t - 1) * kTile);
       __syncthreads();  // every wave is done with block t - 1
       store_raw<NT>(kn, lds, tid);
-      store_raw<1>(vn, lds + NT * kDTile, tid);
+      store_raw<NV>(vn, lds + NT * kDTile, tid);
       __syncthreads();
     }
     // block t, while tile t + 1's query rows arrive
@@ -624,7 +647,7 @@ __global__ __launch_bounds__(kThreads) void xb_fwd_run(BandArgs args) {
 // (Q and dOut as terms), its band, the coefficients a = ca, c = cc, the dQ
 // accumulators -- and the pieces the MODE passes are made of.  dbh / dst:
 // dTau of this (b, h) and the wave's staging rows.
-template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool DTAU>
 struct DqTile {
   using E = Elem<NT>;
   int b, h, g, c, lane;
@@ -671,8 +694,10 @@ struct DqTile {
     const bf16* vt = kt + NT * kDTile;
 #pragma unroll
     for (int ch = 0; ch < D / 32; ++ch) {
-      const bf16x8 va = dt_row8(vt, 16 * j + c, 4 * ch + g);
-      dp = mmx<1, NT, 2>(&va, of[ch], dp);
+      bf16x8 va[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) va[i] = dt_row8(vt + i * kDTile, 16 * j + c, 4 * ch + g);
+      dp = mmx<NV, NT, 2>(va, of[ch], dp);
     }
   }
 
@@ -705,7 +730,7 @@ struct DqTile {
         bf16x8 ka[NT];
 #pragma unroll
         for (int i = 0; i < NT; ++i) ka[i] = dt_tr8(kt + i * kDTile, m, 32 * kk, g, c);
-        acc[m] = mmx<NT, NT, 2>(ka, gs, acc[m]);
+        acc[m] = mmx_run<NT, NT, 2, NV == 3>(ka, gs, acc[m]);
       }
     }
   }
@@ -761,7 +786,7 @@ struct DqTile {
 
   // MODE 1: the band's blocks (bl.n <= 2) sit in LDS buffers u0, u1
   __device__ __forceinline__ void mode1(const BandParams& p, const bf16* lds, int u0, int u1) {
-    const bf16* kts[2] = {key_buf<NT>((bf16*)lds, u0), key_buf<NT>((bf16*)lds, u1)};
+    const bf16* kts[2] = {key_buf<NT, NV>((bf16*)lds, u0), key_buf<NT, NV>((bf16*)lds, u1)};
     float P[2][4][4], Dp[2][4][4];
     E dv[2][DTAU ? 16 : 1];
     if constexpr (DTAU) {
@@ -883,10 +908,10 @@ struct QueryRaw {
   RawFrag<NT> q[D / 32], o[D / 32];
 };
 
-template <int NT, int D, int NORM, bool BIAS, bool DTAU>
-__device__ __forceinline__ DqTile<NT, D, NORM, BIAS, DTAU> dq_tile_base(const BandParams& p, int b, int h, int lane,
-                                                                        Elem<NT>* dst) {
-  DqTile<NT, D, NORM, BIAS, DTAU> q;
+template <int NT, int NV, int D, int NORM, bool BIAS, bool DTAU>
+__device__ __forceinline__ DqTile<NT, NV, D, NORM, BIAS, DTAU> dq_tile_base(const BandParams& p, int b, int h,
+                                                                            int lane, Elem<NT>* dst) {
+  DqTile<NT, NV, D, NORM, BIAS, DTAU> q;
   q.b = b;
   q.h = h;
   q.lane = lane;
@@ -898,12 +923,12 @@ __device__ __forceinline__ DqTile<NT, D, NORM, BIAS, DTAU> dq_tile_base(const Ba
   return q;
 }
 
-template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool DTAU, int MODE>
 __global__ __launch_bounds__(kThreads) void xb_dq(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
   constexpr int NBUF = (NT == 1 || MODE == 1) ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 lds[NBUF * (NT + NV) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -913,10 +938,10 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandArgs args) {
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const Elem<NV>* vb_ = (const Elem<NV>*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
-  DqTile<NT, D, NORM, BIAS, DTAU> st =
-      dq_tile_base<NT, D, NORM, BIAS, DTAU>(p, b, h, lane, dstage + (DTAU ? wave * kStageRows : 0));
+  DqTile<NT, NV, D, NORM, BIAS, DTAU> st =
+      dq_tile_base<NT, NV, D, NORM, BIAS, DTAU>(p, b, h, lane, dstage + (DTAU ? wave * kStageRows : 0));
   st.at(p, id.tile * kTile, wave);
 #pragma unroll
   for (int ch = 0; ch < D / 32; ++ch) {
@@ -927,28 +952,28 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandArgs args) {
   auto g_pass = [&](const bf16* kt, int kb0) { st.g_pass(p, kt, kb0); };
 
   if constexpr (MODE == 0) {
-    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+    stream_keys<NT, NV, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
   } else if constexpr (MODE == 3) {
     st.saved_coefficients(p);
-    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+    stream_keys<NT, NV, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
   } else if constexpr (MODE == 1) {
     // both blocks stay resident (buffers 0 and 1)
     if (bl.n > 0) {
-      store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first, T, tid), key_buf<NT>(lds, 0), tid);
-      store_raw<1>(load_raw<1, D>(vb_, p.v.s1, bl.first, T, tid), key_buf<NT>(lds, 0) + NT * kDTile, tid);
+      store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first, T, tid), key_buf<NT, NV>(lds, 0), tid);
+      store_raw<NV>(load_raw<NV, D>(vb_, p.v.s1, bl.first, T, tid), key_buf<NT, NV>(lds, 0) + NT * kDTile, tid);
     }
     if (bl.n > 1) {
-      store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first + kTile, T, tid), key_buf<NT>(lds, 1), tid);
-      store_raw<1>(load_raw<1, D>(vb_, p.v.s1, bl.first + kTile, T, tid), key_buf<NT>(lds, 1) + NT * kDTile,
-                   tid);
+      store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, bl.first + kTile, T, tid), key_buf<NT, NV>(lds, 1), tid);
+      store_raw<NV>(load_raw<NV, D>(vb_, p.v.s1, bl.first + kTile, T, tid),
+                    key_buf<NT, NV>(lds, 1) + NT * kDTile, tid);
     }
     __syncthreads();
     st.mode1(p, lds, 0, 1);
   } else {
-    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid,
+    stream_keys<NT, NV, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid,
                              [&](const bf16* kt, int kb0) { st.sums_pass(p, kt, kb0); });
     st.coefficients(p);
-    stream_keys<NT, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
+    stream_keys<NT, NV, D, NBUF>(lds, kb_, p.k.s1, vb_, p.v.s1, bl, T, tid, g_pass);
   }
   st.store(p, (float)(1.0 / p.scale));
 }
@@ -959,12 +984,12 @@ __global__ __launch_bounds__(kThreads) void xb_dq(BandArgs args) {
 // buffer j & 1, so tile t + 1 finds block t where tile t left it, and block
 // t + 1 and the next tile's query rows load into registers while tile t
 // computes.
-template <int NT, int D, int NORM, bool BIAS, bool DTAU, int MODE>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool DTAU, int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void xb_dq_run(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
   static_assert(MODE == 0 || MODE == 1, "runs take the one-pass and register tau-mass modes");
-  __shared__ __attribute__((aligned(16))) bf16 lds[2 * (NT + 1) * kDTile];
+  __shared__ __attribute__((aligned(16))) bf16 lds[2 * (NT + NV) * kDTile];
   __shared__ __attribute__((aligned(16))) Elem<NT> dstage[DTAU ? 4 * kStageRows : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -979,11 +1004,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const Elem<NV>* vb_ = (const Elem<NV>*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
   const float inv_scale = (float)(1.0 / p.scale);
-  DqTile<NT, D, NORM, BIAS, DTAU> st =
-      dq_tile_base<NT, D, NORM, BIAS, DTAU>(p, b, h, lane, dstage + (DTAU ? wave * kStageRows : 0));
+  DqTile<NT, NV, D, NORM, BIAS, DTAU> st =
+      dq_tile_base<NT, NV, D, NORM, BIAS, DTAU>(p, b, h, lane, dstage + (DTAU ? wave * kStageRows : 0));
   st.at(p, tA * kTile, wave);
 #pragma unroll
   for (int ch = 0; ch < D / 32; ++ch) {
@@ -992,19 +1017,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
   }
   // blocks tA - 1 (when tA > 0) and tA
   for (int j = tA > 0 ? tA - 1 : 0; j <= tA; ++j) {
-    bf16* kbuf = key_buf<NT>(lds, j & 1);
+    bf16* kbuf = key_buf<NT, NV>(lds, j & 1);
     store_raw<NT>(load_raw<NT, D>(kb_, p.k.s1, j * kTile, T, tid), kbuf, tid);
-    store_raw<1>(load_raw<1, D>(vb_, p.v.s1, j * kTile, T, tid), kbuf + NT * kDTile, tid);
+    store_raw<NV>(load_raw<NV, D>(vb_, p.v.s1, j * kTile, T, tid), kbuf + NT * kDTile, tid);
   }
   __syncthreads();
   for (int t = tA; t < tB; ++t) {
     const bool more = t + 1 < tB;
     Raw<NT> kn;
-    Raw<1> vn;
+    Raw<NV> vn;
     QueryRaw<NT, D> qn;
     if (more) {
       kn = load_raw<NT, D>(kb_, p.k.s1, (t + 1) * kTile, T, tid);
-      vn = load_raw<1, D>(vb_, p.v.s1, (t + 1) * kTile, T, tid);
+      vn = load_raw<NV, D>(vb_, p.v.s1, (t + 1) * kTile, T, tid);
       const int tq1 = st.tq + kTile;
 #pragma unroll
       for (int ch = 0; ch < D / 32; ++ch) {
@@ -1017,14 +1042,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
     if constexpr (MODE == 1) {
       st.mode1(p, lds, j0 & 1, (j0 + 1) & 1);
     } else {
-      for (int s = 0; s < st.bl.n; ++s) st.g_pass(p, key_buf<NT>(lds, (j0 + s) & 1), (j0 + s) * kTile);
+      for (int s = 0; s < st.bl.n; ++s) st.g_pass(p, key_buf<NT, NV>(lds, (j0 + s) & 1), (j0 + s) * kTile);
     }
     st.store(p, inv_scale);
     if (more) {
       __syncthreads();  // every wave is done with block t - 1's buffer
-      bf16* kbuf = key_buf<NT>(lds, (t + 1) & 1);
+      bf16* kbuf = key_buf<NT, NV>(lds, (t + 1) & 1);
       store_raw<NT>(kn, kbuf, tid);
-      store_raw<1>(vn, kbuf + NT * kDTile, tid);
+      store_raw<NV>(vn, kbuf + NT * kDTile, tid);
       st.at(p, (t + 1) * kTile, wave);
 #pragma unroll
       for (int ch = 0; ch < D / 32; ++ch) {
@@ -1039,18 +1064,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
 // ----------------------------------------------------------------- dK / dV
 
 // One key tile's lane state in the dK / dV kernels: the lane's key row as B
-// operands (K as terms, V exact), the queries that see it, its dK / dV
+// operands (K and V as terms), the queries that see it, its dK / dV
 // accumulators, and the number of query tiles whose band reaches the tile.
-template <int NT, int D>
+template <int NT, int NV, int D>
 struct KeyTile {
-  bf16x8 kf[D / 32][NT], vf[D / 32];
+  bf16x8 kf[D / 32][NT], vf[D / 32][NV];
   f32x4 dk[D / 16], dv[D / 16];
   int tk, qlo, qhi, wq_lo, wq_hi, nqt;
 };
 
 // Key tile k0's geometry for lane (wave, c); accumulators cleared.
-template <int NT, int D>
-__device__ __forceinline__ void key_tile_init(const BandParams& p, int k0, int wave, int c, KeyTile<NT, D>& kt) {
+template <int NT, int NV, int D>
+__device__ __forceinline__ void key_tile_init(const BandParams& p, int k0, int wave, int c,
+                                              KeyTile<NT, NV, D>& kt) {
   const int T = p.T;
   kt.tk = k0 + wave * 16 + c;
   // queries that see this lane's key: [tk + 1 - diag, min(tk + win, T - 1)]
@@ -1069,30 +1095,30 @@ __device__ __forceinline__ void key_tile_init(const BandParams& p, int k0, int w
 }
 
 // The lane's key row (features 8 (4 ch + g) .. +7 of K and V) as loaded.
-template <int NT, int D>
+template <int NT, int NV, int D>
 struct KeyRaw {
   RawFrag<NT> k[D / 32];
-  RawFrag<1> v[D / 32];
+  RawFrag<NV> v[D / 32];
 };
 
-template <int NT, int D>
-__device__ __forceinline__ KeyRaw<NT, D> key_raw_load(const Elem<NT>* kb_, int64_t ks, const bf16* vb_, int64_t vs,
-                                                      int tk, int T, int g) {
-  KeyRaw<NT, D> r;
+template <int NT, int NV, int D>
+__device__ __forceinline__ KeyRaw<NT, NV, D> key_raw_load(const Elem<NT>* kb_, int64_t ks, const Elem<NV>* vb_,
+                                                          int64_t vs, int tk, int T, int g) {
+  KeyRaw<NT, NV, D> r;
 #pragma unroll
   for (int ch = 0; ch < D / 32; ++ch) {
     r.k[ch] = frag_load<NT>(kb_, ks, tk, T, 4 * ch + g);
-    r.v[ch] = frag_load<1>(vb_, vs, tk, T, 4 * ch + g);
+    r.v[ch] = frag_load<NV>(vb_, vs, tk, T, 4 * ch + g);
   }
   return r;
 }
 
-template <int NT, int D>
-__device__ __forceinline__ void key_raw_terms(const KeyRaw<NT, D>& r, KeyTile<NT, D>& kt) {
+template <int NT, int NV, int D>
+__device__ __forceinline__ void key_raw_terms(const KeyRaw<NT, NV, D>& r, KeyTile<NT, NV, D>& kt) {
 #pragma unroll
   for (int ch = 0; ch < D / 32; ++ch) {
     frag_terms<NT>(r.k[ch], kt.kf[ch]);
-    frag_terms<1>(r.v[ch], &kt.vf[ch]);
+    frag_terms<NV>(r.v[ch], kt.vf[ch]);
   }
 }
 
@@ -1126,9 +1152,9 @@ __device__ __forceinline__ void dkv_stage(const BandParams& p, bf16* base, float
 // One query tile q0 (terms in LDS at qt, coefficient rows sa_ / scf_)
 // against key tile kt:  dV^T += dO^T (a P),  dK^T += Q^T G.  dtb / bb: dTau
 // and bias of this (b, h) (dtype of Q / float32).
-template <int NT, int D, bool BIAS, bool DTAU>
+template <int NT, int NV, int D, bool BIAS, bool DTAU>
 __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, const float* sa_, const float* scf_,
-                                          int q0, KeyTile<NT, D>& kt, const Elem<NT>* dtb, const float* bb,
+                                          int q0, KeyTile<NT, NV, D>& kt, const Elem<NT>* dtb, const float* bb,
                                           float k2, int g, int c) {
   const bf16* ot = qt + NT * kDTile;
   float Pa[4][4], G[4][4];
@@ -1179,7 +1205,7 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
         oa_[t] = dt_row8(ot + t * kDTile, 16 * j + c, 4 * ch + g);
       }
       sv = mmx<NT, NT, 2>(qa_, kt.kf[ch], sv);
-      dp = mmx<NT, 1, 2>(oa_, &kt.vf[ch], dp);
+      dp = mmx<NT, NV, 2>(oa_, kt.vf[ch], dp);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1209,25 +1235,26 @@ __device__ __forceinline__ void dkv_visit(const BandParams& p, const bf16* qt, c
         oa_[t] = dt_tr8(ot + t * kDTile, m, 32 * kk, g, c);
         qa_[t] = dt_tr8(qt + t * kDTile, m, 32 * kk, g, c);
       }
-      kt.dv[m] = mmx<NT, NT, 1>(oa_, ps, kt.dv[m]);
-      kt.dk[m] = mmx<NT, NT, 2>(qa_, gs, kt.dk[m]);
+      kt.dv[m] = mmx_run<NT, NT, NV == 1 ? 1 : 2, NV == 3>(oa_, ps, kt.dv[m]);
+      kt.dk[m] = mmx_run<NT, NT, 2, NV == 3>(qa_, gs, kt.dk[m]);
     }
   }
 }
 
-// The lane's dK row (dtype of Q; times 1 / scale) and dV row (bf16).
-template <int NT, int D>
-__device__ __forceinline__ void dkv_store(const BandParams& p, const KeyTile<NT, D>& kt, int b, int h,
+// The lane's dK row (dtype of Q; times 1 / scale) and dV row (dtype of V).
+template <int NT, int NV, int D>
+__device__ __forceinline__ void dkv_store(const BandParams& p, const KeyTile<NT, NV, D>& kt, int b, int h,
                                           float inv_scale, int g) {
   if (kt.tk >= p.T) return;
   using E = Elem<NT>;
+  using EV = Elem<NV>;
   store_acc<E, D>((E*)p.dk.p + b * p.dk.s0 + (int64_t)kt.tk * p.dk.s1 + h * p.dk.s2, kt.dk, inv_scale, g);
-  store_acc<bf16, D>((bf16*)p.dv.p + b * p.dv.s0 + (int64_t)kt.tk * p.dv.s1 + h * p.dv.s2, kt.dv, 1.f, g);
+  store_acc<EV, D>((EV*)p.dv.p + b * p.dv.s0 + (int64_t)kt.tk * p.dv.s1 + h * p.dv.s2, kt.dv, 1.f, g);
 }
 
 // Key tile k: the query tiles whose band reaches it pass through LDS in
 // turn (Q and dOut as NT terms each, plus their rows' coefficients a, c).
-template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
@@ -1245,12 +1272,12 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const Elem<NV>* vb_ = (const Elem<NV>*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
 
-  KeyTile<NT, D> kt;
-  key_tile_init<NT, D>(p, k0, wave, c, kt);
-  key_raw_terms<NT, D>(key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
+  KeyTile<NT, NV, D> kt;
+  key_tile_init<NT, NV, D>(p, k0, wave, c, kt);
+  key_raw_terms<NT, NV, D>(key_raw_load<NT, NV, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
 
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
@@ -1273,7 +1300,7 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
       qn = load_raw<NT, D>(qb_, p.q.s1, q0 + kTile, T, tid);
       on = load_raw<NT, D>(ob_, p.dout.s1, q0 + kTile, T, tid);
     }
-    dkv_visit<NT, D, BIAS, DTAU>(p, lds + buf * TPB * kDTile, sa[buf], scf[buf], q0, kt, dtb, bb, k2, g, c);
+    dkv_visit<NT, NV, D, BIAS, DTAU>(p, lds + buf * TPB * kDTile, sa[buf], scf[buf], q0, kt, dtb, bb, k2, g, c);
     if (more) {
       if (NBUF == 1) __syncthreads();  // every wave is done with the buffer
       const int nb = NBUF == 2 ? (buf ^ 1) : 0;
@@ -1281,7 +1308,7 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
       __syncthreads();
     }
   }
-  dkv_store<NT, D>(p, kt, b, h, inv_scale, g);
+  dkv_store<NT, NV, D>(p, kt, b, h, inv_scale, g);
 }
 
 // Runs of key tiles for local windows W <= 64, where key tile k is seen by
@@ -1294,7 +1321,7 @@ __global__ __launch_bounds__(kThreads) void xb_dkv(BandArgs args) {
 // visits query tile k + 1, then k): two runs that share a boundary query
 // tile then read it at the same time (both at their ends or both at their
 // starts), and the second read is an L2 hit.
-template <int NT, int D, int NORM, bool BIAS, bool DTAU>
+template <int NT, int NV, int D, int NORM, bool BIAS, bool DTAU>
 __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   touch_args(args);
   const BandParams p = band_params(args);
@@ -1315,7 +1342,7 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   using E = Elem<NT>;
   const E* qb_ = (const E*)p.q.p + b * p.q.s0 + h * p.q.s2;
   const E* kb_ = (const E*)p.k.p + b * p.k.s0 + h * p.k.s2;
-  const bf16* vb_ = (const bf16*)p.v.p + b * p.v.s0 + h * p.v.s2;
+  const Elem<NV>* vb_ = (const Elem<NV>*)p.v.p + b * p.v.s0 + h * p.v.s2;
   const E* ob_ = (const E*)p.dout.p + b * p.dout.s0 + h * p.dout.s2;
   const float inv_scale = (float)(1.0 / p.scale);
   const float k2 = -kLog2e * inv_scale;
@@ -1325,9 +1352,9 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
   if (n <= 0) return;
 
   const int kfirst = desc ? kB - 1 : kA;
-  KeyTile<NT, D> kt;
-  key_tile_init<NT, D>(p, kfirst * kTile, wave, c, kt);
-  key_raw_terms<NT, D>(key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
+  KeyTile<NT, NV, D> kt;
+  key_tile_init<NT, NV, D>(p, kfirst * kTile, wave, c, kt);
+  key_raw_terms<NT, NV, D>(key_raw_load<NT, NV, D>(kb_, p.k.s1, vb_, p.v.s1, kt.tk, T, g), kt);
   {
     // a key tile's first visit: query tile k (up), k + 1 when it sees the
     // tile (down); the trip before left that tile in LDS
@@ -1346,7 +1373,7 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
       qn = load_raw<NT, D>(qb_, p.q.s1, q2, T, tid);
       on = load_raw<NT, D>(ob_, p.dout.s1, q2, T, tid);
     }
-    dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, q1, kt, dtb, bb, k2, g, c);
+    dkv_visit<NT, NV, D, BIAS, DTAU>(p, lds, sa, scf, q1, kt, dtb, bb, k2, g, c);
     if (two) {
       __syncthreads();  // every wave is done with the first visit's tile
       dkv_stage<NT, D, NORM>(p, lds, sa, scf, q2, qn, on, b, h, tid);
@@ -1354,20 +1381,20 @@ __global__ __launch_bounds__(kThreads) void xb_dkv_run(BandArgs args) {
     }
     const bool next = i + 1 < n;
     const int kn0 = (desc ? k - 1 : k + 1) * kTile;
-    KeyRaw<NT, D> kr;
-    if (next) kr = key_raw_load<NT, D>(kb_, p.k.s1, vb_, p.v.s1, kn0 + wave * 16 + c, T, g);
-    if (two) dkv_visit<NT, D, BIAS, DTAU>(p, lds, sa, scf, q2, kt, dtb, bb, k2, g, c);
-    dkv_store<NT, D>(p, kt, b, h, inv_scale, g);
+    KeyRaw<NT, NV, D> kr;
+    if (next) kr = key_raw_load<NT, NV, D>(kb_, p.k.s1, vb_, p.v.s1, kn0 + wave * 16 + c, T, g);
+    if (two) dkv_visit<NT, NV, D, BIAS, DTAU>(p, lds, sa, scf, q2, kt, dtb, bb, k2, g, c);
+    dkv_store<NT, NV, D>(p, kt, b, h, inv_scale, g);
     if (next) {
-      key_tile_init<NT, D>(p, kn0, wave, c, kt);
-      key_raw_terms<NT, D>(kr, kt);
+      key_tile_init<NT, NV, D>(p, kn0, wave, c, kt);
+      key_raw_terms<NT, NV, D>(kr, kt);
     }
   }
 }
 
 // ----------------------------------------------------------------- launch
 
-template <int NT, int D, int NORM, int PHASE>
+template <int NT, int NV, int D, int NORM, int PHASE>
 void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
   const bool bias = p.bias.p != nullptr;
   const dim3 grid(n), block(kThreads);
@@ -1375,11 +1402,11 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
 #define XB_BT(K, ...)                                                                           \
   do {                                                                                          \
     if (bias) {                                                                                 \
-      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, true, true __VA_ARGS__>), grid, block, 0, st, a);  \
-      else hipLaunchKernelGGL((K<NT, D, NORM, true, false __VA_ARGS__>), grid, block, 0, st, a);     \
+      if (opt) hipLaunchKernelGGL((K<NT, NV, D, NORM, true, true __VA_ARGS__>), grid, block, 0, st, a);  \
+      else hipLaunchKernelGGL((K<NT, NV, D, NORM, true, false __VA_ARGS__>), grid, block, 0, st, a);     \
     } else {                                                                                    \
-      if (opt) hipLaunchKernelGGL((K<NT, D, NORM, false, true __VA_ARGS__>), grid, block, 0, st, a); \
-      else hipLaunchKernelGGL((K<NT, D, NORM, false, false __VA_ARGS__>), grid, block, 0, st, a);    \
+      if (opt) hipLaunchKernelGGL((K<NT, NV, D, NORM, false, true __VA_ARGS__>), grid, block, 0, st, a); \
+      else hipLaunchKernelGGL((K<NT, NV, D, NORM, false, false __VA_ARGS__>), grid, block, 0, st, a);    \
     }                                                                                           \
   } while (0)
   if constexpr (PHASE == 0) {
@@ -1391,14 +1418,25 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
     // runs of tiles (a local window W <= 64): float32 Q / K at head dim 32
     // without dTau, where they measured faster (B32 H4 T1024 W32 tau-mass
     // step 82.8 -> 76.5 us); at head dim 64 the run kernel's registers
-    // (246 VGPRs, and spills with dTau) cost what the shared blocks save
-    constexpr bool kRuns = NT == 3 && D == 32;
-    if (kRuns && p.chunk > 0 && !opt) {
-      constexpr int M = NORM == NORM_MASS_ ? 1 : 0;
-      if (bias) hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, true, false, M>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((xb_dq_run<NT, D, NORM, false, false, M>), grid, block, 0, st, a);
-    } else if constexpr (NORM != NORM_MASS_) {
+    // (246 VGPRs, and spills with dTau) cost what the shared blocks save;
+    // with a float32 V two resident key blocks of six terms each would
+    // take 96 KB of LDS
+    constexpr bool kRuns = NT == 3 && NV == 1 && D == 32;
+    if constexpr (kRuns) {
+      if (p.chunk > 0 && !opt) {
+        constexpr int M = NORM == NORM_MASS_ ? 1 : 0;
+        if (bias) hipLaunchKernelGGL((xb_dq_run<NT, NV, D, NORM, true, false, M>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((xb_dq_run<NT, NV, D, NORM, false, false, M>), grid, block, 0, st, a);
+        return;
+      }
+    }
+    if constexpr (NORM != NORM_MASS_) {
       XB_BT(xb_dq, , 0);
+    } else if constexpr (NV == 3) {
+      // float32 V: the register tau-mass mode would keep two blocks of six
+      // terms in LDS (96 KB); the saved rows (one pass) or two passes
+      if (p.coef_pre) XB_BT(xb_dq, , 3);
+      else XB_BT(xb_dq, , 2);
     } else if constexpr (NT == 3) {
       // a band within two blocks keeps P and dP in registers (faster than
       // one pass from saved rows at W = 64: 42 against 48 us at config 2)
@@ -1419,19 +1457,19 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
 
 // PHASE 0: forward, 1: dQ (+ coefficients), 2: dK / dV; one workgroup per
 // 64-row tile (n of them)
-template <int NT, int PHASE>
+template <int NT, int NV, int PHASE>
 void launch(const BandParams& p, hipStream_t st, unsigned n) {
   const int norm = (p.flags & TENSION_NORM_MASS)    ? NORM_MASS_
                    : (p.flags & TENSION_NORM_COUNT) ? NORM_COUNT_
                                                     : NORM_RAW;
   if (p.D == 32) {
-    if (norm == NORM_MASS_) launch_norm<NT, 32, NORM_MASS_, PHASE>(p, st, n);
-    else if (norm == NORM_COUNT_) launch_norm<NT, 32, NORM_COUNT_, PHASE>(p, st, n);
-    else launch_norm<NT, 32, NORM_RAW, PHASE>(p, st, n);
+    if (norm == NORM_MASS_) launch_norm<NT, NV, 32, NORM_MASS_, PHASE>(p, st, n);
+    else if (norm == NORM_COUNT_) launch_norm<NT, NV, 32, NORM_COUNT_, PHASE>(p, st, n);
+    else launch_norm<NT, NV, 32, NORM_RAW, PHASE>(p, st, n);
   } else {
-    if (norm == NORM_MASS_) launch_norm<NT, 64, NORM_MASS_, PHASE>(p, st, n);
-    else if (norm == NORM_COUNT_) launch_norm<NT, 64, NORM_COUNT_, PHASE>(p, st, n);
-    else launch_norm<NT, 64, NORM_RAW, PHASE>(p, st, n);
+    if (norm == NORM_MASS_) launch_norm<NT, NV, 64, NORM_MASS_, PHASE>(p, st, n);
+    else if (norm == NORM_COUNT_) launch_norm<NT, NV, 64, NORM_COUNT_, PHASE>(p, st, n);
+    else launch_norm<NT, NV, 64, NORM_RAW, PHASE>(p, st, n);
   }
 }
 

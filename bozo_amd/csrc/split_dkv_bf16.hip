@@ -5,7 +5,7 @@
 namespace tension {
 
 void launch_split_dkv_bf16(const BandParams& p, hipStream_t st, unsigned n) {
-  split::launch<1, 2>(p, st, n);
+  split::launch<1, 1, 2>(p, st, n);
 }
 
 }  // namespace tension

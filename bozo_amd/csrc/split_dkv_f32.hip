@@ -1,11 +1,12 @@
 // Instantiates the split-operand band kernels (split_band.h) for phase
-// dkv, float32 Q / K / dOut (three bf16 terms).
+// dkv, float32 Q / K / dOut with a bf16 V (three bf16 terms per
+// float32 value).
 #include "split_band.h"
 
 namespace tension {
 
 void launch_split_dkv_f32(const BandParams& p, hipStream_t st, unsigned n) {
-  split::launch<3, 2>(p, st, n);
+  split::launch<3, 1, 2>(p, st, n);
 }
 
 }  // namespace tension

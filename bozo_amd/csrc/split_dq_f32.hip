@@ -1,11 +1,12 @@
 // Instantiates the split-operand band kernels (split_band.h) for phase
-// dq, float32 Q / K / dOut (three bf16 terms).
+// dq, float32 Q / K / dOut with a bf16 V (three bf16 terms per
+// float32 value).
 #include "split_band.h"
 
 namespace tension {
 
 void launch_split_dq_f32(const BandParams& p, hipStream_t st, unsigned n) {
-  split::launch<3, 1>(p, st, n);
+  split::launch<3, 1, 1>(p, st, n);
 }
 
 }  // namespace tension

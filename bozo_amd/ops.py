@@ -99,8 +99,9 @@ _EXACT_WARNED = set()
 
 def _note_exact_path(what: str, Q: Tensor, K: Tensor, V: Tensor, pairs: int) -> None:
     """Warn once per dtype / head-dim combination when a large call ran on the
-    exact kernels (one thread per row, no MFMA): float16, float32 V, head
-    dims other than 32 / 64 or unaligned rows.  float64 is exact on purpose."""
+    exact kernels (one thread per row, no MFMA): float16, mixes other than
+    float32 Q / K with a bf16 or float32 V, head dims other than 32 / 64 or
+    unaligned rows.  float64 is exact on purpose."""
     if pairs < (1 << 20) or Q.dtype == torch.float64:
         return
     if int(L.lib().tension_last_kernel()) != L.KERNEL_EXACT:
@@ -112,7 +113,8 @@ def _note_exact_path(what: str, Q: Tensor, K: Tensor, V: Tensor, pairs: int) -> 
     import warnings
     warnings.warn(f"{what}: Q/K/V {Q.dtype}/{K.dtype}/{V.dtype} with head dim {Q.shape[-1]} ran on the exact "
                   "(non-MFMA) kernels, one thread per row; the MFMA kernels take bf16, or float32 Q/K with "
-                  "a bf16 V, at head dim 32 or 64 with 16-byte aligned rows", RuntimeWarning, stacklevel=3)
+                  "a bf16 or float32 V, at head dim 32 or 64 with 16-byte aligned rows", RuntimeWarning,
+                  stacklevel=3)
 
 
 def _window_fwd(Q, K, V, W, scale, tau, bias, flags, mass):
@@ -137,9 +139,9 @@ class _CausalTensionFn(torch.autograd.Function):
         if Bias is not None and tuple(Bias.shape) != (B, T, W):
             raise ValueError(f"bias must be [B, T, W]=[{B}, {T}, {W}], got {tuple(Bias.shape)}")
         tau = torch.empty(B, T, H, W, dtype=Q.dtype, device=Q.device) if return_tau else None
-        # the backward recomputes tau from the inputs; in the autocast flow
-        # (float32 Q / K, bf16 V) under tau-mass it takes the per-query
-        # coefficients from the forward's float32 rows and tau mass
+        # the backward recomputes tau from the inputs; with float32 Q / K
+        # under tau-mass it takes the per-query coefficients from the
+        # forward's float32 rows and tau mass where that is the faster dQ
         # (tension_window_bwd_saved: one pass over the band instead of two)
         rows = _saved_rows_flow(Q, K, V, W, flags)
         mass = torch.empty(B, T, H, dtype=torch.float32, device=Q.device) if rows else None
@@ -167,12 +169,17 @@ class _CausalTensionFn(torch.autograd.Function):
 
 
 def _saved_rows_flow(Q: Tensor, K: Tensor, V: Tensor, W: int, flags: int) -> bool:
-    """Tau-mass in the reference's autocast flow (float32 Q / K, bf16 V, head
-    dim 32 / 64) with a window wider than 64: the backward takes its
-    coefficients from the forward's rows (narrower bands form them in
-    registers, which is faster)."""
-    return bool(flags & L.NORM_MASS) and W > 64 and Q.dtype == torch.float32 and K.dtype == torch.float32 \
-        and V.dtype == torch.bfloat16 and Q.shape[-1] in (32, 64)
+    """Tau-mass with float32 Q / K at head dim 32 / 64, where the backward
+    takes its coefficients from the forward's rows: with a bf16 V (the
+    reference's autocast flow) for windows wider than 64 (narrower bands
+    form them in registers, which is faster), with a float32 V at every
+    window (its dQ kernel keeps no band in registers)."""
+    if not (flags & L.NORM_MASS) or Q.dtype != torch.float32 or K.dtype != torch.float32 \
+            or Q.shape[-1] not in (32, 64):
+        return False
+    if V.dtype == torch.bfloat16:
+        return W > 64
+    return V.dtype == torch.float32
 
 
 def _window_bwd(Q, K, V, dOut, dTau, Bias, W, scale, flags, out=None, mass=None):
