@@ -456,16 +456,20 @@ def bench_window_variants(dev, steps, warmup):
         and in bf16 (the dedicated bf16 kernels, W > 64 split backward);
       * head dim 32 in bf16 (the reference's default model, model.py:33-36):
         BASELINE config 1's shape (B4 H4 T256 W32) and a 32-sequence batch
-        at T1024."""
+        at T1024;
+      * the reference's float32 flow (no autocast: Q, K, V, out, dOut and
+        every gradient float32; the split kernels with V as three terms
+        too) at the 117M layer, the 350M local layer and head dim 32."""
     def sets_for(B, H, T, D, W, flow, n=4, seed=11):
         raw = make_window_sets(n, B, T, H, D, dev, seed=seed)
         g = torch.Generator(device=dev).manual_seed(seed + 1)
         out = []
         for s in raw:
-            if flow == "f32qk":
+            if flow in ("f32qk", "f32"):
+                v = s["V"].detach().float().requires_grad_(True) if flow == "f32" else s["V"]
                 s = dict(Q=s["Q"].detach().float().requires_grad_(True),
-                         K=s["K"].detach().float().requires_grad_(True), V=s["V"], dO=s["dO"].float())
-            dt = torch.float32 if flow == "f32qk" else torch.bfloat16
+                         K=s["K"].detach().float().requires_grad_(True), V=v, dO=s["dO"].float())
+            dt = torch.bfloat16 if flow == "bf16" else torch.float32
             s["dTau"] = (torch.randn(B, T, H, W, device=dev, generator=g) * 0.1).to(dt)
             out.append(s)
         return out
@@ -479,27 +483,34 @@ def bench_window_variants(dev, steps, warmup):
             ("117m_local_autocast", (8, 12, 1024, 64, 64), "f32qk", False),
             ("d32_bf16_config1", (4, 4, 256, 32, 32), "bf16", False),
             ("d32_bf16_b32_t1024", (32, 4, 1024, 32, 32), "bf16", False),
-            ("d32_autocast_b32_t1024", (32, 4, 1024, 32, 32), "f32qk", False)):
+            ("d32_autocast_b32_t1024", (32, 4, 1024, 32, 32), "f32qk", False),
+            ("117m_local_f32", (8, 12, 1024, 64, 64), "f32", False),
+            ("350m_local_f32", (4, 16, 1024, 64, 256), "f32", False),
+            ("d32_f32_b32_t1024", (32, 4, 1024, 32, 32), "f32", False)):
         sets = sets_for(B, H, T, D, W, flow)
         run = Runner([window_step_fn(s, W, math.sqrt(D), "mass", return_tau=tau) for s in sets])
         ms = time_units(run, max(steps, 40), warmup, f"variant:{name}")
         kernel = int(L.lib().tension_last_kernel())
         del run, sets
-        el_qk = 4 if flow == "f32qk" else 2
+        el_qk = 2 if flow == "bf16" else 4
+        el_v = 4 if flow == "f32" else 2
         # compulsory bytes: fwd reads Q, K, V, writes out; bwd reads Q, K, V, dO,
-        # writes dQ, dK, dV (out / dO / dQ / dK in Q's dtype, V / dV bf16)
+        # writes dQ, dK, dV (out / dO / dQ / dK in Q's dtype, V / dV in V's)
         nel = B * T * H * D
-        step_bytes = nel * (el_qk * 2 + 2 + el_qk) + nel * (el_qk * 2 + 2 + el_qk + el_qk * 2 + 2)
+        step_bytes = nel * (el_qk * 2 + el_v + el_qk) + nel * (el_qk * 2 + el_v + el_qk + el_qk * 2 + el_v)
         if tau:
             step_bytes += 2 * B * T * H * W * el_qk
         rows.append({"name": name, "B": B, "H": H, "T": T, "head_dim": D, "window": W,
-                     "dtype_flow": "fp32 Q/K/out/dOut, bf16 V/dV" if flow == "f32qk" else "bf16",
+                     "dtype_flow": {"f32qk": "fp32 Q/K/out/dOut, bf16 V/dV", "f32": "fp32 throughout",
+                                    "bf16": "bf16"}[flow],
                      "tau_and_dtau": tau, "ms_per_step": round(ms, 5),
                      "tokens_per_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": step_bytes,
                      "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "kernel_family": {0: "exact", 1: "mfma_bf16", 2: "split_bf16", 3: "split_f32"}.get(kernel)})
+                     "kernel_family": {0: "exact", 1: "mfma_bf16", 2: "split_bf16", 3: "split_f32",
+                                       4: "split_f32v"}.get(kernel)})
         log(f"[bench] variant {rows[-1]}")
-    return {"config": "window op at the reference's other shipped shapes (350M preset W256, head dim 32)",
+    return {"config": "window op at the reference's other shipped shapes (350M preset W256, head dim 32) "
+                      "and in its float32 flow",
             "rows": rows}
 
 

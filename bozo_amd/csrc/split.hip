@@ -28,11 +28,16 @@ int launch_split(int phase, int flow, const BandParams& p_in, hipStream_t st, hi
   // p.chunk > 0: runs of consecutive tiles per workgroup (p.chunk runs per
   // (b, h)) for a local window W <= 64: the forward, sized for about three
   // resident workgroups per CU, and the backward kernels for about two: dK /
-  // dV always, dQ for float32 Q / K with a bf16 V at head dim 32 without
-  // dTau (where its run kernel measured faster); 0: one tile per workgroup
+  // dV except with a float32 V at head dim 64 (there its run kernel holds
+  // 272 registers, one wave per SIMD, and one tile per workgroup measured
+  // faster: 134 against 142 us per float32 step at B8 H12 T1024 W64), dQ
+  // for float32 Q / K with a bf16 V at head dim 32 without dTau (where its
+  // run kernel measured faster); 0: one tile per workgroup
   p.chunk = 0;
   const bool dq_runs = flow == SPLIT_FLOW_F32 && p.D == 32 && p.dtau.p == nullptr;
-  if ((phase == 0 || phase == 2 || (phase == 1 && dq_runs)) && !p.glob && p.win >= 1 && p.win <= 64) {
+  const bool dkv_runs = !(flow == SPLIT_FLOW_F32V && p.D == 64);
+  if ((phase == 0 || (phase == 2 && dkv_runs) || (phase == 1 && dq_runs)) && !p.glob && p.win >= 1 &&
+      p.win <= 64) {
     const int64_t bh = (int64_t)p.B * p.H;
     const int64_t per_cu = phase == 0 ? 3 : 2;
     int64_t runs = (per_cu * (int64_t)device_cus() + bh / 2) / bh;
