@@ -459,7 +459,9 @@ def bench_window_variants(dev, steps, warmup):
         at T1024;
       * the reference's float32 flow (no autocast: Q, K, V, out, dOut and
         every gradient float32; the split kernels with V as three terms
-        too) at the 117M layer, the 350M local layer and head dim 32."""
+        too) at the 117M layer, the 350M local layer and head dim 32;
+      * float16 throughout (two terms per value) at the 117M and 350M
+        layers."""
     def sets_for(B, H, T, D, W, flow, n=4, seed=11):
         raw = make_window_sets(n, B, T, H, D, dev, seed=seed)
         g = torch.Generator(device=dev).manual_seed(seed + 1)
@@ -469,7 +471,9 @@ def bench_window_variants(dev, steps, warmup):
                 v = s["V"].detach().float().requires_grad_(True) if flow == "f32" else s["V"]
                 s = dict(Q=s["Q"].detach().float().requires_grad_(True),
                          K=s["K"].detach().float().requires_grad_(True), V=v, dO=s["dO"].float())
-            dt = torch.bfloat16 if flow == "bf16" else torch.float32
+            if flow == "f16":
+                s = {k: s[k].detach().half().requires_grad_(k != "dO") for k in ("Q", "K", "V", "dO")}
+            dt = {"bf16": torch.bfloat16, "f16": torch.float16}.get(flow, torch.float32)
             s["dTau"] = (torch.randn(B, T, H, W, device=dev, generator=g) * 0.1).to(dt)
             out.append(s)
         return out
@@ -486,13 +490,15 @@ def bench_window_variants(dev, steps, warmup):
             ("d32_autocast_b32_t1024", (32, 4, 1024, 32, 32), "f32qk", False),
             ("117m_local_f32", (8, 12, 1024, 64, 64), "f32", False),
             ("350m_local_f32", (4, 16, 1024, 64, 256), "f32", False),
-            ("d32_f32_b32_t1024", (32, 4, 1024, 32, 32), "f32", False)):
+            ("d32_f32_b32_t1024", (32, 4, 1024, 32, 32), "f32", False),
+            ("117m_local_f16", (8, 12, 1024, 64, 64), "f16", False),
+            ("350m_local_f16", (4, 16, 1024, 64, 256), "f16", False)):
         sets = sets_for(B, H, T, D, W, flow)
         run = Runner([window_step_fn(s, W, math.sqrt(D), "mass", return_tau=tau) for s in sets])
         ms = time_units(run, max(steps, 40), warmup, f"variant:{name}")
         kernel = int(L.lib().tension_last_kernel())
         del run, sets
-        el_qk = 2 if flow == "bf16" else 4
+        el_qk = 2 if flow in ("bf16", "f16") else 4
         el_v = 4 if flow == "f32" else 2
         # compulsory bytes: fwd reads Q, K, V, writes out; bwd reads Q, K, V, dO,
         # writes dQ, dK, dV (out / dO / dQ / dK in Q's dtype, V / dV in V's)
@@ -502,15 +508,15 @@ def bench_window_variants(dev, steps, warmup):
             step_bytes += 2 * B * T * H * W * el_qk
         rows.append({"name": name, "B": B, "H": H, "T": T, "head_dim": D, "window": W,
                      "dtype_flow": {"f32qk": "fp32 Q/K/out/dOut, bf16 V/dV", "f32": "fp32 throughout",
-                                    "bf16": "bf16"}[flow],
+                                    "bf16": "bf16", "f16": "fp16 throughout"}[flow],
                      "tau_and_dtau": tau, "ms_per_step": round(ms, 5),
                      "tokens_per_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": step_bytes,
                      "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "kernel_family": {0: "exact", 1: "mfma_bf16", 2: "split_bf16", 3: "split_f32",
-                                       4: "split_f32v"}.get(kernel)})
+                                       4: "split_f32v", 5: "split_f16"}.get(kernel)})
         log(f"[bench] variant {rows[-1]}")
     return {"config": "window op at the reference's other shipped shapes (350M preset W256, head dim 32) "
-                      "and in its float32 flow",
+                      "and in its float32 flow (and float16)",
             "rows": rows}
 
 

@@ -31,7 +31,7 @@ TAU_VALID_ONLY = 1 << 5
 NOALLOC_SCRATCH_BYTES = 8 << 20
 
 # kernel families (tension_last_kernel)
-KERNEL_EXACT, KERNEL_MFMA, KERNEL_SPLIT_BF16, KERNEL_SPLIT_F32, KERNEL_SPLIT_F32V = 0, 1, 2, 3, 4
+KERNEL_EXACT, KERNEL_MFMA, KERNEL_SPLIT_BF16, KERNEL_SPLIT_F32, KERNEL_SPLIT_F32V, KERNEL_SPLIT_F16 = 0, 1, 2, 3, 4, 5
 
 # status codes
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3

@@ -28,6 +28,7 @@ SOURCES = [
     "split.hip", "split_fwd_bf16.hip", "split_dq_bf16.hip", "split_dkv_bf16.hip",
     "split_fwd_f32.hip", "split_dq_f32.hip", "split_dkv_f32.hip",
     "split_fwd_f32v.hip", "split_dq_f32v.hip", "split_dkv_f32v.hip",
+    "split_fwd_f16.hip", "split_dq_f16.hip", "split_dkv_f16.hip",
     "tau_export.hip", "graph_bias.hip", "aux_loss.hip",
     "exact_fwd_f32.hip", "exact_dq_f32.hip", "exact_dkv_f32.hip",
     "exact_fwd_f64.hip", "exact_dq_f64.hip", "exact_dkv_f64.hip",

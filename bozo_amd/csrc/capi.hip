@@ -67,11 +67,14 @@ bool any_f64(const tension_buf* a, const tension_buf* b, const tension_buf* c) {
   return is_f64(a) || is_f64(b) || is_f64(c);
 }
 
-bool aligned_bf16_rows(const tension_buf* b) {
-  if (!b || b->dtype != TENSION_BF16) return false;
+bool aligned_rows16(const tension_buf* b, int32_t dtype) {
+  if (!b || b->dtype != dtype) return false;
   if (((uintptr_t)b->ptr & 15) != 0) return false;
   return (b->s[0] % 8 == 0) && (b->s[1] % 8 == 0) && (b->s[2] % 8 == 0);
 }
+
+bool aligned_bf16_rows(const tension_buf* b) { return aligned_rows16(b, TENSION_BF16); }
+bool aligned_f16_rows(const tension_buf* b) { return aligned_rows16(b, TENSION_F16); }
 
 hipStream_t hs(tension_stream_t s) { return (hipStream_t)s; }
 
@@ -133,9 +136,10 @@ bool aligned_f32_rows(const tension_buf* b) {
 // local or global, every float32 value carried as three bf16 terms:
 // float32 Q / K with a bfloat16 V -- the reference's autocast flow,
 // float32 out / dOut / dQ / dK, bf16 dV -- (SPLIT_F32), float32 throughout
-// (SPLIT_F32V), or bf16 everywhere (SPLIT_BF16) for what the dedicated
-// bf16 kernels (head dim 64) do not take.
-enum { SPLIT_NONE = 0, SPLIT_BF16 = 1, SPLIT_F32 = 2, SPLIT_F32V = 3 };
+// (SPLIT_F32V), float16 throughout as two terms per value (SPLIT_F16), or
+// bf16 everywhere (SPLIT_BF16) for what the dedicated bf16 kernels (head
+// dim 64) do not take.
+enum { SPLIT_NONE = 0, SPLIT_BF16 = 1, SPLIT_F32 = 2, SPLIT_F32V = 3, SPLIT_F16 = 4 };
 
 int split_kind(const tension_buf* q, const tension_buf* k, const tension_buf* v, const tension_buf* bias,
                int64_t D, int flags) {
@@ -147,25 +151,30 @@ int split_kind(const tension_buf* q, const tension_buf* k, const tension_buf* v,
     return SPLIT_NONE;
   }
   if (aligned_bf16_rows(q) && aligned_bf16_rows(k) && aligned_bf16_rows(v)) return SPLIT_BF16;
+  if (aligned_f16_rows(q) && aligned_f16_rows(k) && aligned_f16_rows(v)) return SPLIT_F16;
   return SPLIT_NONE;
 }
 
-// A further operand of a split kernel: float32 rows with float32 Q / K,
-// bf16 rows with SPLIT_BF16 (outputs and gradients of Q / K / out).
+// Q's dtype in a split kernel
+int32_t split_qk_dtype(int kind) {
+  return kind == SPLIT_BF16 ? TENSION_BF16 : kind == SPLIT_F16 ? TENSION_F16 : TENSION_F32;
+}
+
+// A further operand of a split kernel: rows in Q's dtype (outputs and
+// gradients of Q / K / out).
 bool split_rows(int kind, const tension_buf* b) {
-  return kind == SPLIT_BF16 ? aligned_bf16_rows(b) : aligned_f32_rows(b);
+  const int32_t dt = split_qk_dtype(kind);
+  return dt == TENSION_F32 ? aligned_f32_rows(b) : aligned_rows16(b, dt);
 }
 
 // dV of a split kernel: rows in V's dtype.
 bool split_dv_rows(int kind, const tension_buf* b) {
-  return kind == SPLIT_F32V ? aligned_f32_rows(b) : aligned_bf16_rows(b);
+  return kind == SPLIT_F32V ? aligned_f32_rows(b) : kind == SPLIT_F16 ? aligned_f16_rows(b) : aligned_bf16_rows(b);
 }
 
 // tau / dtau of a split kernel: absent, or in Q's dtype (the kernels index
 // them as typed rows).
-bool split_side(int kind, const tension_buf* b) {
-  return !b || b->dtype == (kind == SPLIT_BF16 ? TENSION_BF16 : TENSION_F32);
-}
+bool split_side(int kind, const tension_buf* b) { return !b || b->dtype == split_qk_dtype(kind); }
 
 // Local windows wider than one 64-row tile run on the split kernels in bf16
 // too: 14-20% faster per fwd+bwd step than the dedicated band kernels'
@@ -182,7 +191,14 @@ bool wide_on_split(bool global, int64_t W) {
 #endif
 }
 
-enum { KERNEL_EXACT = 0, KERNEL_MFMA = 1, KERNEL_SPLIT_BF16 = 2, KERNEL_SPLIT_F32 = 3, KERNEL_SPLIT_F32V = 4 };
+enum {
+  KERNEL_EXACT = 0,
+  KERNEL_MFMA = 1,
+  KERNEL_SPLIT_BF16 = 2,
+  KERNEL_SPLIT_F32 = 3,
+  KERNEL_SPLIT_F32V = 4,
+  KERNEL_SPLIT_F16 = 5
+};
 
 thread_local int g_last_kernel = -1;
 
@@ -192,7 +208,8 @@ int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_
   // a larger one runs on the exact kernels
   BandArgs probe;
   if (kind != KERNEL_EXACT && phase != 3 && !band_args(p, &probe)) kind = KERNEL_EXACT;
-  int r = kind == KERNEL_SPLIT_F32V   ? launch_split(phase, SPLIT_FLOW_F32V, p, hs(stream), &e)
+  int r = kind == KERNEL_SPLIT_F16    ? launch_split(phase, SPLIT_FLOW_F16, p, hs(stream), &e)
+          : kind == KERNEL_SPLIT_F32V ? launch_split(phase, SPLIT_FLOW_F32V, p, hs(stream), &e)
           : kind == KERNEL_SPLIT_F32  ? launch_split(phase, SPLIT_FLOW_F32, p, hs(stream), &e)
           : kind == KERNEL_SPLIT_BF16 ? launch_split(phase, SPLIT_FLOW_BF16, p, hs(stream), &e)
           : kind == KERNEL_MFMA       ? launch_mfma(phase, p, hs(stream), &e)
@@ -207,7 +224,10 @@ int run_band(int phase, int kind, bool f64, const BandParams& p, tension_stream_
 }
 
 int split_kernel(int kind) {
-  return kind == SPLIT_F32V ? KERNEL_SPLIT_F32V : kind == SPLIT_F32 ? KERNEL_SPLIT_F32 : KERNEL_SPLIT_BF16;
+  return kind == SPLIT_F16    ? KERNEL_SPLIT_F16
+         : kind == SPLIT_F32V ? KERNEL_SPLIT_F32V
+         : kind == SPLIT_F32  ? KERNEL_SPLIT_F32
+                              : KERNEL_SPLIT_BF16;
 }
 
 // ---------------------------------------------------------------- forward
@@ -335,7 +355,7 @@ int band_bwd_dq(const tension_buf* q, const tension_buf* k, const tension_buf* v
     TRY(check_buf(mass, "mass", true, -1));
     const bool f32_mass = mass->dtype == TENSION_F32;
     const bool rows_mf = mf && global && aligned_bf16_rows(out) && f32_mass;
-    const bool rows_sp = sp && sk != SPLIT_BF16 && ((flags & TENSION_NORM_MASS) || global) &&
+    const bool rows_sp = sp && (sk == SPLIT_F32 || sk == SPLIT_F32V) && ((flags & TENSION_NORM_MASS) || global) &&
                          aligned_f32_rows(out) && f32_mass;
     if (rows_mf || rows_sp) {
       p.out = make_buf(out);

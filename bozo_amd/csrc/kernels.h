@@ -83,9 +83,9 @@ int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err)
 int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32 = false);
 // split-operand kernels (split_band.h), by flow: SPLIT_FLOW_BF16 bf16
 // throughout, SPLIT_FLOW_F32 float32 Q / K / dOut with a bfloat16 V,
-// SPLIT_FLOW_F32V float32 Q / K / V / dOut; head dim 32 or 64; phase 0
-// forward, 1 dQ, 2 dK / dV
-enum { SPLIT_FLOW_BF16 = 0, SPLIT_FLOW_F32 = 1, SPLIT_FLOW_F32V = 2 };
+// SPLIT_FLOW_F32V float32 Q / K / V / dOut, SPLIT_FLOW_F16 float16
+// throughout; head dim 32 or 64; phase 0 forward, 1 dQ, 2 dK / dV
+enum { SPLIT_FLOW_BF16 = 0, SPLIT_FLOW_F32 = 1, SPLIT_FLOW_F32V = 2, SPLIT_FLOW_F16 = 3 };
 int launch_split(int phase, int flow, const BandParams& p, hipStream_t st, hipError_t* err);
 // Compute units of the current device (queried once per device).
 int device_cus();

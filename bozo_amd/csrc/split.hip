@@ -13,9 +13,12 @@ void launch_split_dkv_f32(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_fwd_f32v(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_dq_f32v(const BandParams& p, hipStream_t st, unsigned n);
 void launch_split_dkv_f32v(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_fwd_f16(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dq_f16(const BandParams& p, hipStream_t st, unsigned n);
+void launch_split_dkv_f16(const BandParams& p, hipStream_t st, unsigned n);
 
 int launch_split(int phase, int flow, const BandParams& p_in, hipStream_t st, hipError_t* err) {
-  if (flow != SPLIT_FLOW_BF16 && flow != SPLIT_FLOW_F32 && flow != SPLIT_FLOW_F32V) return -1;
+  if (flow < SPLIT_FLOW_BF16 || flow > SPLIT_FLOW_F16) return -1;
   if (phase < 0 || phase > 2) return -1;
   BandArgs probe;
   if (!band_args(p_in, &probe)) return -1;  // the kernels take 32-bit strides
@@ -49,10 +52,11 @@ int launch_split(int phase, int flow, const BandParams& p_in, hipStream_t st, hi
   }
   const unsigned n = (unsigned)nwg;
   typedef void (*Launch)(const BandParams&, hipStream_t, unsigned);
-  static const Launch table[3][3] = {
+  static const Launch table[4][3] = {
       {launch_split_fwd_bf16, launch_split_dq_bf16, launch_split_dkv_bf16},
       {launch_split_fwd_f32, launch_split_dq_f32, launch_split_dkv_f32},
-      {launch_split_fwd_f32v, launch_split_dq_f32v, launch_split_dkv_f32v}};
+      {launch_split_fwd_f32v, launch_split_dq_f32v, launch_split_dkv_f32v},
+      {launch_split_fwd_f16, launch_split_dq_f16, launch_split_dkv_f16}};
   table[flow][phase](p, st, n);
   *err = hipGetLastError();
   return 0;

@@ -2,6 +2,9 @@
 // v_mfma_f32_16x16x32_bf16 as a sum of NT bf16 terms.
 //
 //   NT = 1  bf16 tensors, taken as stored;
+//   NT = 2  float16 tensors, split as x = t0 + t1 with t0 = bf16(x),
+//           t1 = bf16(x - t0): exact (11 significant bits in two terms of
+//           8, the exponent range of bf16 covers float16's);
 //   NT = 3  float32 tensors, split on their way into registers or LDS as
 //           x = t0 + t1 + t2 + r with t0 = bf16(x), t1 = bf16(x - t0),
 //           t2 = bf16(x - t0 - t1) (both differences are exact in float32)
@@ -21,8 +24,11 @@
 //
 // NV: the terms of V (and the element of dV), 1 for a bf16 V as above, 3
 // for a float32 V (the reference's float32 flow, no autocast: every input
-// and gradient float32).  Products with V then keep t_i v_j with
-// i + j <= 2, and dV, float32 too, keeps L = 2.
+// and gradient float32), 2 for a float16 V (float16 throughout).  Products
+// with V then keep t_i v_j with i + j <= 2, and so does dV.  With NT = 2
+// every product of two float16 operands is exact (all four terms); the
+// fp32 P, P' and G fed to the second products go in as two terms
+// (residual <= 2^-18 relative, below float16's own rounding).
 //
 // Head dim D = 32 or 64: LDS tiles are 64 rows x 64 bf16 (direct tiles,
 // mfma_common.h); D = 32 fills the first four 16-byte chunks of each row
@@ -41,7 +47,19 @@ namespace tension {
 namespace split {
 
 template <int NT>
-using Elem = typename std::conditional<NT == 1, bf16, float>::type;
+using Elem = typename std::conditional<NT == 1, bf16, typename std::conditional<NT == 2, f16, float>::type>::type;
+
+typedef f16 f16x8v __attribute__((ext_vector_type(8)));
+typedef f16 f16x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned short f16_bits(f16 x) { return __builtin_bit_cast(unsigned short, x); }
+
+// 8 float16 values (as stored) as float32 (whole-vector bit cast)
+__device__ __forceinline__ void f16x8_to_f32(const u16x8& u, float* x) {
+  const f16x8v h = __builtin_bit_cast(f16x8v, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (float)h[e];
+}
 
 // ----------------------------------------------------------------- terms
 
@@ -52,11 +70,11 @@ __device__ __forceinline__ void split8(const float* x, u16x8* t) {
   for (int e = 0; e < 8; ++e) {
     const bf16 h = (bf16)x[e];
     t[0][e] = bf16_bits(h);
-    if constexpr (NT == 3) {
+    if constexpr (NT >= 2) {
       const float r = x[e] - (float)h;
       const bf16 m = (bf16)r;
       t[1][e] = bf16_bits(m);
-      t[2][e] = bf16_bits((bf16)(r - (float)m));
+      if constexpr (NT == 3) t[2][e] = bf16_bits((bf16)(r - (float)m));
     }
   }
 }
@@ -111,6 +129,10 @@ struct RawFrag<1> {
   u16x8 a;
 };
 template <>
+struct RawFrag<2> {
+  u16x8 a;
+};
+template <>
 struct RawFrag<3> {
   f32x4 a, b;
 };
@@ -120,7 +142,7 @@ __device__ __forceinline__ RawFrag<NT> frag_load(const Elem<NT>* base, int64_t r
   RawFrag<NT> x;
   const bool ok = row >= 0 && row < T;
   const Elem<NT>* src = base + (int64_t)row * rs + 8 * chunk;
-  if constexpr (NT == 1) {
+  if constexpr (NT != 3) {
     x.a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
     if (ok) x.a = *(const u16x8*)src;
   } else {
@@ -138,7 +160,16 @@ __device__ __forceinline__ void frag_terms(const RawFrag<NT>& x, bf16x8* t) {
   if constexpr (NT == 1) {
     t[0] = __builtin_bit_cast(bf16x8, x.a);
   } else {
-    const float v[8] = {x.a[0], x.a[1], x.a[2], x.a[3], x.b[0], x.b[1], x.b[2], x.b[3]};
+    float v[8];
+    if constexpr (NT == 2) {
+      f16x8_to_f32(x.a, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = x.a[e];
+        v[4 + e] = x.b[e];
+      }
+    }
     u16x8 u[NT];
     split8<NT>(v, u);
 #pragma unroll
@@ -155,11 +186,15 @@ __device__ __forceinline__ void frag_row(const Elem<NT>* base, int64_t rs, int r
 // ----------------------------------------------------------------- staging
 
 // A thread's two staged rows (staged_row(tid), +8; chunk tid % 8) of a
-// 64-row tile as loaded: bf16 (NT = 1) or float32 (NT = 3).
+// 64-row tile as loaded: bf16 (NT = 1), float16 (NT = 2) or float32 (NT = 3).
 template <int NT>
 struct Raw;
 template <>
 struct Raw<1> {
+  u16x8 a, b;
+};
+template <>
+struct Raw<2> {
   u16x8 a, b;
 };
 template <>
@@ -175,7 +210,7 @@ __device__ __forceinline__ Raw<NT> load_raw(const Elem<NT>* base, int64_t rs, in
   const bool okc = ch < D / 8;
   const bool oka = okc && ra >= 0 && ra < T, okb = okc && rb >= 0 && rb < T;
   Raw<NT> x;
-  if constexpr (NT == 1) {
+  if constexpr (NT != 3) {
     x.a = x.b = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
     if (oka) x.a = *(const u16x8*)(base + (int64_t)ra * rs + 8 * ch);
     if (okb) x.b = *(const u16x8*)(base + (int64_t)rb * rs + 8 * ch);
@@ -199,8 +234,19 @@ __device__ __forceinline__ void store_raw(const Raw<NT>& x, bf16* tile0, int tid
   if constexpr (NT == 1) {
     tile_store_direct(TileRegs{x.a, x.b}, tile0, tid);
   } else {
-    const float a[8] = {x.a0[0], x.a0[1], x.a0[2], x.a0[3], x.a1[0], x.a1[1], x.a1[2], x.a1[3]};
-    const float b[8] = {x.b0[0], x.b0[1], x.b0[2], x.b0[3], x.b1[0], x.b1[1], x.b1[2], x.b1[3]};
+    float a[8], b[8];
+    if constexpr (NT == 2) {
+      f16x8_to_f32(x.a, a);
+      f16x8_to_f32(x.b, b);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[e] = x.a0[e];
+        a[4 + e] = x.a1[e];
+        b[e] = x.b0[e];
+        b[4 + e] = x.b1[e];
+      }
+    }
     u16x8 ta[NT], tb[NT];
     split8<NT>(a, ta);
     split8<NT>(b, tb);
@@ -219,7 +265,10 @@ __device__ __forceinline__ void store_acc(O* row, const f32x4* acc, float f, int
     } else {
       u16x4 o;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)(acc[m][r] * f));
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (std::is_same<O, f16>::value) o[r] = f16_bits((f16)(acc[m][r] * f));
+        else o[r] = bf16_bits((bf16)(acc[m][r] * f));
+      }
       *(u16x4*)(row + 16 * m + 4 * g) = o;
     }
   }
@@ -320,7 +369,10 @@ __device__ __forceinline__ void stage_put4(E* st, int c, int j, int g, const flo
   } else {
     u16x4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = bf16_bits((bf16)v[r]);
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (std::is_same<E, f16>::value) o[r] = f16_bits((f16)v[r]);
+      else o[r] = bf16_bits((bf16)v[r]);
+    }
     *(u16x4*)at = o;
   }
 }
@@ -331,6 +383,10 @@ __device__ __forceinline__ void stage_get4(const E* st, int c, int j, int g, flo
   if constexpr (std::is_same<E, float>::value) {
     const f32x4 x = *(const f32x4*)at;
     v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+  } else if constexpr (std::is_same<E, f16>::value) {
+    const f16x4v x = __builtin_bit_cast(f16x4v, *(const u16x4*)at);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = (float)x[r];
   } else {
     // bit-cast the whole vector (a bit_cast of one subscripted element has
     // compiled to element 0 for every index on this toolchain)

@@ -1,0 +1,11 @@
+// Instantiates the split-operand band kernels (split_band.h) for phase
+// fwd, float16 Q / K / V / dOut (two bf16 terms per value).
+#include "split_band.h"
+
+namespace tension {
+
+void launch_split_fwd_f16(const BandParams& p, hipStream_t st, unsigned n) {
+  split::launch<2, 2, 0>(p, st, n);
+}
+
+}  // namespace tension

@@ -99,8 +99,8 @@ _EXACT_WARNED = set()
 
 def _note_exact_path(what: str, Q: Tensor, K: Tensor, V: Tensor, pairs: int) -> None:
     """Warn once per dtype / head-dim combination when a large call ran on the
-    exact kernels (one thread per row, no MFMA): float16, mixes other than
-    float32 Q / K with a bf16 or float32 V, head dims other than 32 / 64 or
+    exact kernels (one thread per row, no MFMA): mixes other than float32
+    Q / K with a bf16 or float32 V, head dims other than 32 / 64 or
     unaligned rows.  float64 is exact on purpose."""
     if pairs < (1 << 20) or Q.dtype == torch.float64:
         return
@@ -112,8 +112,8 @@ def _note_exact_path(what: str, Q: Tensor, K: Tensor, V: Tensor, pairs: int) -> 
     _EXACT_WARNED.add(key)
     import warnings
     warnings.warn(f"{what}: Q/K/V {Q.dtype}/{K.dtype}/{V.dtype} with head dim {Q.shape[-1]} ran on the exact "
-                  "(non-MFMA) kernels, one thread per row; the MFMA kernels take bf16, or float32 Q/K with "
-                  "a bf16 or float32 V, at head dim 32 or 64 with 16-byte aligned rows", RuntimeWarning,
+                  "(non-MFMA) kernels, one thread per row; the MFMA kernels take bf16, float16, or float32 "
+                  "Q/K with a bf16 or float32 V, at head dim 32 or 64 with 16-byte aligned rows", RuntimeWarning,
                   stacklevel=3)
 
 

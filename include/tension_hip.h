@@ -360,7 +360,8 @@ enum {
   TENSION_KERNEL_MFMA = 1,       /* dedicated bf16 kernels, head dim 64 */
   TENSION_KERNEL_SPLIT_BF16 = 2, /* split-operand kernels, bf16, head dim 32 / 64 */
   TENSION_KERNEL_SPLIT_F32 = 3,  /* split-operand kernels, float32 Q / K with bf16 V */
-  TENSION_KERNEL_SPLIT_F32V = 4  /* split-operand kernels, float32 Q / K / V */
+  TENSION_KERNEL_SPLIT_F32V = 4, /* split-operand kernels, float32 Q / K / V */
+  TENSION_KERNEL_SPLIT_F16 = 5   /* split-operand kernels, float16 Q / K / V */
 };
 int tension_last_kernel(void);
 
