@@ -4,19 +4,23 @@ Forty-eight configurations drawn once from a fixed generator cover the
 space the targeted tests in test_window_gpu.py sample by hand: batch and
 head counts that change the launch geometry, ragged T around the 64-row
 tiles, windows below, at and above 64 (the fused single-pass backward, the
-split backward, the exact kernels), head dims 64 and 32, bfloat16 and
-float32, every normalisation, with and without the bias, with and without
-tau and its gradient.  Sixteen more run the split-operand kernels of the
+split backward), head dims 64 and 32, bfloat16 and float32 (the
+float32 flow: the split kernels with every operand as three bf16 terms),
+every normalisation, with and without the bias, with and without tau and
+its gradient.  Sixteen more run the split-operand kernels of the
 reference's autocast flow (float32 Q / K, bfloat16 V) at head dims 32 and
-64 and windows up to 300.  Tolerances are the ones of test_window_gpu.py
-(float32 max-abs 1e-5 absolute, raw sums included; bfloat16 2e-2 relative
-L2; tau elementwise), checked against the same oracle functions.
+64 and windows up to 300, and twelve float16 throughout.  Tolerances are
+the ones of test_window_gpu.py (float32 max-abs 1e-5 absolute, raw sums
+included; bfloat16 2e-2 relative L2; tau elementwise) and of
+test_float16_flow_gpu.py (float16 1e-3 relative L2, tau 2^-11), checked
+against the same oracle functions.
 """
 import numpy as np
 import pytest
 import torch
 
 from tests._util import f64, make_inputs, max_abs
+from tests.test_float16_flow_gpu import check as check_f16
 from tests.test_window_gpu import check_bf16, check_mixed, hip_run, mixed_inputs, oracle_run
 
 pytestmark = pytest.mark.gpu
@@ -111,3 +115,20 @@ def test_window_sweep_mixed(dev, case):
     hip = hip_run(inp, W, scale, dev, normalize=norm, return_tau=tau, use_bias=bias, use_dtau=tau)
     ref = oracle_run(inp, W, scale, normalize=norm, use_bias=bias, use_dtau=tau)
     check_mixed(hip, ref, tau)
+
+
+F16 = _draw_mixed(12, 2028)
+
+
+@pytest.mark.parametrize("case", F16, ids=[f"{c[0]}-B{c[1]}H{c[2]}T{c[3]}W{c[4]}D{c[5]}-{c[6]}"
+                                           f"{'-bias' if c[7] else ''}{'-tau' if c[8] else ''}" for c in F16])
+def test_window_sweep_f16(dev, case):
+    i, B, H, T, W, D, norm, bias, tau = case
+    inp = make_inputs(B, T, H, D, seed=400 + i, std=0.5, dtype=torch.float16, W=W,
+                      dtau_std=0.1 if tau else None, bias_std=0.5 if bias else None,
+                      bias_shape=(B, T, W) if bias else None)
+    scale = float(np.sqrt(D))
+    print(f"[sweep f16 {case}]", flush=True)
+    hip = hip_run(inp, W, scale, dev, normalize=norm, return_tau=tau, use_bias=bias, use_dtau=tau)
+    ref = oracle_run(inp, W, scale, normalize=norm, use_bias=bias, use_dtau=tau)
+    check_f16(hip, ref, tau)
