@@ -617,7 +617,7 @@ def _phase_regions(cur):
             msg = json.loads(ext or "{}").get("message", "")
         except ValueError:
             msg = ""
-        if msg.startswith(("step", "kernel:", "global", "decode", "model:")):
+        if msg.startswith(("step", "kernel:", "variant:", "global", "decode", "model:")):
             out.append((msg, a, b))
     return out
 
