@@ -1499,7 +1499,7 @@ void launch_norm(const BandParams& p, hipStream_t st, unsigned n) {
       if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
       else if (p.coef_pre) XB_BT(xb_dq, , 3);
       else XB_BT(xb_dq, , 2);
-    } else {  // bf16 rows: the coefficients from the band (a bf16 out would cancel)
+    } else {  // bf16 / fp16 rows: the coefficients from the band (a 16-bit out would cancel)
       if (!p.glob && p.win <= kTile) XB_BT(xb_dq, , 1);
       else XB_BT(xb_dq, , 2);
     }
