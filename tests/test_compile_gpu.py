@@ -28,7 +28,9 @@ def qkv(B, T, H, D, dtype, dev, seed, requires_grad=False):
 @pytest.mark.parametrize("dtype,W,tau,flags,bias", [
     (torch.bfloat16, 64, True, 1, False),   # MFMA kernels, tau-mass
     (torch.bfloat16, 64, False, 2, False),  # MFMA, valid-count
-    (torch.float32, 17, True, 0, True),     # exact kernels, raw sum, bias
+    (torch.float32, 17, True, 0, True),     # split kernels (float32 flow), raw sum, bias
+    (torch.float16, 100, True, 1, False),   # split kernels (float16), tau-mass, W > 64
+    (torch.float64, 9, False, 1, False),    # exact kernels
 ])
 def test_opcheck_window(dev, dtype, W, tau, flags, bias):
     B, T, H, D = 2, 200, 3, 64
