@@ -590,27 +590,45 @@ int tension_decode_step(const tension_buf* q, const tension_buf* k_new, const te
   p.pos_in = pos_in; p.pos_out = pos_out;
   p.N = (int)N; p.H = (int)H; p.D = (int)D; p.W = (int)W;
   p.scale = scale; p.inv_scale = (float)(1.0 / scale); p.flags = flags;
-  auto a16 = [](const tension_buf* b, bool four) {
-    if (b->dtype != TENSION_BF16 || ((uintptr_t)b->ptr & 15)) return false;
+  // 16-byte aligned rows of a 16-bit dtype (bf16 or float16)
+  auto a16 = [](const tension_buf* b, bool four, int32_t dt) {
+    if (b->dtype != dt || ((uintptr_t)b->ptr & 15)) return false;
     return b->s[0] % 8 == 0 && b->s[1] % 8 == 0 && (!four || b->s[2] % 8 == 0);
   };
-  // the fast kernel reads each (n, h) cache slab through a buffer descriptor
-  // of W * row_stride * 2 bytes (31-bit range, rows of at least 64 elements)
-  auto slab_fits = [&](const tension_buf* b) { return b->s[2] >= 64 && mul_cap(W, b->s[2], (1 << 30) - 1) >= 0; };
-  const bool fast = !(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 1024 && a16(q, false) &&
-                    a16(k_new, false) && a16(v_new, false) && a16(out, false) && a16(k_cache, true) &&
-                    a16(v_cache, true) && slab_fits(k_cache) && slab_fits(v_cache);
-  // the reference's autocast flow: float32 q / K (promoted by RoPE), bf16 V
-  auto f16b = [](const tension_buf* b, bool four) {  // 16-byte aligned float32 rows
+  // 16-byte aligned float32 rows
+  auto a32 = [](const tension_buf* b, bool four) {
     if (b->dtype != TENSION_F32 || ((uintptr_t)b->ptr & 15)) return false;
     return b->s[0] % 4 == 0 && b->s[1] % 4 == 0 && (!four || b->s[2] % 4 == 0);
   };
-  const bool kf32 = !fast && !(flags & TENSION_FORCE_EXACT) && !(flags & TENSION_DECODE_SELF) && D == 64 &&
-                    W <= 1024 && f16b(q, false) && f16b(k_new, false) && f16b(out, false) && f16b(k_cache, true) &&
-                    a16(v_new, false) && a16(v_cache, true) && k_cache->s[2] >= 64 &&
-                    mul_cap(W, k_cache->s[2], (1 << 29) - 1) >= 0 && slab_fits(v_cache);
+  // the fast kernel reads each (n, h) cache slab through a buffer descriptor
+  // of W * row_stride * element bytes (31-bit range, rows of at least 64
+  // elements)
+  auto slab_fits = [&](const tension_buf* b, int el) {
+    return b->s[2] >= 64 && mul_cap(W, b->s[2], ((int64_t)1 << 31) / el - 1) >= 0;
+  };
+  auto all16 = [&](int32_t dt) {
+    return a16(q, false, dt) && a16(k_new, false, dt) && a16(v_new, false, dt) && a16(out, false, dt) &&
+           a16(k_cache, true, dt) && a16(v_cache, true, dt) && slab_fits(k_cache, 2) && slab_fits(v_cache, 2);
+  };
+  const bool f32qk = a32(q, false) && a32(k_new, false) && a32(out, false) && a32(k_cache, true) &&
+                     slab_fits(k_cache, 4);
+  int flow = DECODE_EXACT;
+  if (!(flags & TENSION_FORCE_EXACT) && D == 64 && W <= 1024) {
+    if (all16(TENSION_BF16)) {
+      flow = DECODE_BF16;
+    } else if (all16(TENSION_F16)) {
+      flow = DECODE_F16;
+    } else if (f32qk && !(flags & TENSION_DECODE_SELF)) {
+      // the reference's autocast flow: float32 q / K (promoted by RoPE), bf16
+      // V; or float32 throughout (no autocast)
+      if (a16(v_new, false, TENSION_BF16) && a16(v_cache, true, TENSION_BF16) && slab_fits(v_cache, 2))
+        flow = DECODE_KF32;
+      else if (W <= 512 && a32(v_new, false) && a32(v_cache, true) && slab_fits(v_cache, 4))
+        flow = DECODE_F32;
+    }
+  }
   hipError_t e = hipSuccess;
-  launch_decode(fast || kf32, is_f64(q) || is_f64(k_cache) || is_f64(v_cache), p, hs(stream), &e, kf32);
+  launch_decode(flow, is_f64(q) || is_f64(k_cache) || is_f64(v_cache), p, hs(stream), &e);
   return launched(e, "tension_decode_step");
 }
 

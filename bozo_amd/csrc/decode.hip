@@ -75,11 +75,25 @@ struct DecodeFastArgs {
   float inv_scale;
 };
 
-template <int NW, int NP, bool KF32 = false, bool SELF = false>
-__global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
+// FLOW (the element types of one step): kDecodeBF16 -- bf16 throughout;
+// kDecodeKF32 -- float32 q / K / out, bf16 V (KF32 above); kDecodeF32 --
+// float32 throughout (the reference's flow without autocast: V rows of 256
+// bytes too); kDecodeF16 -- float16 throughout (the bf16 layout, float16
+// arithmetic conversions).  SELF with bf16 or float16 only.
+enum { kDecodeBF16 = 0, kDecodeKF32 = 1, kDecodeF32 = 2, kDecodeF16 = 3 };
+
+template <int NW, int NP, int FLOW, bool SELF>
+__device__ __forceinline__ void decode_d64_body(const DecodeFastArgs& p) {
+  constexpr bool KF32 = FLOW == kDecodeKF32 || FLOW == kDecodeF32;
+  constexpr bool VF32 = FLOW == kDecodeF32;
+  constexpr bool H16 = FLOW == kDecodeF16;  // the 16-bit element is float16
+  static_assert(!(SELF && KF32), "the self-key step takes 16-bit rows");
   constexpr int kRows = 8 * NW;  // cache rows per pass
   constexpr int kKBytes = KF32 ? 4 : 2;   // bytes per K / q / out element
   constexpr int kKChunks = KF32 ? 16 : 8;  // 16-byte chunks of a K row
+  constexpr int kVBytes = VF32 ? 4 : 2;   // bytes per V element
+  constexpr int kVChunks = VF32 ? 16 : 8;  // 16-byte chunks of a V row
+  using VE = typename std::conditional<VF32, float, bf16>::type;  // V addressing (16-bit: bf16 or float16)
   __shared__ float red[NW * 4][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int ch = lane & 7, rw = lane >> 3;  // d-chunk, row within a pass
@@ -107,11 +121,11 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
       (void*)((const char*)p.kn + ((int64_t)n * p.kn_n + (int64_t)h * p.kn_h) * kKBytes), (short)0, 16 * kKChunks,
       kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vnr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const bf16*)p.vn + (int64_t)n * p.vn_n + (int64_t)h * p.vn_h), (short)0, 128, kRawBufWord3);
+      (void*)((const VE*)p.vn + (int64_t)n * p.vn_n + (int64_t)h * p.vn_h), (short)0, 16 * kVChunks, kRawBufWord3);
   const u16x8 knew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
       knr, (ai >= 0 && ai < kKChunks) ? 16 * ai : 16 * kKChunks, 0, 0));
   const u16x8 vnew = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-      vnr, (ai >= kKChunks && ai < kKChunks + 8) ? 16 * (ai - kKChunks) : 128, 0, 0));
+      vnr, (ai >= kKChunks && ai < kKChunks + kVChunks) ? 16 * (ai - kKChunks) : 16 * kVChunks, 0, 0));
 
   // One descriptor per cache slab; loads of rows past its range return
   // zeros.  The range is W rows, or, for a self-key step (a global layer's
@@ -125,16 +139,16 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
     rows = pe < W ? pe : W;
   }
   const char* kbase = (const char*)p.kc + ((int64_t)n * p.kc_n + (int64_t)h * p.kc_h) * kKBytes;
-  const bf16* vbase = (const bf16*)p.vc + (int64_t)n * p.vc_n + (int64_t)h * p.vc_h;
+  const VE* vbase = (const VE*)p.vc + (int64_t)n * p.vc_n + (int64_t)h * p.vc_h;
   const __amdgpu_buffer_rsrc_t kr_ = __builtin_amdgcn_make_buffer_rsrc(
       (void*)kbase, (short)0, (int)((int64_t)rows * p.kc_w * kKBytes), kRawBufWord3);
   const __amdgpu_buffer_rsrc_t vr_ = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)vbase, (short)0, (int)((int64_t)rows * p.vc_w * 2), kRawBufWord3);
+      (void*)vbase, (short)0, (int)((int64_t)rows * p.vc_w * kVBytes), kRawBufWord3);
   const uint32_t row0 = (uint32_t)(wave * 8 + rw);
-  const uint32_t kstep = (uint32_t)(kRows * p.kc_w * kKBytes), vstep = (uint32_t)(kRows * p.vc_w * 2);
+  const uint32_t kstep = (uint32_t)(kRows * p.kc_w * kKBytes), vstep = (uint32_t)(kRows * p.vc_w * kVBytes);
   const uint32_t koff = row0 * (uint32_t)(p.kc_w * kKBytes) + 8 * kKBytes * ch;
-  const uint32_t voff = row0 * (uint32_t)(p.vc_w * 2) + 16 * ch;
-  u16x8 kr[NP], kr2[KF32 ? NP : 1], vr[NP];
+  const uint32_t voff = row0 * (uint32_t)(p.vc_w * kVBytes) + 8 * kVBytes * ch;
+  u16x8 kr[NP], kr2[KF32 ? NP : 1], vr[NP], vr2[VF32 ? NP : 1];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     kr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(kr_, (int)(koff + i * kstep), 0, kCacheAux));
@@ -143,8 +157,12 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
                                                                                kCacheAux));
   }
 #pragma unroll
-  for (int i = 0; i < NP; ++i)
+  for (int i = 0; i < NP; ++i) {
     vr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(vr_, (int)(voff + i * vstep), 0, kCacheAux));
+    if constexpr (VF32)
+      vr2[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(vr_, (int)(voff + i * vstep + 16), 0,
+                                                                               kCacheAux));
+  }
 
   const int pos = p.pos_in[n] > 0 ? p.pos_in[n] : 0;
   const int live = pos < W ? pos : W;  // slots [0, live) hold tokens
@@ -158,6 +176,10 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
       q[e] = qa[e] * p.inv_scale;
       q[4 + e] = qb[e] * p.inv_scale;
     }
+  } else if constexpr (H16) {
+    const f16x8 qv = __builtin_bit_cast(f16x8, qbits);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = (float)qv[e] * p.inv_scale;
   } else {
     const bf16x8 qv = __builtin_bit_cast(bf16x8, qbits);
 #pragma unroll
@@ -173,6 +195,10 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
       const f32x4 ka = __builtin_bit_cast(f32x4, kr[i]), kb = __builtin_bit_cast(f32x4, kr2[i]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) part += q[e] * ka[e] + q[4 + e] * kb[e];
+    } else if constexpr (H16) {
+      const f16x8 kv = __builtin_bit_cast(f16x8, kr[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += q[e] * (float)kv[e];
     } else {
       const bf16x8 kv = __builtin_bit_cast(bf16x8, kr[i]);
 #pragma unroll
@@ -190,9 +216,22 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
       }
     }
     msum += tau;
-    const bf16x8 vv = __builtin_bit_cast(bf16x8, vr[i]);
+    if constexpr (VF32) {
+      const f32x4 va = __builtin_bit_cast(f32x4, vr[i]), vb = __builtin_bit_cast(f32x4, vr2[i]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vv[e];
+      for (int e = 0; e < 4; ++e) {
+        acc[e] += tau * va[e];
+        acc[4 + e] += tau * vb[e];
+      }
+    } else if constexpr (H16) {
+      const f16x8 vv = __builtin_bit_cast(f16x8, vr[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vv[e];
+    } else {
+      const bf16x8 vv = __builtin_bit_cast(bf16x8, vr[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += tau * (float)vv[e];
+    }
   }
   // TENSION_DECODE_SELF: the new token is a key too (global layers attend to
   // s <= t).  Wave 1 holds its k row in lanes 0-7 and its v row in lanes
@@ -201,16 +240,30 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
   // scale their v chunk; the results meet the cache sums in LDS.
   __shared__ float sred[65];
   if (!KF32 && self_key && wave == 1) {
-    const bf16x8 kv = __builtin_bit_cast(bf16x8, knew);
+    float kx[8], vx[8];
+    if constexpr (H16) {
+      const f16x8 kv = __builtin_bit_cast(f16x8, knew), vv = __builtin_bit_cast(f16x8, vnew);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kx[e] = (float)kv[e];
+        vx[e] = (float)vv[e];
+      }
+    } else {
+      const bf16x8 kv = __builtin_bit_cast(bf16x8, knew), vv = __builtin_bit_cast(bf16x8, vnew);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kx[e] = (float)kv[e];
+        vx[e] = (float)vv[e];
+      }
+    }
     float part = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part += q[e] * (float)kv[e];
+    for (int e = 0; e < 8; ++e) part += q[e] * kx[e];
     const float ts = sigmoid_fast(row_sum8(part));
     const float tv = dpp_move<0x128>(ts);  // lanes 8-15 <- lanes 0-7
     if (lane >= 8 && lane < 16) {
-      const bf16x8 vv = __builtin_bit_cast(bf16x8, vnew);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sred[8 * (lane - 8) + e] = tv * (float)vv[e];
+      for (int e = 0; e < 8; ++e) sred[8 * (lane - 8) + e] = tv * vx[e];
     }
     if (lane == 0) sred[64] = ts;
   }
@@ -243,23 +296,38 @@ __global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
     const float inv = decode_norm(p.flags, m, live + (self_key ? 1 : 0));
     if constexpr (KF32) {
       ((float*)p.out)[(int64_t)n * p.out_n + (int64_t)h * p.out_h + tid] = o * inv;
+    } else if constexpr (H16) {
+      f16* orow = (f16*)p.out + (int64_t)n * p.out_n + (int64_t)h * p.out_h;
+      orow[tid] = (f16)(o * inv);
     } else {
       bf16* orow = (bf16*)p.out + (int64_t)n * p.out_n + (int64_t)h * p.out_h;
       orow[tid] = (bf16)(o * inv);
     }
-  } else if (ai < kKChunks + 8) {
+  } else if (ai < kKChunks + kVChunks) {
     // append k_new / v_new at slot pos % W (16 bytes per lane)
     const int slot = pos % W;
     if (ai < kKChunks) {
       char* dst = (char*)p.kc + ((int64_t)n * p.kc_n + (int64_t)h * p.kc_h + (int64_t)slot * p.kc_w) * kKBytes;
       *(u16x8*)(dst + 16 * ai) = knew;
     } else {
-      bf16* dst = (bf16*)p.vc + (int64_t)n * p.vc_n + (int64_t)h * p.vc_h + (int64_t)slot * p.vc_w;
-      *(u16x8*)(dst + 8 * (ai - kKChunks)) = vnew;
+      VE* dst = (VE*)p.vc + (int64_t)n * p.vc_n + (int64_t)h * p.vc_h + (int64_t)slot * p.vc_w;
+      *(u16x8*)(dst + (16 / kVBytes) * (ai - kKChunks)) = vnew;
     }
-  } else if (ai == kKChunks + 8 && h == 0 && p.pos_out) {
+  } else if (ai == kKChunks + kVChunks && h == 0 && p.pos_out) {
     p.pos_out[n] = pos + 1;
   }
+}
+
+template <int NW, int NP, bool KF32 = false, bool SELF = false>
+__global__ __launch_bounds__(64 * NW) void decode_bf16_d64(DecodeFastArgs p) {
+  decode_d64_body<NW, NP, KF32 ? kDecodeKF32 : kDecodeBF16, SELF>(p);
+}
+
+// The fast path for the float32 (FLOW kDecodeF32) and float16 (kDecodeF16)
+// flows.
+template <int NW, int NP, int FLOW, bool SELF = false>
+__global__ __launch_bounds__(64 * NW) void decode_d64(DecodeFastArgs p) {
+  decode_d64_body<NW, NP, FLOW, SELF>(p);
 }
 
 // Exact path: any dtype, any D <= 256, any W; one thread per (n, h).  The
@@ -345,11 +413,40 @@ bool fast_args(const DecodeParams& p, DecodeFastArgs* a) {
 
 }  // namespace
 
-int launch_decode(bool fast, bool f64, const DecodeParams& p_in, hipStream_t st, hipError_t* err, bool kf32) {
+int launch_decode(int flow, bool f64, const DecodeParams& p_in, hipStream_t st, hipError_t* err) {
   DecodeFastArgs p;
+  bool fast = flow != DECODE_EXACT && !(flow == DECODE_F32 && p_in.W > 512);
   if (fast && !fast_args(p_in, &p)) fast = false;
-  if (!fast) kf32 = false;
-  if (fast && kf32) {
+  const bool kf32 = fast && flow == DECODE_KF32;
+  if (fast && (flow == DECODE_F32 || flow == DECODE_F16)) {
+    // float32 throughout (no self key; W <= 512: sixteen passes of float32
+    // K and V rows would not fit the registers), or float16 throughout
+    // (W <= 1024); D == 64
+    const dim3 grid((unsigned)(p_in.N * p_in.H));
+#define DECODE_WIDE(FL, SELF, TOP)                                                         \
+  do {                                                                                     \
+    if (p.W <= 32)                                                                         \
+      hipLaunchKernelGGL((decode_d64<4, 1, FL, SELF>), grid, dim3(256), 0, st, p);         \
+    else if (p.W <= 64)                                                                    \
+      hipLaunchKernelGGL((decode_d64<8, 1, FL, SELF>), grid, dim3(512), 0, st, p);         \
+    else if (p.W <= 128)                                                                   \
+      hipLaunchKernelGGL((decode_d64<8, 2, FL, SELF>), grid, dim3(512), 0, st, p);         \
+    else if (p.W <= 256)                                                                   \
+      hipLaunchKernelGGL((decode_d64<4, 8, FL, SELF>), grid, dim3(256), 0, st, p);         \
+    else if (p.W <= 512 || TOP == 8)                                                       \
+      hipLaunchKernelGGL((decode_d64<8, 8, FL, SELF>), grid, dim3(512), 0, st, p);         \
+    else                                                                                   \
+      hipLaunchKernelGGL((decode_d64<8, TOP, FL, SELF>), grid, dim3(512), 0, st, p);       \
+  } while (0)
+    if (flow == DECODE_F32) {
+      DECODE_WIDE(kDecodeF32, false, 8);
+    } else if (p.flags & TENSION_DECODE_SELF) {
+      DECODE_WIDE(kDecodeF16, true, 16);
+    } else {
+      DECODE_WIDE(kDecodeF16, false, 16);
+    }
+#undef DECODE_WIDE
+  } else if (fast && kf32) {
     // float32 q / K / out, bf16 V (D == 64, W <= 1024, no self key)
     const dim3 grid((unsigned)(p_in.N * p_in.H));
     if (p.W <= 32)

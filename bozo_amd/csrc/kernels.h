@@ -79,8 +79,12 @@ struct AuxLossParams {
 // grid would exceed 2^31 - 1 workgroups (band.h).
 int launch_exact(int phase, bool f64, const BandParams& p, hipStream_t st, hipError_t* err);
 int launch_mfma(int phase, const BandParams& p, hipStream_t st, hipError_t* err);
-// kf32 (with fast): float32 q / k_new / K cache / out and a bf16 V
-int launch_decode(bool fast, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err, bool kf32 = false);
+// decode step by flow: DECODE_EXACT (any dtype / head dim), or the fast
+// kernel (head dim 64, W <= 1024) for bf16 throughout (DECODE_BF16), float32
+// q / K / out with a bf16 V (DECODE_KF32), float32 throughout (DECODE_F32),
+// float16 throughout (DECODE_F16)
+enum { DECODE_EXACT = 0, DECODE_BF16 = 1, DECODE_KF32 = 2, DECODE_F32 = 3, DECODE_F16 = 4 };
+int launch_decode(int flow, bool f64, const DecodeParams& p, hipStream_t st, hipError_t* err);
 // split-operand kernels (split_band.h), by flow: SPLIT_FLOW_BF16 bf16
 // throughout, SPLIT_FLOW_F32 float32 Q / K / dOut with a bfloat16 V,
 // SPLIT_FLOW_F32V float32 Q / K / V / dOut, SPLIT_FLOW_F16 float16

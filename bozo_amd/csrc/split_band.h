@@ -49,14 +49,11 @@ namespace split {
 template <int NT>
 using Elem = typename std::conditional<NT == 1, bf16, typename std::conditional<NT == 2, f16, float>::type>::type;
 
-typedef f16 f16x8v __attribute__((ext_vector_type(8)));
-typedef f16 f16x4v __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ unsigned short f16_bits(f16 x) { return __builtin_bit_cast(unsigned short, x); }
 
 // 8 float16 values (as stored) as float32 (whole-vector bit cast)
 __device__ __forceinline__ void f16x8_to_f32(const u16x8& u, float* x) {
-  const f16x8v h = __builtin_bit_cast(f16x8v, u);
+  const f16x8 h = __builtin_bit_cast(f16x8, u);
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = (float)h[e];
 }
@@ -384,7 +381,7 @@ __device__ __forceinline__ void stage_get4(const E* st, int c, int j, int g, flo
     const f32x4 x = *(const f32x4*)at;
     v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
   } else if constexpr (std::is_same<E, f16>::value) {
-    const f16x4v x = __builtin_bit_cast(f16x4v, *(const u16x4*)at);
+    const f16x4 x = __builtin_bit_cast(f16x4, *(const u16x4*)at);
 #pragma unroll
     for (int r = 0; r < 4; ++r) v[r] = (float)x[r];
   } else {

@@ -32,7 +32,12 @@ def seq_inputs(N, L, H, D, seed, std=0.5):
     (torch.bfloat16, 64, 288, 7),     # fast path, 8 passes
     (torch.bfloat16, 64, 384, 390),   # fast path, 8 passes
     (torch.bfloat16, 64, 512, 515),   # fast path, largest window
-    (torch.float32, 64, 64, 70),      # exact path
+    (torch.float32, 64, 64, 70),      # fast path, float32 throughout
+    (torch.float32, 64, 512, 515),    # fast path, float32, largest window it takes
+    (torch.float32, 64, 600, 610),    # exact path (float32 beyond W = 512)
+    (torch.float32, 32, 64, 70),      # exact path (D != 64)
+    (torch.float16, 64, 64, 70),      # fast path, float16 throughout
+    (torch.float16, 64, 1024, 1030),  # fast path, float16, 16 passes
     (torch.bfloat16, 32, 16, 3),      # exact path (D != 64)
 ])
 def test_decode_matches_window_rows(dev, dtype, D, W, prefill):
@@ -51,6 +56,9 @@ def test_decode_matches_window_rows(dev, dtype, D, W, prefill):
         if dtype == torch.float32:
             assert max_abs(f64(out), ref[:, t]) <= 1e-5
             assert max_abs(f64(tt), tau[:, t]) <= 1e-5
+        elif dtype == torch.float16:
+            assert rel_l2(f64(out), ref[:, t]) <= 1e-3
+            assert max_abs(f64(tt), tau[:, t]) <= 2.0 ** -11
         else:
             assert rel_l2(f64(out), ref[:, t]) <= 2e-2
             assert max_abs(f64(tt), tau[:, t]) <= 4e-3

@@ -5,9 +5,10 @@ sequence and head counts, head dims 64 (the fast kernels) and 32 / 128 (the
 exact kernel), windows from one slot to 512, a cache that is empty, partly
 filled, exactly full or wrapped when the checked steps begin, every
 normalisation (tau mass, valid count, raw), with and without the tau output,
-and five dtype flows: bf16 (fast kernel), float32 and float64 (exact
-kernel), float16 (exact kernel, 16-bit rows), and float32 q / K with a bf16 V
-cache (the reference's autocast flow, float32-K fast kernel).  Each step must
+and five dtype flows: bf16, float32 and float16 (the fast kernel at head
+dim 64, float32 up to W = 512; the exact kernel otherwise), float64 (exact
+kernel), and float32 q / K with a bf16 V cache (the reference's autocast
+flow, float32-K fast kernel).  Each step must
 equal the last row of the local window over the same sequence (the decode
 contract; the oracle's window_forward / normalize_* are pinned by
 test_oracle.py), computed in float64 from the rounded inputs.  Eight more
