@@ -8,7 +8,8 @@ V included -- enters the bf16 MFMAs as three bf16 terms, and every output
 max-abs 1e-5 absolute, against the float64 oracle.  Shapes: the reference's
 117M layer (B8 H12 T1024 W64), its 350M preset's local layer (W256, 16
 heads), its default model (head dim 32, W32), and the
-global block.
+global block; and the float32 calls that stay on the exact kernels (other
+head dims, unaligned rows), at the same bound.
 """
 import ctypes
 import math
@@ -114,3 +115,34 @@ def test_float32_flow_global(dev, D, T):
         err = max_abs(f64(g), r)
         print(f"  {name}: max abs err {err:.3e}", flush=True)
         assert g.dtype == torch.float32 and err <= 1e-5, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("D,aligned", [(16, True), (128, True), (64, False)])
+def test_float32_exact_kernels(dev, D, aligned):
+    """float32 calls the split kernels do not take -- head dims other than
+    32 / 64, rows that are not 16-byte aligned (here Q, K, V are views one
+    element into a wider buffer) -- run on the exact kernels, at the same
+    fp32 bound."""
+    from bozo_amd import causal_tension, _lib as L
+    B, T, H, W = 2, 150, 3, 40
+    inp = make_inputs(B, T, H, D, seed=130 + D, std=0.5, W=W, dtau_std=0.1)
+    if aligned:
+        Q, K, V = (inp[n].to(dev).requires_grad_(True) for n in "QKV")
+        leaves = (Q, K, V)
+    else:
+        base = [torch.zeros(B, T, H, D + 1, device=dev) for _ in range(3)]
+        for b_, n in zip(base, "QKV"):
+            b_[..., 1:].copy_(inp[n].to(dev))
+        leaves = tuple(b_.requires_grad_(True) for b_ in base)
+        Q, K, V = (b_[..., 1:] for b_ in leaves)
+        assert Q.data_ptr() % 16 != 0
+    out, tau = causal_tension(Q, K, V, W, math.sqrt(D), return_tau=True, normalize="mass")
+    assert last_kernel() == L.KERNEL_EXACT
+    loss = (out * inp["dO"].to(dev)).sum() + (tau * inp["dTau"].to(dev)).sum()
+    grads = torch.autograd.grad(loss, leaves)
+    if not aligned:
+        grads = tuple(g[..., 1:] for g in grads)
+    torch.cuda.synchronize()
+    assert last_kernel() == L.KERNEL_EXACT
+    compare((out, tau, grads), oracle_run(inp, W, math.sqrt(D), normalize="mass", use_dtau=True), torch.float32,
+            True)
