@@ -523,8 +523,9 @@ def bench_window_variants(dev, steps, warmup):
 def profile_kernels(n, dev):
     """Counter-collection driver (run under rocprofv3 --pmc): n eager launches
     of each band kernel on rotated config-2 sets (bf16, then fp32 Q / K with
-    bf16 V), of the split kernels at the 350M preset's W = 256 shape (bf16
-    and fp32 Q / K), n config-4 decode steps
+    bf16 V, then fp32 throughout and fp16 throughout), of the split kernels
+    at the 350M preset's W = 256 shape (bf16 and fp32 Q / K), n config-4
+    decode steps
     over 4 rotated caches and n config-3 global forward + backward calls, then
     a plain device copy of
     known size (256 MiB read + 256 MiB written) whose FETCH_SIZE/WRITE_SIZE
@@ -549,6 +550,19 @@ def profile_kernels(n, dev):
             fns[i % 2][0][name]()
         torch.cuda.synchronize()
     del fns, mixed
+    # config 2 in the float32 flow (fp32 Q / K / V, V as three terms too) and
+    # in fp16 (two terms per value), valid-count normalised (one-pass dQ)
+    base = make_window_sets(2, B, T, H, D, dev, seed=5)
+    flows = [{k: s[k].detach().float() for k in ("Q", "K", "V", "dO")} for s in base]
+    flows += [{k: s[k].detach().half() for k in ("Q", "K", "V", "dO")} for s in base]
+    del base
+    fns = [kernel_fns(s, W, math.sqrt(D), L.NORM_COUNT) for s in flows]
+    for name in ("fwd", "dq", "dkv"):
+        for i in range(n):
+            fns[i % 2][0][name]()       # float32 throughout
+            fns[2 + i % 2][0][name]()   # float16 throughout
+        torch.cuda.synchronize()
+    del fns, flows
     # the 350M preset's local layer (B4 H16 T1024 W256) on the split kernels,
     # bf16 and in the autocast flow, valid-count normalised (its CE-only step;
     # distinct kernel instances from the tau-mass config-2 ones above)
