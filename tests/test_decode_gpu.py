@@ -122,6 +122,7 @@ def test_decode_fp32_qk_bf16_v(dev, W, prefill, normalize):
     (torch.bfloat16, 300, 150),    # fast path, 8 passes
     (torch.bfloat16, 64, 3),       # fast path, one pass
     (torch.float32, 40, 20),       # exact path
+    (torch.float16, 1024, 700),    # fast path, float16, 16 passes
 ])
 def test_decode_self_matches_global_rows(dev, dtype, W, prefill):
     """include_self over a cache that holds every earlier token is the global
