@@ -66,11 +66,12 @@ def test_float16_flow_bias(dev, W, T):
     check(hip, oracle_run(inp, W, 8.0, normalize="mass", use_bias=True, use_dtau=True), True)
 
 
-@pytest.mark.parametrize("D,T", [(64, 130), (32, 97)])
-def test_float16_flow_global(dev, D, T):
-    """The global block with a bias [B, T, T], tau_local and its gradient."""
+@pytest.mark.parametrize("D,T,Wl", [(64, 130, 16), (32, 97, 16), (64, 200, 130)])
+def test_float16_flow_global(dev, D, T, Wl):
+    """The global block with a bias [B, T, T], tau_local (over one key
+    block, or three) and its gradient."""
     from bozo_amd import _lib as L
-    B, H, Wl = 2, 3, 16
+    B, H = 2, 3
     inp = make_inputs(B, T, H, D, seed=127 + D + T, std=0.5, dtype=torch.float16, W=Wl, dtau_std=0.1,
                       bias_std=0.5, bias_shape=(B, T, T))
     scale = math.sqrt(D)

@@ -97,13 +97,13 @@ def test_float32_flow_saved_rows_match_recompute(dev, W, D, tau):
             check_fp32(got, want, name)
 
 
-@pytest.mark.parametrize("D,T", [(64, 130), (32, 97), (64, 256)])
-def test_float32_flow_global(dev, D, T):
+@pytest.mark.parametrize("D,T,Wl", [(64, 130, 16), (32, 97, 16), (64, 256, 16), (64, 256, 100)])
+def test_float32_flow_global(dev, D, T, Wl):
     """The global block (model.py:217-238) with float32 Q / K / V, a bias
-    [B, T, T], tau_local and its gradient: out, dQ, dK, dV and tau_local at
-    the fp32 bound."""
+    [B, T, T], tau_local (over one key block, or two) and its gradient: out,
+    dQ, dK, dV and tau_local at the fp32 bound."""
     from bozo_amd import _lib as L
-    B, H, Wl = 2, 3, 16
+    B, H = 2, 3
     inp = make_inputs(B, T, H, D, seed=99 + D + T, std=0.5, W=Wl, dtau_std=0.1, bias_std=0.5, bias_shape=(B, T, T))
     scale = math.sqrt(D)
     hip = global_hip_run(inp, scale, dev, W_local=Wl, use_bias=True, use_dtl=True)
