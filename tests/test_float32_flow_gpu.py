@@ -146,3 +146,33 @@ def test_float32_exact_kernels(dev, D, aligned):
     assert last_kernel() == L.KERNEL_EXACT
     compare((out, tau, grads), oracle_run(inp, W, math.sqrt(D), normalize="mass", use_dtau=True), torch.float32,
             True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_strided_kv_views(dev, dtype):
+    """model.py:206-207 splits one fused wkv projection: K and V are views of
+    one [B, T, H, 2 D] tensor (row stride 2 D).  The split kernels read them
+    in place in the float32 and float16 flows too; forward and backward
+    against the float64 oracle (float32 at its 1e-5 bound, float16 at 1e-3
+    relative L2)."""
+    from bozo_amd import causal_tension, _lib as L
+    from tests._util import rel_l2
+    B, T, H, D, W = 2, 200, 3, 64, 64
+    inp = make_inputs(B, T, H, D, seed=140, std=0.5, dtype=dtype, W=W)
+    kv = torch.cat([inp["K"], inp["V"]], dim=-1).to(dev).requires_grad_(True)
+    q = inp["Q"].to(dev).requires_grad_(True)
+    k, v = kv[..., :D], kv[..., D:]
+    assert k.stride(2) == 2 * D
+    out = causal_tension(q, k, v, W, 8.0, normalize="mass")
+    assert last_kernel() == (L.KERNEL_SPLIT_F32V if dtype == torch.float32 else L.KERNEL_SPLIT_F16)
+    dq, dkv = torch.autograd.grad((out.float() * inp["dO"].to(dev).float()).sum(), (q, kv))
+    ref = oracle_run(inp, W, 8.0, normalize="mass")
+    got = (out, dq, dkv[..., :D], dkv[..., D:])
+    want = (ref[0],) + tuple(ref[2])
+    for name, g, r in zip(("out", "dQ", "dK", "dV"), got, want):
+        if dtype == torch.float32:
+            check_fp32(g, r, name)
+        else:
+            err = rel_l2(f64(g), r)
+            print(f"  {name}: rel L2 err {err:.3e}", flush=True)
+            assert err <= 1e-3, (name, err)
