@@ -3,7 +3,8 @@ coefficients in the library's fixed device scratch instead of a caller
 workspace.  Through the C ABI, two calls in a row (the second with a smaller
 input, so stale scratch contents from the first would show) must give the
 same dQ, dK, dV bits as tension_global_bwd with a caller workspace, on the
-bf16 MFMA kernels and on the float32 exact kernels.  The refusal of
+bf16 MFMA kernels, on the split kernels (float32 and float16 flows) and on
+the exact kernels.  The refusal of
 requests beyond the scratch happens before any HIP call and is checked on
 the CPU (tests/test_abi.py)."""
 import ctypes
@@ -52,7 +53,9 @@ def _backward(lib, noalloc, q, k, v, do, dtl, bias, out, mass, Wl, scale, st):
 
 @pytest.mark.parametrize("dtype,D,shapes", [
     (torch.bfloat16, 64, [(2, 700, 12), (1, 300, 4)]),   # MFMA kernels
-    (torch.float32, 32, [(2, 130, 3), (1, 70, 2)]),      # exact kernels
+    (torch.float32, 32, [(2, 130, 3), (1, 70, 2)]),      # split kernels, float32 flow
+    (torch.float16, 64, [(2, 300, 3), (1, 100, 2)]),     # split kernels, float16
+    (torch.float32, 16, [(2, 130, 3), (1, 70, 2)]),      # exact kernels
 ])
 def test_noalloc_matches_workspace_entry_point(dev, dtype, D, shapes):
     lib = L.lib()
